@@ -1,0 +1,272 @@
+"""Benchmark of the fused TurboAdam step on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c3]
+
+A step is one TurboAdam.step() over the whole synthetic parameter set with
+its gradients already resident in HBM.  Default workload (the headline of
+BASELINE.json): the Llama-3-8B-shaped parameter set (291 tensors,
+8,030,261,248 parameters) in bf16, m+v compression, v_bits=4.  Prints one
+JSON line with throughput (parameters updated per second), the roofline of
+the dominant kernel (pass 1) timed live with HIP events on the launch stream,
+and a CPU baseline: the CPU oracle (a scalar restatement of the reference's
+CPU step) timed on a bounded sample on this host.
+"""
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "params updated/sec per step + % HBM roofline, 8B-shaped m+v 4-bit"
+HBM_PEAK_GBPS = 8000.0
+
+
+# ---------------------------------------------------------------- workloads
+def llama3_8b_shapes():
+    h, kv, inter, vocab, layers = 4096, 1024, 14336, 128256, 32
+    shapes = [("embed", (vocab, h))]
+    for i in range(layers):
+        shapes += [
+            (f"l{i}.q", (h, h)), (f"l{i}.k", (kv, h)), (f"l{i}.v", (kv, h)), (f"l{i}.o", (h, h)),
+            (f"l{i}.gate", (inter, h)), (f"l{i}.up", (inter, h)), (f"l{i}.down", (h, inter)),
+            (f"l{i}.norm1", (h,)), (f"l{i}.norm2", (h,)),
+        ]
+    shapes += [("norm", (h,)), ("lm_head", (vocab, h))]
+    return shapes
+
+
+def gpt2_block_shapes(prefix=""):
+    return [(prefix + "ln_1.w", (768,)), (prefix + "ln_1.b", (768,)), (prefix + "attn.c_attn.w", (768, 2304)),
+            (prefix + "attn.c_attn.b", (2304,)), (prefix + "attn.c_proj.w", (768, 768)),
+            (prefix + "attn.c_proj.b", (768,)), (prefix + "ln_2.w", (768,)), (prefix + "ln_2.b", (768,)),
+            (prefix + "mlp.c_fc.w", (768, 3072)), (prefix + "mlp.c_fc.b", (3072,)),
+            (prefix + "mlp.c_proj.w", (3072, 768)), (prefix + "mlp.c_proj.b", (768,))]
+
+
+def gpt2_124m_shapes():
+    s = [("wte", (50257, 768)), ("wpe", (1024, 768))]
+    for i in range(12):
+        s += gpt2_block_shapes(f"h{i}.")
+    s += [("ln_f.w", (768,)), ("ln_f.b", (768,))]
+    return s
+
+
+def ragged_shapes(seed=0, count=1000):
+    rng = np.random.default_rng(seed)
+    sizes = np.maximum(1, np.round(2.0 ** (20 * rng.random(count)))).astype(np.int64)
+    return [(f"t{i}", (int(n),)) for i, n in enumerate(sizes)]
+
+
+WORKLOADS = {
+    # name: (shapes fn, dtype, optimizer kwargs, log-sigma center, description)
+    "c3": (llama3_8b_shapes, torch.bfloat16, dict(lr=3e-4, weight_decay=0.1, v_bits=4), math.log(1e-4),
+           "llama3-8b-shaped bf16 m+v v_bits=4"),
+    "c1": (lambda: [("p", (1 << 28,))], torch.float32, dict(lr=1e-3, compress_m=False, v_bits=4), math.log(1e-3),
+           "v-only 2^28 fp32 v_bits=4"),
+    "c2": (gpt2_124m_shapes, torch.float32, dict(lr=6e-4, weight_decay=0.01, v_bits=4), math.log(1e-3),
+           "gpt2-124m fp32 m+v v_bits=4"),
+    "c0": (gpt2_block_shapes, torch.float32, dict(lr=6e-4, weight_decay=0.01, v_bits=4), math.log(1e-3),
+           "gpt2-block fp32 m+v v_bits=4"),
+    "c4": (ragged_shapes, torch.float32, dict(lr=1e-3, v_bits=4), math.log(1e-3),
+           "ragged 1000 tensors fp32 m+v v_bits=4"),
+}
+
+
+def bytes_per_param(dtype_bytes: int, costate: bool, compress_v: bool = True):
+    """Algorithmic HBM bytes per parameter per step (whole step and pass 1 alone).
+
+    pass 1 reads p, g, the 1Q indices and scales and (CoState) the previous
+    signs/labels/norms/amplitudes and writes p, indices and scales; an fp32-m
+    tensor reads and writes exp_avg instead.  CoState adds pass 2 (g, the
+    previous encoding, new encoding, ratios) and the selection (ratios, labels).
+    """
+    P = G = dtype_bytes
+    v = (2.0 + 8.0 / 128) if compress_v else 8.0
+    if costate:
+        k1 = 2 * P + G + v + (1.0 / 8 + 7.0 / 128)
+        total = 2 * P + 2 * G + 2.0 + 3.0 / 8 + 37.0 / 128
+    else:
+        k1 = 2 * P + G + v + 8.0
+        total = k1
+    return k1, total
+
+
+# ---------------------------------------------------------------- CPU baseline
+def cpu_baseline(shapes, dtype, kw, log_sigma, budget_s=12.0):
+    """Time the CPU oracle on a bounded sample of the workload's tensors."""
+    from oracle import oracle as O
+
+    dt = {torch.float32: O.DT_F32, torch.bfloat16: O.DT_BF16, torch.float16: O.DT_F16}[dtype]
+    rng = np.random.default_rng(7)
+    # sample: tensors in workload order until ~24M parameters
+    sample, total = [], 0
+    for name, shp in shapes:
+        n = int(np.prod(shp))
+        if n > 20_000_000 and sample:
+            continue
+        sample.append((name, n))
+        total += n
+        if total >= 20_000_000:
+            break
+
+    def enc(x):
+        x = x.astype(np.float32)
+        if dt == O.DT_F32:
+            return x
+        return torch.from_numpy(x).to(dtype).view(torch.int16).numpy().view(np.uint16).copy()
+
+    params = [enc(rng.standard_normal(n) * 0.02) for _, n in sample]
+    opt = O.OracleTurboAdam(params, dtypes=[dt] * len(params), seed=1, **kw)
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < 2:
+        grads = [enc(rng.standard_normal(n) * math.exp(log_sigma)) for _, n in sample]
+        t0 = time.perf_counter()
+        opt.step(grads)
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 5:
+            break
+    steady = times[1:] if len(times) > 1 else times
+    t = float(np.median(steady))
+    return {"value": total / t, "unit": "params/s", "cores": 1, "kind": "port",
+            "sample": f"{len(sample)} tensors ({total} params: {', '.join(n for n, _ in sample[:4])}...) of the "
+                      f"same workload, {len(times)} steps, median of steps 2+; scalar C oracle, 1 thread"}
+
+
+# ---------------------------------------------------------------- main
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="c3", choices=sorted(WORKLOADS))
+    ap.add_argument("--grad-sets", type=int, default=2)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build measures one GPU only (the optimizer step is single-device); "
+              "run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    from turboadam_amd import TurboAdam, _lib
+
+    _lib.load()
+    shapes_fn, dtype, kw, log_sigma, desc = WORKLOADS[args.workload]
+    shapes = shapes_fn()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+
+    params, grad_sets = [], [[] for _ in range(args.grad_sets)]
+    sig_rng = np.random.default_rng(1)
+    for name, shp in shapes:
+        p = torch.empty(shp, dtype=dtype, device=dev)
+        if "norm" in name or name.startswith("ln") or ".ln_" in name:
+            p.fill_(1.0)
+        else:
+            p.normal_(0.0, 0.02, generator=gen)
+        params.append(torch.nn.Parameter(p))
+        sigma = math.exp(log_sigma + sig_rng.standard_normal())
+        drift = torch.randn(shp, device=dev, generator=gen, dtype=torch.float32)
+        for k in range(args.grad_sets):
+            z = torch.randn(shp, device=dev, generator=gen, dtype=torch.float32)
+            grad_sets[k].append((sigma * (z + 0.3 * drift)).to(dtype))
+        del drift, z
+    nparams = sum(p.numel() for p in params)
+    opt = TurboAdam(params, **kw)
+
+    def set_grads(k):
+        for p, g in zip(params, grad_sets[k % args.grad_sets]):
+            p.grad = g
+
+    for s in range(args.warmup):
+        set_grads(s)
+        opt.step()
+    torch.cuda.synchronize()
+
+    # timed region: K steps; pass 1 bracketed by events on the launch stream
+    ev = []
+
+    def hook(k, when):
+        if k == 0:
+            e = torch.cuda.Event(enable_timing=True)
+            e.record(torch.cuda.current_stream(dev))
+            ev.append(e)
+
+    opt._pass_hook = hook
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for s in range(args.steps):
+        set_grads(args.warmup + s)
+        opt.step()
+    stop.record()
+    torch.cuda.synchronize()
+    opt._pass_hook = None
+    total_ms = start.elapsed_time(stop)
+    ms_step = total_ms / args.steps
+    k1_ms = [ev[2 * i].elapsed_time(ev[2 * i + 1]) for i in range(len(ev) // 2)]
+    k1_avg = float(np.mean(k1_ms))
+
+    dbytes = torch.tensor([], dtype=dtype).element_size()
+    k1_bytes = 0.0
+    step_bytes = 0.0
+    for p in params:
+        st = opt.state[p]
+        k1, tot = bytes_per_param(dbytes, st["_compress_m"], "compressed_v" in st)
+        k1_bytes += k1 * p.numel()
+        step_bytes += tot * p.numel()
+    k1_gbps = k1_bytes / (k1_avg * 1e-3) / 1e9
+    step_gbps = step_bytes / (ms_step * 1e-3) / 1e9
+
+    out = {
+        "metric": METRIC,
+        "value": nparams / (ms_step * 1e-3),
+        "unit": "params/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": desc,
+            "params": nparams,
+            "tensors": len(params),
+            "param_dtype": str(dtype).replace("torch.", ""),
+            "grad_dtype": str(dtype).replace("torch.", ""),
+            "optimizer": {k: v for k, v in kw.items()},
+            "step_bytes_alg": step_bytes,
+            "step_hbm_frac": step_gbps / HBM_PEAK_GBPS,
+        },
+        "roofline": {
+            "kernel": "tam_k1_main (pass 1)",
+            "bound": "hbm",
+            "achieved": k1_gbps,
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": k1_gbps / HBM_PEAK_GBPS,
+            "traffic": None,
+            "ms_per_launch": k1_avg,
+            "bytes_alg_per_launch": k1_bytes,
+        },
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(shapes, dtype, kw, log_sigma)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,160 @@
+/* turboadam_amd.h -- C ABI of the MI355X (gfx950) TurboAdam packed-state step.
+ *
+ * Plain pointers and sizes only.  Every device pointer is HIP device memory
+ * owned by the caller; the library allocates no device memory in any entry
+ * point below.  Work is enqueued on the caller's HIP stream (`stream` is a
+ * hipStream_t passed as void*; NULL = the legacy default stream) and returns
+ * without synchronising.  Return value: 0 on success, otherwise a TAM_E_*
+ * code; tam_last_error() gives a message for the calling thread.
+ *
+ * Arithmetic contract: results equal, bit for bit, the reference CPU path
+ * (davidkny22/turboadam, src/turboadam/{optimizer,costate,quantize}.py) with
+ * its library-defined operations fixed as follows: exp/log correctly rounded;
+ * dot products and block L2 norms accumulated in fp64 over a balanced pairwise
+ * tree (128-element blocks, then blocks zero-padded to a power of two) and
+ * rounded to fp32 once; sqrt correctly rounded.  Stochastic-rounding draws come
+ * from Philox4x32-10 (counter = (element/4, tensor_id, step, element/2^34),
+ * key = seed), word element%4, uniform = (word >> 8) * 2^-24.
+ */
+#ifndef TURBOADAM_AMD_H
+#define TURBOADAM_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TAM_ABI_VERSION 1
+#define TAM_BLOCK_SIZE 128 /* elements per quantisation / CoState block */
+
+/* error codes */
+#define TAM_OK 0
+#define TAM_E_INVALID 1  /* bad argument: dtype, size, flag, null pointer */
+#define TAM_E_WORKSPACE 2 /* workspace too small */
+#define TAM_E_HIP 3      /* a HIP runtime call failed */
+#define TAM_E_UNSUPPORTED 4
+
+/* TamTensor.dtype */
+#define TAM_DTYPE_F32 0
+#define TAM_DTYPE_BF16 1
+#define TAM_DTYPE_F16 2
+
+/* TamTensor.flags */
+#define TAM_FLAG_COSTATE 0x1u    /* m kept as CoState (else fp32 exp_avg)       */
+#define TAM_FLAG_COMPRESS_V 0x2u /* v kept as 1Q indices (else fp32 exp_avg_sq) */
+#define TAM_FLAG_HAS_STATE 0x4u  /* CoState holds a previous encoding          */
+#define TAM_FLAG_WD 0x8u         /* apply decoupled weight decay p *= c_wd     */
+
+/* One parameter tensor of one optimizer step.  The caller fills the fields
+ * marked [in]; tam_prepare() fills the fields marked [derived].  The array is
+ * then copied to device memory and handed to tam_multi_tensor_step().
+ *
+ * Replaces the per-parameter body of TurboAdam._full_step_kernel
+ * (reference src/turboadam/optimizer.py:97-170) and the state it touches
+ * (optimizer.py:242-286, costate.py:357-365, oneq.py:41-48). */
+typedef struct TamTensor {
+  void* param;          /* [in] n elements of dtype, updated in place        */
+  const void* grad;     /* [in] n elements of dtype                          */
+  uint8_t* v_idx;       /* [in] COMPRESS_V: u8[nb*128] 1Q indices (in/out)   */
+  uint16_t* v_scales;   /* [in] COMPRESS_V: f16[nb*2] (log_min, log_max)     */
+  float* exp_avg_sq;    /* [in] !COMPRESS_V: f32[n] second moment            */
+  float* exp_avg;       /* [in] !COSTATE: f32[n] first moment                */
+  uint8_t* signs;       /* [in] COSTATE: u8[ceil(n/8)] sign bits, MSB first  */
+  uint8_t* labels;      /* [in] COSTATE: u8[nb] 0 null, 1 phase, 2 amplitude */
+  float* norms;         /* [in] COSTATE: f32[nb] residual block L2 norms     */
+  uint16_t* amp;        /* [in] COSTATE: f16[nb] amplitude scales            */
+  float* alpha;         /* [in] COSTATE: f32[1] projection alpha (in/out)    */
+  uint64_t n;           /* [in] number of elements (>= 1)                    */
+  uint32_t dtype;       /* [in] TAM_DTYPE_* of param and grad                */
+  uint32_t flags;       /* [in] TAM_FLAG_*                                   */
+  uint32_t v_bits;      /* [in] 2, 3, 4, 6 or 8                              */
+  uint32_t tensor_id;   /* [in] Philox counter word 1                        */
+  uint32_t step;        /* [in] 1-based step number (Philox counter word 2)  */
+  uint32_t k_lo, k_hi;  /* [in] COSTATE: ranks of the P_null / P_amp ratios  */
+  uint32_t pad1;
+  float c_wd;           /* [in] f32(1 - lr*wd)                               */
+  float beta1, one_minus_beta1, beta2, one_minus_beta2; /* [in] f32 of the doubles */
+  float bias_correction1, bias_correction2;             /* [in] f32(1-beta^step)   */
+  float eps, neg_lr;    /* [in] f32(eps), f32(-lr)                           */
+  float sqrt_block;     /* [in] f32(sqrt(128))                               */
+  uint32_t nb;          /* [derived] ceil(n/128)                             */
+  uint32_t tile0;       /* [derived] first tile (16 blocks) of this tensor   */
+  uint32_t ntiles;      /* [derived] ceil(nb/16)                             */
+  uint32_t pad0;
+  uint64_t ratio_off;   /* [derived] COSTATE: offset of its ratios (blocks)  */
+} TamTensor;
+
+/* Launch summary and workspace layout, filled by tam_prepare(). */
+typedef struct TamStepInfo {
+  int32_t n_tensors;
+  uint32_t total_tiles;
+  uint32_t n_costate;
+  uint32_t pad0;
+  uint64_t ratio_blocks;   /* sum of nb over CoState tensors */
+  uint64_t off_partials;   /* workspace byte offsets */
+  uint64_t off_alpha;
+  uint64_t off_ratios;
+  uint64_t ws_bytes;       /* required workspace size */
+} TamStepInfo;
+
+/* Version of this ABI (TAM_ABI_VERSION). */
+int tam_abi_version(void);
+
+/* sizeof(TamTensor) for which == 0, sizeof(TamStepInfo) for which == 1, so a
+ * binding can check its struct mirror. */
+size_t tam_struct_size(int which);
+
+/* Message for the last failing call on this thread ("" if none). */
+const char* tam_last_error(void);
+
+/* Host only (no HIP call): validate `tensors`, fill the [derived] fields and
+ * the launch summary.  Replaces the lazy-init bookkeeping of TurboAdam.step
+ * (reference optimizer.py:232-286) for one step's tensor list. */
+int tam_prepare(TamTensor* tensors, int n_tensors, TamStepInfo* info);
+
+/* One fused optimizer step over every tensor of `d_tensors` (device copy of
+ * the array prepared by tam_prepare) in four launches: pass 1 (decode, EMA,
+ * 1Q re-quantisation, AdamW update, dot partials), alpha, pass 2 (CoState
+ * encode, block ratios), selection + classification.
+ * Replaces TurboAdam._full_step_kernel (reference optimizer.py:88-170) with
+ * CoStateManager.update (costate.py:367-464) and fused_v_update
+ * (quantize.py:222-299 / triton_kernels.py:105-165) inlined.  `workspace`
+ * must hold info->ws_bytes bytes of device memory (contents need not be kept
+ * between calls).  `h_tensors` is the host array tam_prepare() filled; it is
+ * read for launch sizes only. */
+int tam_multi_tensor_step(const TamTensor* d_tensors, const TamTensor* h_tensors,
+                          const TamStepInfo* info, uint64_t seed, void* workspace,
+                          size_t ws_bytes, void* stream);
+
+/* One of the four launches of tam_multi_tensor_step (same arguments):
+ * pass 0 = fused pass 1, 1 = alpha, 2 = CoState encode, 3 = selection and
+ * labels.  Issuing passes 0..3 in order on one stream equals one
+ * tam_multi_tensor_step call; callers use it to time the launches one by one.
+ * No counterpart in the reference (its step is not split into passes). */
+int tam_step_pass(int pass, const TamTensor* d_tensors, const TamStepInfo* info, uint64_t seed,
+                  void* workspace, size_t ws_bytes, void* stream);
+
+/* Decode 1Q indices to fp32 v: out[i] = exp(lmin + ((idx+0.5)/2^bits)*span)
+ * for i < n.  Replaces dequantize_logscale_nbits (reference quantize.py:183-214)
+ * as used by decompress_v (oneq.py:51-67). */
+int tam_v_dequantize(const uint8_t* v_idx, const uint16_t* v_scales, uint64_t n,
+                     uint32_t v_bits, float* out, void* stream);
+
+/* Stochastic-rounding uniforms of elements [0, count) of tensor `tensor_id`
+ * at `step` (the draws the step consumes).  Replaces the rand_buf refill
+ * (reference optimizer.py:131) / torch.rand_like (quantize.py:291). */
+int tam_philox_uniforms(uint32_t tensor_id, uint32_t step, uint64_t seed,
+                        uint64_t count, float* out, void* stream);
+
+/* Self-check of the device arithmetic: out[i] = f(in[i]) with f selected by
+ * `fn` (0 log, 1 exp, 2 f32->f16->f32, 3 f32->bf16->f32).  No counterpart in
+ * the reference: it lets a caller confirm the device math equals the host. */
+int tam_math_eval(int fn, const float* in, float* out, uint64_t n, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TURBOADAM_AMD_H */

@@ -1,0 +1,424 @@
+/* tam_oracle.c -- TEST INFRASTRUCTURE ONLY.  Never linked into, loaded by or
+ * called from the turboadam_amd product path; only tests/, the smoke check
+ * and bench.py's cpu_baseline leg use it, as the checker.
+ *
+ * A scalar CPU restatement of the reference TurboAdam step
+ * (davidkny22/turboadam, src/turboadam), one parameter tensor at a time, in
+ * "exact mode": the reference's library-defined operations are fixed to
+ *   - exp / log: correctly rounded fp32 (evaluated as (float)expl / (float)logl,
+ *     64-bit-significand x87 arithmetic),
+ *   - dot products and block L2 norms: fp64 accumulation over a balanced
+ *     pairwise tree (per 128-element block, then over the blocks zero-padded
+ *     to a power of two), rounded to fp32 once,
+ *   - sqrt: correctly rounded,
+ * and every other operation is the fp32 operation torch performs, in the
+ * reference's order (fma exactly where torch fuses: Tensor.add_(alpha=) and
+ * addcmul_).  Stochastic-rounding uniforms: Philox4x32-10 (its own
+ * implementation here), counter (e/4, tensor_id, step, e>>34), key seed,
+ * word e%4, u = (word >> 8) * 2^-24.  Compiled with -ffp-contract=off.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define OR_BS 128
+
+/* ---------------------------------------------------------------- bits */
+static inline uint32_t f2u(float x) { uint32_t u; memcpy(&u, &x, 4); return u; }
+static inline float u2f(uint32_t u) { float x; memcpy(&x, &u, 4); return x; }
+
+/* ---------------------------------------------------------------- philox */
+/* Philox4x32-10 (Salmon, Moraes, Dror, Shaw, SC'11). */
+void or_philox4x32_10(const uint32_t ctr[4], uint32_t k0, uint32_t k1, uint32_t out[4]) {
+  uint32_t c0 = ctr[0], c1 = ctr[1], c2 = ctr[2], c3 = ctr[3];
+  for (int r = 0; r < 10; ++r) {
+    uint64_t a = (uint64_t)0xD2511F53u * c0;
+    uint64_t b = (uint64_t)0xCD9E8D57u * c2;
+    uint32_t n0 = (uint32_t)(b >> 32) ^ c1 ^ k0;
+    uint32_t n1 = (uint32_t)b;
+    uint32_t n2 = (uint32_t)(a >> 32) ^ c3 ^ k1;
+    uint32_t n3 = (uint32_t)a;
+    c0 = n0; c1 = n1; c2 = n2; c3 = n3;
+    k0 += 0x9E3779B9u;
+    k1 += 0xBB67AE85u;
+  }
+  out[0] = c0; out[1] = c1; out[2] = c2; out[3] = c3;
+}
+
+static float or_uniform(uint64_t e, uint32_t tid, uint32_t step, uint64_t seed) {
+  uint64_t q = e >> 2;
+  uint32_t ctr[4] = {(uint32_t)q, tid, step, (uint32_t)(q >> 32)};
+  uint32_t w[4];
+  or_philox4x32_10(ctr, (uint32_t)seed, (uint32_t)(seed >> 32), w);
+  return (float)(w[e & 3] >> 8) * (1.0f / 16777216.0f);
+}
+
+void or_philox_uniforms(uint32_t tid, uint32_t step, uint64_t seed, uint64_t count, float* out) {
+  for (uint64_t e = 0; e < count; ++e) out[e] = or_uniform(e, tid, step, seed);
+}
+
+/* ------------------------------------------------------ fp16 / bf16 RNE */
+uint16_t or_f32_to_f16(float x) {
+  uint32_t u = f2u(x);
+  uint32_t sign = (u >> 16) & 0x8000u;
+  uint32_t a = u & 0x7fffffffu;
+  if (a >= 0x7f800000u) { /* inf / nan */
+    if (a > 0x7f800000u) return (uint16_t)(sign | 0x7e00u | ((a >> 13) & 0x3ffu));
+    return (uint16_t)(sign | 0x7c00u);
+  }
+  int e = (int)(a >> 23) - 127;
+  uint32_t mant = (a & 0x7fffffu) | 0x800000u; /* 24-bit significand (normal) */
+  if (a < 0x00800000u) return (uint16_t)sign;  /* fp32 subnormal -> +-0 in fp16 */
+  if (e > 15) return (uint16_t)(sign | 0x7c00u);
+  int shift;                                   /* bits to drop from the 24-bit significand */
+  uint32_t hexp;
+  if (e >= -14) { shift = 13; hexp = (uint32_t)(e + 15); }
+  else { shift = 13 + (-14 - e); hexp = 0; }
+  if (shift > 24) return (uint16_t)sign;       /* below half of the smallest subnormal */
+  uint32_t q = mant >> shift;
+  uint32_t rem = mant & ((1u << shift) - 1u);
+  uint32_t half = 1u << (shift - 1);
+  if (rem > half || (rem == half && (q & 1u))) q += 1;
+  uint32_t h;
+  if (hexp == 0) h = q;                        /* subnormal (q may carry into the normal range) */
+  else h = (hexp << 10) + (q - 0x400u);        /* q in [0x400, 0x800]; carry bumps the exponent */
+  if (h >= 0x7c00u) h = 0x7c00u;
+  return (uint16_t)(sign | h);
+}
+
+float or_f16_to_f32(uint16_t h) {
+  uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
+  uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+  if (e == 0x1f) return u2f(sign | 0x7f800000u | (m << 13));
+  if (e == 0) { float v = (float)m * (1.0f / 16777216.0f); return sign ? -v : v; } /* m * 2^-24 */
+  return u2f(sign | ((e + 112u) << 23) | (m << 13));
+}
+
+uint16_t or_f32_to_bf16(float x) {
+  if (x != x) return 0x7fc0u;
+  uint32_t u = f2u(x);
+  uint32_t lsb = (u >> 16) & 1u;
+  return (uint16_t)((u + 0x7fffu + lsb) >> 16);
+}
+float or_bf16_to_f32(uint16_t b) { return u2f((uint32_t)b << 16); }
+
+/* ------------------------------------------------------ exact transcendentals */
+float or_logf(float x) {
+  if (x != x) return x;
+  if (x < 0.0f) return u2f(0x7fc00000u);
+  if (x == 0.0f) return -INFINITY;
+  if (isinf(x)) return x;
+  return (float)logl((long double)x);
+}
+float or_expf(float x) {
+  if (x != x) return x;
+  if (x > 100.0f) return INFINITY;
+  if (x < -110.0f) return 0.0f;
+  return (float)expl((long double)x);
+}
+
+/* ------------------------------------------------------ pairwise fp64 sums */
+static double pairwise(const double* x, uint64_t n) { /* n is a power of two */
+  if (n == 1) return x[0];
+  return pairwise(x, n / 2) + pairwise(x + n / 2, n / 2);
+}
+
+/* Balanced pairwise sum of x[0..n) zero-padded to the next power of two. */
+double or_pairwise_sum(const double* x, uint64_t n) {
+  uint64_t P = 1;
+  while (P < n) P <<= 1;
+  double* buf = (double*)calloc(P, sizeof(double));
+  memcpy(buf, x, n * sizeof(double));
+  double s = pairwise(buf, P);
+  free(buf);
+  return s;
+}
+
+/* ------------------------------------------------------ element access */
+static float ld(const void* p, int dtype, uint64_t i) {
+  if (dtype == 0) return ((const float*)p)[i];
+  uint16_t h = ((const uint16_t*)p)[i];
+  return dtype == 1 ? or_bf16_to_f32(h) : or_f16_to_f32(h);
+}
+static float round_p(float x, int dtype) {
+  if (dtype == 0) return x;
+  if (dtype == 1) return or_bf16_to_f32(or_f32_to_bf16(x));
+  return or_f16_to_f32(or_f32_to_f16(x));
+}
+static void st(void* p, int dtype, uint64_t i, float v) {
+  if (dtype == 0) ((float*)p)[i] = v;
+  else if (dtype == 1) ((uint16_t*)p)[i] = or_f32_to_bf16(v);
+  else ((uint16_t*)p)[i] = or_f32_to_f16(v);
+}
+
+/* ------------------------------------------------------ CoState pieces */
+/* decode_blocks, reference costate.py:261-324 (m_hat = alpha*g + scale*sign). */
+void or_decode_blocks(const uint8_t* labels, const uint8_t* signs, const float* norms, const uint16_t* amp,
+                      float alpha, const float* g, uint64_t n, float q, float* m_hat) {
+  for (uint64_t i = 0; i < n; ++i) {
+    uint64_t b = i / OR_BS;
+    float s = 0.0f;
+    if (labels[b] == 1) s = norms[b] / q;           /* :306, :313 */
+    else if (labels[b] == 2) s = or_f16_to_f32(amp[b]); /* :314 */
+    uint32_t bit = (signs[i >> 3] >> (7 - (i & 7))) & 1u; /* :203-209 */
+    float sgn = 1.0f - 2.0f * (float)bit;
+    float d = s * sgn;                              /* :317-319 */
+    float ag = alpha * g[i];
+    m_hat[i] = ag + d;                              /* :323 */
+  }
+}
+
+/* decompose, reference costate.py:22-43. */
+float or_decompose(const float* m, const float* g, uint64_t n, float* delta) {
+  uint64_t nb = (n + OR_BS - 1) / OR_BS;
+  double* bgg = (double*)malloc(nb * sizeof(double));
+  double* bmg = (double*)malloc(nb * sizeof(double));
+  double blk[OR_BS];
+  for (uint64_t b = 0; b < nb; ++b) {
+    for (int j = 0; j < OR_BS; ++j) {
+      uint64_t i = b * OR_BS + j;
+      blk[j] = i < n ? (double)g[i] * (double)g[i] : 0.0;
+    }
+    bgg[b] = pairwise(blk, OR_BS);
+    for (int j = 0; j < OR_BS; ++j) {
+      uint64_t i = b * OR_BS + j;
+      blk[j] = i < n ? (double)m[i] * (double)g[i] : 0.0;
+    }
+    bmg[b] = pairwise(blk, OR_BS);
+  }
+  float gg = (float)(or_pairwise_sum(bgg, nb) + 0.0);
+  float mg = (float)(or_pairwise_sum(bmg, nb) + 0.0);
+  free(bgg);
+  free(bmg);
+  float alpha = gg > 0.0f ? mg / gg : 0.0f;        /* :39-41 */
+  for (uint64_t i = 0; i < n; ++i) {
+    float ag = alpha * g[i];
+    delta[i] = m[i] - ag;                          /* :42 */
+  }
+  return alpha;
+}
+
+/* L2 norm of block b of x (zero padded), fp64 pairwise, rounded once. */
+static float block_norm(const float* x, uint64_t n, uint64_t b) {
+  double blk[OR_BS];
+  for (int j = 0; j < OR_BS; ++j) {
+    uint64_t i = b * OR_BS + j;
+    double v = i < n ? (double)x[i] : 0.0;
+    blk[j] = v * v;
+  }
+  return (float)sqrt(pairwise(blk, OR_BS));
+}
+
+/* compute_block_ratios, reference costate.py:51-86. */
+void or_block_ratios(const float* delta, const float* m, uint64_t n, float* ratios) {
+  uint64_t nb = (n + OR_BS - 1) / OR_BS;
+  for (uint64_t b = 0; b < nb; ++b) {
+    float dn = block_norm(delta, n, b);
+    float mn = block_norm(m, n, b);
+    ratios[b] = mn == 0.0f ? 0.0f : dn / mn;       /* :81-84 */
+  }
+}
+
+static int cmp_u32(const void* a, const void* b) {
+  uint32_t x = *(const uint32_t*)a, y = *(const uint32_t*)b;
+  return x < y ? -1 : (x > y ? 1 : 0);
+}
+
+/* compute_thresholds, reference costate.py:94-118 (ratios are >= +0 or NaN,
+ * so the fp32 bit patterns sort like torch.sort with NaN last). */
+void or_thresholds(const float* ratios, uint64_t nb, uint64_t k_lo, uint64_t k_hi, float* tau0, float* tau1) {
+  uint32_t* s = (uint32_t*)malloc(nb * sizeof(uint32_t));
+  for (uint64_t i = 0; i < nb; ++i) s[i] = f2u(ratios[i]);
+  qsort(s, nb, sizeof(uint32_t), cmp_u32);
+  *tau0 = u2f(s[k_lo]);
+  *tau1 = u2f(s[k_hi]);
+  free(s);
+}
+
+/* classify_blocks, reference costate.py:126-149. */
+void or_classify(const float* ratios, uint64_t nb, float tau0, float tau1, uint8_t* labels) {
+  for (uint64_t b = 0; b < nb; ++b) {
+    uint8_t l = 0;
+    if (ratios[b] >= tau0) l = 1;
+    if (ratios[b] >= tau1) l = 2;
+    labels[b] = l;
+  }
+}
+
+/* encode_blocks, reference costate.py:213-258 (+ _pack_signs :157-182). */
+void or_encode(const float* delta, uint64_t n, float q, uint8_t* signs, float* norms, uint16_t* amp) {
+  uint64_t nb = (n + OR_BS - 1) / OR_BS;
+  for (uint64_t b = 0; b < nb; ++b) {
+    float nd = block_norm(delta, n, b);
+    norms[b] = nd;
+    amp[b] = or_f32_to_f16(nd / q);
+  }
+  uint64_t nbytes = (n + 7) / 8;
+  for (uint64_t j = 0; j < nbytes; ++j) {
+    uint32_t byte = 0;
+    for (int k = 0; k < 8; ++k) {
+      uint64_t i = j * 8 + k;
+      uint32_t bit = (i < n && delta[i] < 0.0f) ? 1u : 0u;
+      byte |= bit << (7 - k);
+    }
+    signs[j] = (uint8_t)byte;
+  }
+}
+
+/* CoStateManager.update, reference costate.py:367-464 (no error feedback).
+ * State arrays are updated in place; *alpha is alpha_{t-1} on entry and
+ * alpha_t on exit.  m_out receives m_t. */
+void or_costate_update(const float* g, uint64_t n, float beta1, float one_minus_beta1, float q,
+                       uint64_t k_lo, uint64_t k_hi, int has_state, uint8_t* labels, uint8_t* signs,
+                       float* norms, uint16_t* amp, float* alpha, float* m_out) {
+  uint64_t nb = (n + OR_BS - 1) / OR_BS;
+  float* m_hat = (float*)calloc(n, sizeof(float));
+  if (has_state) or_decode_blocks(labels, signs, norms, amp, *alpha, g, n, q, m_hat);
+  for (uint64_t i = 0; i < n; ++i) {
+    float a = beta1 * m_hat[i];
+    float b = one_minus_beta1 * g[i];
+    m_out[i] = a + b;                              /* :416 */
+  }
+  float* delta = (float*)malloc(n * sizeof(float));
+  float* ratios = (float*)malloc(nb * sizeof(float));
+  float al = or_decompose(m_out, g, n, delta);
+  or_block_ratios(delta, m_out, n, ratios);
+  float t0, t1;
+  or_thresholds(ratios, nb, k_lo, k_hi, &t0, &t1);
+  or_classify(ratios, nb, t0, t1, labels);
+  or_encode(delta, n, q, signs, norms, amp);
+  *alpha = al;
+  free(m_hat);
+  free(delta);
+  free(ratios);
+}
+
+/* fused_v_update, reference quantize.py:222-299.  idx (N_pad) and scales
+ * (2*nb f16) updated in place; v_out receives v (n). */
+void or_fused_v_update(uint8_t* idx, uint16_t* scales, const float* g, uint64_t n, int bits, float beta2,
+                       float one_minus_beta2, uint32_t tid, uint32_t step, uint64_t seed, float* v_out) {
+  uint64_t nb = (n + OR_BS - 1) / OR_BS;
+  float nbk = (float)(1u << bits);
+  float vb[OR_BS], lg[OR_BS];
+  for (uint64_t b = 0; b < nb; ++b) {
+    float lmin = or_f16_to_f32(scales[2 * b]);
+    float lmax = or_f16_to_f32(scales[2 * b + 1]);
+    float span = lmax - lmin;                      /* :253-255 */
+    float nmin = INFINITY, nmax = -INFINITY;
+    int nan_seen = 0;
+    float nan_val = 0.0f;
+    for (int j = 0; j < OR_BS; ++j) {
+      uint64_t i = b * OR_BS + j;
+      float t = ((float)idx[i] + 0.5f) / nbk;      /* :256 */
+      float lv = lmin + t * span;
+      float vo = or_expf(lv);
+      float g2 = i < n ? g[i] * g[i] : 0.0f;       /* :259-267 */
+      float vb1 = vo * beta2;
+      vb[j] = fmaf(one_minus_beta2, g2, vb1);      /* :270 add_(alpha=) is fused */
+      float c = vb[j] < 1e-38f ? 1e-38f : vb[j];   /* :275 clamp(min=1e-38) */
+      lg[j] = or_logf(c);
+      if (i < n) {                                 /* :276-280, NaN propagates */
+        if (lg[j] != lg[j]) { if (!nan_seen) { nan_seen = 1; nan_val = lg[j]; } }
+        else {
+          if (lg[j] < nmin) nmin = lg[j];
+          if (lg[j] > nmax) nmax = lg[j];
+        }
+      }
+    }
+    if (nan_seen) { nmin = nan_val; nmax = nan_val; }
+    scales[2 * b] = or_f32_to_f16(nmin);           /* :281 */
+    scales[2 * b + 1] = or_f32_to_f16(nmax);
+    float sp = nmax - nmin;
+    if (sp < 1e-10f) sp = 1e-10f;                  /* :283 clamp(min=1e-10) */
+    for (int j = 0; j < OR_BS; ++j) {
+      uint64_t i = b * OR_BS + j;
+      float c = ((lg[j] - nmin) / sp) * nbk;       /* :284-285 */
+      float f = floorf(c);
+      float fr = c - f;
+      float u = or_uniform(i, tid, step, seed);
+      float r = f + (u < fr ? 1.0f : 0.0f);        /* :288-294 */
+      if (r < 0.0f) r = 0.0f;
+      if (r > nbk - 1.0f) r = nbk - 1.0f;
+      idx[i] = (r != r) ? 0 : (uint8_t)r;
+      if (i < n) v_out[i] = vb[j];
+    }
+  }
+}
+
+/* ------------------------------------------------------ one parameter's step */
+typedef struct OrTensor {
+  void* param;
+  const void* grad;
+  uint8_t* v_idx;
+  uint16_t* v_scales;
+  float* exp_avg_sq;
+  float* exp_avg;
+  uint8_t* signs;
+  uint8_t* labels;
+  float* norms;
+  uint16_t* amp;
+  float* alpha;
+  uint64_t n;
+  uint32_t dtype, flags, v_bits, tensor_id, step, k_lo, k_hi, pad1;
+  float c_wd, beta1, one_minus_beta1, beta2, one_minus_beta2, bias_correction1, bias_correction2, eps,
+      neg_lr, sqrt_block;
+} OrTensor;
+
+#define OR_FLAG_COSTATE 1u
+#define OR_FLAG_COMPRESS_V 2u
+#define OR_FLAG_HAS_STATE 4u
+#define OR_FLAG_WD 8u
+
+/* TurboAdam._full_step_kernel body for one parameter, reference
+ * optimizer.py:97-170 (the caller increments the step counter and supplies
+ * the fp32 scalars). */
+void or_step_tensor(OrTensor* t, uint64_t seed) {
+  uint64_t n = t->n;
+  float* g = (float*)malloc(n * sizeof(float));
+  float* p = (float*)malloc(n * sizeof(float));
+  float* m = (float*)malloc(n * sizeof(float));
+  float* v = (float*)malloc(n * sizeof(float));
+  for (uint64_t i = 0; i < n; ++i) {
+    g[i] = ld(t->grad, (int)t->dtype, i);
+    p[i] = ld(t->param, (int)t->dtype, i);
+  }
+  if (t->flags & OR_FLAG_WD)                        /* :106-107 */
+    for (uint64_t i = 0; i < n; ++i) p[i] = round_p(p[i] * t->c_wd, (int)t->dtype);
+  if (t->flags & OR_FLAG_COSTATE) {                 /* :110-111 */
+    or_costate_update(g, n, t->beta1, t->one_minus_beta1, t->sqrt_block, t->k_lo, t->k_hi,
+                      (t->flags & OR_FLAG_HAS_STATE) != 0, t->labels, t->signs, t->norms, t->amp, t->alpha, m);
+  } else {                                          /* :113-114 */
+    for (uint64_t i = 0; i < n; ++i) {
+      float a = t->exp_avg[i] * t->beta1;
+      t->exp_avg[i] = fmaf(t->one_minus_beta1, g[i], a);
+      m[i] = t->exp_avg[i];
+    }
+  }
+  if (t->flags & OR_FLAG_COMPRESS_V) {              /* :121-163 */
+    or_fused_v_update(t->v_idx, t->v_scales, g, n, (int)t->v_bits, t->beta2, t->one_minus_beta2, t->tensor_id,
+                      t->step, seed, v);
+  } else {                                          /* :165-167 */
+    for (uint64_t i = 0; i < n; ++i) {
+      float a = t->exp_avg_sq[i] * t->beta2;
+      float b = t->one_minus_beta2 * g[i];
+      t->exp_avg_sq[i] = fmaf(b, g[i], a);
+      v[i] = t->exp_avg_sq[i];
+    }
+  }
+  for (uint64_t i = 0; i < n; ++i) {
+    float vq = v[i] / t->bias_correction2;          /* :163 */
+    float den = sqrtf(vq) + t->eps;
+    float d2 = den * t->bias_correction1;           /* :170 */
+    float num = t->neg_lr * m[i];
+    float upd = num / d2;
+    p[i] = p[i] + upd;
+    st(t->param, (int)t->dtype, i, p[i]);
+  }
+  free(g);
+  free(p);
+  free(m);
+  free(v);
+}
+
+size_t or_struct_size(void) { return sizeof(OrTensor); }

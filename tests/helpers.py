@@ -1,0 +1,148 @@
+"""Shared helpers: run the GPU TurboAdam and the CPU oracle side by side."""
+
+import sys
+
+import numpy as np
+import torch
+
+from oracle import oracle as O
+
+TORCH_DT = {O.DT_F32: torch.float32, O.DT_BF16: torch.bfloat16, O.DT_F16: torch.float16}
+
+
+def log(msg: str) -> None:
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def to_bits(x: np.ndarray, dt: int) -> np.ndarray:
+    """fp32 numpy -> oracle representation of dtype dt (fp32 or uint16 bits, RNE)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    if dt == O.DT_F32:
+        return x.copy()
+    t = torch.from_numpy(x).to(TORCH_DT[dt])
+    return t.view(torch.int16).numpy().view(np.uint16).copy()
+
+
+def to_torch(a: np.ndarray, dt: int, shape, device) -> torch.Tensor:
+    if dt == O.DT_F32:
+        t = torch.from_numpy(a.copy())
+    else:
+        t = torch.from_numpy(a.view(np.int16).copy()).view(TORCH_DT[dt])
+    return t.reshape(shape).to(device)
+
+
+def from_torch(t: torch.Tensor) -> np.ndarray:
+    t = t.detach().reshape(-1).cpu()
+    if t.dtype == torch.float32:
+        return t.numpy().copy()
+    if t.dtype in (torch.bfloat16, torch.float16):
+        return t.view(torch.int16).numpy().view(np.uint16).copy()
+    if t.dtype == torch.uint8:
+        return t.numpy().copy()
+    raise TypeError(t.dtype)
+
+
+def f16_bits(t: torch.Tensor) -> np.ndarray:
+    return t.detach().reshape(-1).cpu().view(torch.int16).numpy().view(np.uint16).copy()
+
+
+def gpu_state(opt, p) -> dict:
+    """Numpy view of a GPU TurboAdam parameter state in the oracle's key names."""
+    st = opt.state[p]
+    out = {"step": st["step"], "_compress_m": st["_compress_m"]}
+    if st["_compress_m"]:
+        mgr = st["m_mgr"]
+        enc = mgr._encoded
+        out["labels"] = from_torch(enc["labels"])
+        out["sign_packed"] = from_torch(enc["sign_packed"])
+        out["block_norms"] = from_torch(enc["block_norms"])
+        out["amp"] = f16_bits(enc["scales"])
+        out["alpha"] = from_torch(mgr._alpha.reshape(1))
+        out["has_state"] = mgr._has_state
+    else:
+        out["exp_avg"] = from_torch(st["exp_avg"])
+    if "exp_avg_sq" in st:
+        out["exp_avg_sq"] = from_torch(st["exp_avg_sq"])
+    if "compressed_v" in st:
+        out["indices"] = from_torch(st["compressed_v"]["indices"])
+        out["scales"] = f16_bits(st["compressed_v"]["scales"])
+    return out
+
+
+STATE_KEYS = ["labels", "sign_packed", "block_norms", "amp", "alpha", "exp_avg", "exp_avg_sq", "indices", "scales"]
+
+
+def compare_states(gst: dict, ost: dict, where: str) -> list:
+    """Bit-exact comparison; returns a list of mismatch descriptions."""
+    bad = []
+    for k in STATE_KEYS:
+        if k not in ost:
+            continue
+        a = gst.get(k)
+        b = ost[k]
+        if a is None:
+            bad.append(f"{where}: {k} missing on GPU")
+            continue
+        if a.shape != b.shape:
+            bad.append(f"{where}: {k} shape {a.shape} vs {b.shape}")
+            continue
+        av = a.view(np.uint32) if a.dtype == np.float32 else a
+        bv = b.view(np.uint32) if b.dtype == np.float32 else b
+        nd = int(np.count_nonzero(av != bv))
+        if nd:
+            i = int(np.flatnonzero(av != bv)[0])
+            bad.append(f"{where}: {k} differs in {nd}/{a.size} (first at {i}: gpu {a[i]} oracle {b[i]})")
+    return bad
+
+
+def make_grads(rng, sizes, dts, sigmas, drifts=None, drift_scale=0.3):
+    out = []
+    for i, n in enumerate(sizes):
+        g = rng.standard_normal(n).astype(np.float32) * np.float32(sigmas[i])
+        if drifts is not None:
+            g = g + np.float32(drift_scale * sigmas[i]) * drifts[i]
+        out.append(to_bits(g.astype(np.float32), dts[i]))
+    return out
+
+
+def run_side_by_side(sizes, dts, steps, seed=0, check_every=1, shapes=None, grad_none=None, **kw):
+    """Step the GPU optimizer and the oracle on identical inputs; return mismatch list."""
+    from turboadam_amd import TurboAdam
+
+    dev = torch.device("cuda:0")
+    rng = np.random.default_rng(seed)
+    shapes = shapes or [(n,) for n in sizes]
+    init = [to_bits((rng.standard_normal(n) * 0.02).astype(np.float32), dts[i]) for i, n in enumerate(sizes)]
+    o_params = [a.copy() for a in init]
+    g_params = [torch.nn.Parameter(to_torch(a, dts[i], shapes[i], dev)) for i, a in enumerate(init)]
+    opt = TurboAdam(g_params, **kw)
+    opt.philox_seed = 1234567 + seed
+    orc = O.OracleTurboAdam(o_params, dtypes=dts, seed=1234567 + seed, **kw)
+    sigmas = np.exp(np.log(1e-3) + rng.standard_normal(len(sizes)))
+    drifts = [rng.standard_normal(n).astype(np.float32) for n in sizes]
+    bad = []
+    for s in range(steps):
+        grads = make_grads(rng, sizes, dts, sigmas, drifts)
+        if grad_none is not None:
+            grads = [None if grad_none(s, i) else g for i, g in enumerate(grads)]
+        for i, p in enumerate(g_params):
+            p.grad = None if grads[i] is None else to_torch(grads[i], dts[i], shapes[i], dev)
+        opt.step()
+        orc.step(grads)
+        if (s + 1) % check_every == 0 or s == steps - 1:
+            torch.cuda.synchronize()
+            for i, p in enumerate(g_params):
+                if i not in orc.state:
+                    continue
+                where = f"step {s + 1} tensor {i} (n={sizes[i]})"
+                pa = from_torch(p.data)
+                pb = o_params[i]
+                if not np.array_equal(pa.view(np.uint32) if pa.dtype == np.float32 else pa,
+                                      pb.view(np.uint32) if pb.dtype == np.float32 else pb):
+                    nd = int(np.count_nonzero(pa != pb))
+                    bad.append(f"{where}: param differs in {nd}/{pa.size}")
+                bad += compare_states(gpu_state(opt, p), orc.state[i], where)
+            if bad:
+                return bad
+    return bad

@@ -1,0 +1,156 @@
+"""GPU parity: the gfx950 kernels (through the C ABI) against the CPU oracle.
+
+Bar: bit-exact for every packed-state byte (1Q indices, fp16 scales, sign
+bits, labels, fp16 amplitudes), for block norms, alpha and parameters, on
+identical inputs and Philox draws.  Sizes are small enough for the scalar
+oracle to finish in seconds; full-size configurations are covered by the
+size-independent checks in test_gpu_invariants.py.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from tests.helpers import log, run_side_by_side
+
+pytestmark = pytest.mark.gpu
+
+F32, BF16, F16 = O.DT_F32, O.DT_BF16, O.DT_F16
+
+
+def _lib():
+    from turboadam_amd import _lib
+
+    return _lib, _lib.load()
+
+
+def _eval(fn, x):
+    _l, lib = _lib()
+    dev = torch.device("cuda:0")
+    xi = torch.from_numpy(x).to(dev)
+    out = torch.empty_like(xi)
+    _l.check(lib.tam_math_eval(fn, xi.data_ptr(), out.data_ptr(), x.size, _l.stream_of(dev)), "tam_math_eval")
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+def _edge_floats(rng, n):
+    bits = rng.integers(0, 0x7F800000, size=n, dtype=np.uint32)
+    specials = np.array([0x00000001, 0x007FFFFF, 0x00800000, 0x3F800000, 0x3F7FFFFF, 0x3F800001,
+                         0x7F7FFFFF, 0x00000000, 0x7F800000, 0x0036F9F6], dtype=np.uint32)
+    return np.concatenate([bits, specials]).view(np.float32)
+
+
+def test_device_log_is_correctly_rounded():
+    log("tam_math_eval log: 4M random positive fp32 + edges")
+    rng = np.random.default_rng(1)
+    x = _edge_floats(rng, 1 << 22)
+    got = _eval(0, x)
+    L = O.lib()
+    idx = rng.choice(x.size, 200000, replace=False)
+    want = np.array([L.or_logf(float(v)) for v in x[idx]], dtype=np.float32)
+    assert np.array_equal(got[idx].view(np.uint32), want.view(np.uint32))
+    # device == host build of the same function over all samples
+    host = np.log(x.astype(np.longdouble)).astype(np.float32)
+    ok = np.isfinite(x) & (x > 0)
+    assert np.array_equal(got[ok].view(np.uint32), host[ok].view(np.uint32))
+
+
+def test_device_exp_is_correctly_rounded():
+    log("tam_math_eval exp: [-104, 89]")
+    rng = np.random.default_rng(2)
+    x = np.concatenate([rng.uniform(-104, 89, 1 << 22), rng.uniform(-90, -60, 1 << 20),
+                        np.array([-87.5, -69.0625, 0.0, 88.72, -103.9])]).astype(np.float32)
+    got = _eval(1, x)
+    want = np.exp(x.astype(np.longdouble)).astype(np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_device_half_and_bf16_rounding():
+    log("tam_math_eval f16/bf16 round trips")
+    rng = np.random.default_rng(3)
+    x = np.concatenate([_edge_floats(rng, 1 << 20), -_edge_floats(rng, 1 << 18)]).astype(np.float32)
+    x = x[np.isfinite(x)]
+    got16 = _eval(2, x)
+    want16 = x.astype(np.float16).astype(np.float32)
+    assert np.array_equal(got16.view(np.uint32), want16.view(np.uint32))
+    gotbf = _eval(3, x)
+    wantbf = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(gotbf.view(np.uint32), wantbf.view(np.uint32))
+
+
+def test_device_sqrt_is_correctly_rounded():
+    rng = np.random.default_rng(4)
+    x = _edge_floats(rng, 1 << 20)
+    got = _eval(4, x)
+    assert np.array_equal(got.view(np.uint32), np.sqrt(x).view(np.uint32))
+
+
+def test_philox_uniforms_match_oracle():
+    _l, lib = _lib()
+    dev = torch.device("cuda:0")
+    for tid, step, seed, count in [(0, 1, 0, 1000), (7, 123, 0x7A3D5EED0BADC0DE, 4099), (291, 20, 42, 1 << 16)]:
+        log(f"philox tid={tid} step={step} count={count}")
+        out = torch.empty(count, dtype=torch.float32, device=dev)
+        _l.check(lib.tam_philox_uniforms(tid, step, seed, count, out.data_ptr(), _l.stream_of(dev)), "philox")
+        torch.cuda.synchronize()
+        want = O.philox_uniforms(tid, step, seed, count)
+        assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
+def _check(bad):
+    assert not bad, "\n".join(bad[:20])
+
+
+def test_v_only_fp32_ragged():
+    log("v-only fp32, sizes with tails, 8 steps")
+    _check(run_side_by_side([70000, 300, 1, 4096 + 77], [F32] * 4, steps=8, compress_m=False, lr=1e-3))
+
+
+def test_m_and_v_fp32_mixed_sizes():
+    log("m+v fp32 (CoState + fp32-m), 10 steps, wd")
+    sizes = [4096, 5000, 128 * 40 + 3, 300, 1, 2304 * 8]
+    _check(run_side_by_side(sizes, [F32] * len(sizes), steps=10, lr=6e-4, weight_decay=0.01))
+
+
+def test_m_and_v_bf16():
+    log("m+v bf16, 8 steps")
+    sizes = [4096 * 3, 8192 + 128, 777]
+    _check(run_side_by_side(sizes, [BF16] * len(sizes), steps=8, lr=1e-3, weight_decay=0.1))
+
+
+def test_m_and_v_fp16():
+    log("m+v fp16, 6 steps")
+    sizes = [4096 * 2, 1000]
+    _check(run_side_by_side(sizes, [F16] * len(sizes), steps=6, lr=1e-3))
+
+
+@pytest.mark.parametrize("bits", [2, 3, 6, 8])
+def test_v_bits(bits):
+    log(f"m+v fp32 v_bits={bits}")
+    sizes = [4096 + 1000, 513]
+    _check(run_side_by_side(sizes, [F32] * 2, steps=5, v_bits=bits, null_pct=0.05, amp_pct=0.95))
+
+
+def test_uncompressed_paths():
+    log("compress_m only / compress_v only / neither")
+    sizes = [6000, 200]
+    _check(run_side_by_side(sizes, [F32] * 2, steps=5, compress_v=False))
+    _check(run_side_by_side(sizes, [F32] * 2, steps=5, compress_m=False))
+    _check(run_side_by_side(sizes, [F32] * 2, steps=5, compress_m=False, compress_v=False))
+
+
+def test_grad_none_and_late_params():
+    log("grad None on some steps")
+    sizes = [5000, 300, 9000]
+    _check(run_side_by_side(sizes, [F32] * 3, steps=6, grad_none=lambda s, i: (i == 1 and s % 2 == 0) or
+                            (i == 2 and s < 2)))
+
+
+def test_gpt2_block_shapes_few_steps():
+    log("GPT-2 block (config 0 shapes), fp32, 3 steps")
+    shapes = [(768,), (768,), (768, 2304), (2304,), (768, 768), (768,), (768,), (768,), (768, 3072), (3072,),
+              (3072, 768), (768,)]
+    sizes = [int(np.prod(s)) for s in shapes]
+    _check(run_side_by_side(sizes, [F32] * len(sizes), steps=3, shapes=shapes, lr=6e-4, weight_decay=0.01))

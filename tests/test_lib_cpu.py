@@ -1,0 +1,123 @@
+"""CPU: the C-ABI library loads, exports every symbol include/turboadam_amd.h
+declares, agrees with the Python struct mirror, and its host-only planning
+(tam_prepare) validates input and lays out tiles and workspace.  No GPU call.
+"""
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from turboadam_amd import _lib
+from turboadam_amd.build import LIB_PATH, REPO_DIR
+
+HEADER = os.path.join(REPO_DIR, "include", "turboadam_amd.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(tam_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(LIB_PATH)
+    names = _declared()
+    assert len(names) >= 9
+    for name in names:
+        assert hasattr(lib, name), name
+    assert set(names) == set(_lib.SIGNATURES), "binding and header disagree"
+
+
+def test_load_checks_abi_and_struct_layout():
+    lib = _lib.load()
+    assert lib.tam_abi_version() == _lib.ABI_VERSION
+    assert lib.tam_struct_size(0) == ctypes.sizeof(_lib.TamTensor) == 192
+    assert lib.tam_struct_size(1) == ctypes.sizeof(_lib.TamStepInfo)
+
+
+def _tensor(n, costate=True, compress_v=True, bits=4):
+    t = _lib.TamTensor()
+    t.param, t.grad = 0x10000, 0x20000
+    t.n = n
+    t.dtype = _lib.TAM_DTYPE_F32
+    t.flags = (_lib.TAM_FLAG_COSTATE if costate else 0) | (_lib.TAM_FLAG_COMPRESS_V if compress_v else 0)
+    t.v_idx, t.v_scales, t.v_bits = 0x30000, 0x40000, bits
+    t.exp_avg_sq = t.exp_avg = 0x50000
+    t.signs = t.labels = t.norms = t.amp = t.alpha = 0x60000
+    nb = (n + 127) // 128
+    t.k_lo, t.k_hi = max(0, int(0.1 * nb) - 1), min(nb - 1, int(0.9 * nb))
+    return t
+
+
+def _prepare(ts):
+    lib = _lib.load()
+    arr = (_lib.TamTensor * len(ts))(*ts)
+    info = _lib.TamStepInfo()
+    rc = lib.tam_prepare(arr, len(ts), ctypes.byref(info))
+    return rc, arr, info, lib.tam_last_error().decode()
+
+
+def test_prepare_layout():
+    rc, arr, info, _ = _prepare([_tensor(5000), _tensor(300, costate=False), _tensor(2048 * 16 + 1)])
+    assert rc == 0
+    assert [a.nb for a in arr] == [40, 3, 257]
+    assert [a.ntiles for a in arr] == [3, 1, 17]
+    assert [a.tile0 for a in arr] == [0, 3, 4]
+    assert info.total_tiles == 21 and info.n_costate == 2 and info.ratio_blocks == 40 + 257
+    assert arr[0].ratio_off == 0 and arr[2].ratio_off == 40
+    assert info.off_partials == 0
+    assert info.off_alpha >= 21 * 16 and info.off_ratios >= info.off_alpha + 3 * 4
+    assert info.ws_bytes >= info.off_ratios + 297 * 4
+    assert info.off_alpha % 256 == 0 and info.off_ratios % 256 == 0
+
+
+@pytest.mark.parametrize("mutate,msg", [
+    (lambda t: setattr(t, "n", 0), "no elements"),
+    (lambda t: setattr(t, "v_bits", 5), "v_bits"),
+    (lambda t: setattr(t, "dtype", 7), "dtype"),
+    (lambda t: setattr(t, "alpha", 0), "CoState"),
+    (lambda t: setattr(t, "v_idx", 0x30001), "misaligned"),
+    (lambda t: setattr(t, "k_hi", 10_000), "rank"),
+])
+def test_prepare_rejects_bad_input(mutate, msg):
+    t = _tensor(5000)
+    mutate(t)
+    rc, _, _, err = _prepare([t])
+    assert rc == 1 and msg in err
+
+
+def test_step_rejects_small_workspace_without_launching():
+    lib = _lib.load()
+    rc, arr, info, _ = _prepare([_tensor(5000)])
+    assert rc == 0
+    rc = lib.tam_multi_tensor_step(0x1000, arr, ctypes.byref(info), 0, 0x2000, info.ws_bytes - 1, None)
+    assert rc == 2 and "workspace" in lib.tam_last_error().decode()
+
+
+def test_optimizer_refuses_cpu_parameters():
+    from turboadam_amd import TurboAdam
+
+    p = torch.nn.Parameter(torch.randn(10))
+    opt = TurboAdam([p])
+    p.grad = torch.randn(10)
+    with pytest.raises(RuntimeError, match="HIP"):
+        opt.step()
+
+
+def test_constructor_validation_matches_reference():
+    from turboadam_amd import TurboAdam
+
+    ps = [torch.nn.Parameter(torch.randn(10, 10))]
+    with pytest.raises(ValueError, match="v_bits must be one of"):
+        TurboAdam(ps, v_bits=10)
+    with pytest.raises(NotImplementedError, match="CUDA graph capture"):
+        TurboAdam(ps, capturable=True)
+    opt = TurboAdam(ps)
+    d = opt.defaults
+    assert (d["lr"], d["betas"], d["eps"], d["weight_decay"], d["block_size"], d["v_bits"]) == \
+        (1e-3, (0.9, 0.999), 1e-8, 0.0, 128, 4)
+    assert d["compress_m"] is True and d["compress_v"] is True
+    assert (d["null_pct"], d["amp_pct"], d["min_m_compress_elements"]) == (0.10, 0.90, 4096)

@@ -1,0 +1,330 @@
+"""CPU: pin the oracle (oracle/tam_oracle.c) before trusting it.
+
+Each check is chosen so that a plausible slip in the oracle -- a wrong
+Philox constant, a wrong rounding in the fp16 conversion, an inaccurate
+transcendental, a dropped term, a transposed bit order, an off-by-one rank --
+fails here.  Sources of truth: published known-answer vectors (Random123),
+library routines (numpy fp16, torch bf16, torch.optim.Adam), exact arithmetic
+(Python decimal / fractions) and the closed forms the reference's own tests
+assert (tests/test_costate.py, tests/test_optimizer.py in the reference).
+"""
+
+import ctypes
+import decimal
+import math
+from decimal import Decimal as D
+from fractions import Fraction
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+
+L = O.lib()
+P = O.ptr
+
+
+# ---------------------------------------------------------------- Philox
+KATS = [  # Random123 kat_vectors, philox4x32 R=10
+    ((0, 0, 0, 0), (0, 0), (0x6627E8D5, 0xE169C58D, 0xBC57AC4C, 0x9B00DBD8)),
+    ((0xFFFFFFFF,) * 4, (0xFFFFFFFF, 0xFFFFFFFF), (0x408F276D, 0x41C83B0E, 0xA20BC7C6, 0x6D5451FD)),
+    ((0x243F6A88, 0x85A308D3, 0x13198A2E, 0x03707344), (0xA4093822, 0x299F31D0),
+     (0xD16CFE09, 0x94FDCCEB, 0x5001E420, 0x24126EA1)),
+]
+
+
+@pytest.mark.parametrize("ctr,key,want", KATS)
+def test_philox_known_answers(ctr, key, want):
+    c = np.array(ctr, np.uint32)
+    out = np.zeros(4, np.uint32)
+    L.or_philox4x32_10(P(c), key[0], key[1], P(out))
+    assert tuple(int(x) for x in out) == want
+
+
+def test_philox_uniform_layout():
+    # element e uses word e%4 of the call with counter (e//4, tid, step, 0)
+    seed = 0x0123456789ABCDEF
+    u = O.philox_uniforms(5, 9, seed, 12)
+    for e in range(12):
+        c = np.array([e // 4, 5, 9, 0], np.uint32)
+        out = np.zeros(4, np.uint32)
+        L.or_philox4x32_10(P(c), seed & 0xFFFFFFFF, seed >> 32, P(out))
+        assert u[e] == np.float32((int(out[e % 4]) >> 8) * 2.0**-24)
+    assert (u >= 0).all() and (u < 1).all()
+
+
+# ---------------------------------------------------------------- fp16 / bf16
+def test_f16_rounding_matches_numpy():
+    rng = np.random.default_rng(0)
+    bits = np.concatenate([
+        rng.integers(0, 2**32, 400000, dtype=np.uint64).astype(np.uint32),
+        # every fp32 near each fp16 boundary: fp16 values, their midpoints and neighbours
+        (np.arange(0, 0x7C00, dtype=np.uint32).astype(np.uint16).view(np.float16).astype(np.float32)
+         .view(np.uint32)[:, None] + np.array([0, 1, 0xFFFFFFFF, 0x1000, 0xFFF, 0x1001], np.uint32)).ravel(),
+    ])
+    x = bits.view(np.float32)
+    x = x[np.isfinite(x)]
+    want = x.astype(np.float16).view(np.uint16)
+    f = L.or_f32_to_f16
+    got = np.array([f(float(v)) for v in x], dtype=np.uint16)
+    assert np.array_equal(got, want)
+
+
+def test_bf16_rounding_matches_torch():
+    rng = np.random.default_rng(1)
+    x = rng.integers(0, 2**32, 200000, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    x = x[np.isfinite(x)]
+    want = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    f = L.or_f32_to_bf16
+    got = np.array([f(float(v)) for v in x], dtype=np.uint16)
+    assert np.array_equal(got, want)
+
+
+# ---------------------------------------------------------------- log / exp
+decimal.getcontext().prec = 50
+
+
+def _round_f32(y: D) -> np.float32:
+    """Correctly rounded fp32 of an exact Decimal (ties to even)."""
+    f = np.float32(float(y))
+    cands = [np.nextafter(f, np.float32(-np.inf)), f, np.nextafter(f, np.float32(np.inf))]
+    best = min(cands, key=lambda c: (abs(D(float(c)) - y), int(np.float32(c).view(np.uint32)) & 1))
+    return np.float32(best)
+
+
+def test_log_is_correctly_rounded():
+    rng = np.random.default_rng(2)
+    bits = np.concatenate([rng.integers(1, 0x7F800000, 6000, dtype=np.uint32),
+                           np.arange(0x3F7FFFF0, 0x3F800010, dtype=np.uint32),  # around 1
+                           np.array([1, 2, 0x007FFFFF, 0x00800000, 0x0036F9F6, 0x7F7FFFFF], np.uint32)])
+    for b in bits:
+        x = np.uint32(b).view(np.float32)
+        if x == 1.0:
+            assert L.or_logf(1.0) == 0.0
+            continue
+        want = _round_f32(D(float(x)).ln())
+        assert np.float32(L.or_logf(float(x))) == want, hex(b)
+
+
+def test_exp_is_correctly_rounded():
+    rng = np.random.default_rng(3)
+    xs = np.concatenate([rng.uniform(-104, 88.7, 6000), rng.uniform(-104, -87, 2000),
+                         [-69.0625, -87.5, 0.0, 1e-7, -1e-7]]).astype(np.float32)
+    for x in xs:
+        want = _round_f32(D(float(x)).exp())
+        assert np.float32(L.or_expf(float(x))) == want, float(x)
+
+
+# ---------------------------------------------------------------- pairwise sums
+def test_pairwise_sum_tree_and_padding():
+    rng = np.random.default_rng(4)
+    for n in [1, 2, 3, 7, 128, 129, 1000]:
+        x = rng.standard_normal(n) * 10.0 ** rng.integers(-8, 8, n)
+        P2 = 1 << max(0, (n - 1).bit_length())
+        buf = np.zeros(P2)
+        buf[:n] = x
+
+        def tree(a):
+            return a[0] if len(a) == 1 else tree(a[: len(a) // 2]) + tree(a[len(a) // 2:])
+
+        got = L.or_pairwise_sum(P(np.ascontiguousarray(x)), n)
+        assert got == tree(list(buf))
+        exact = float(sum(Fraction(v) for v in x))
+        assert abs(got - exact) <= 1e-12 * np.abs(x).sum()
+
+
+# ---------------------------------------------------------------- CoState closed forms
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def test_decompose_closed_forms():
+    rng = np.random.default_rng(5)
+    g = _f32(rng.standard_normal(256))
+    m = _f32(3.0 * g)
+    d = np.empty_like(m)
+    a = L.or_decompose(P(m), P(g), 256, P(d))
+    assert abs(a - 3.0) < 1e-6 and np.linalg.norm(d) < 1e-5
+    g = np.zeros(256, np.float32); g[0] = 1.0
+    m = np.zeros(256, np.float32); m[1] = 5.0
+    a = L.or_decompose(P(m), P(g), 256, P(d))
+    assert a == 0.0 and np.array_equal(d, m)
+    g = np.zeros(128, np.float32)
+    m = _f32(rng.standard_normal(128))
+    d = np.empty_like(m)
+    a = L.or_decompose(P(m), P(g), 128, P(d))
+    assert a == 0.0 and np.array_equal(d, m)
+    # alpha equals the exactly rounded m.g / g.g (dot products each rounded once)
+    m = _f32(rng.standard_normal(3000)); g = _f32(rng.standard_normal(3000)); d = np.empty_like(m)
+    a = L.or_decompose(P(m), P(g), 3000, P(d))
+    mg = np.float32(float(sum(Fraction(float(x)) * Fraction(float(y)) for x, y in zip(m, g))))
+    gg = np.float32(float(sum(Fraction(float(y)) ** 2 for y in g)))
+    assert abs(np.float32(a) - np.float32(mg / gg)) <= 2 * abs(np.spacing(np.float32(a)))
+    assert np.array_equal(d, _f32(m - _f32(np.float32(a) * g)))
+
+
+def test_block_ratios_closed_forms():
+    rng = np.random.default_rng(6)
+    m = _f32(rng.standard_normal(256))
+    r = np.empty(2, np.float32)
+    zero = np.zeros(256, np.float32)
+    mc = m.copy()
+    L.or_block_ratios(P(zero), P(m), 256, P(r))
+    assert (r == 0).all()
+    L.or_block_ratios(P(mc), P(m), 256, P(r))
+    assert np.allclose(r, 1.0, atol=1e-6)
+    L.or_block_ratios(P(m), P(zero), 256, P(r))
+    assert (r == 0).all()
+    # ragged: 300 elements -> 3 blocks, norm over the zero-padded block
+    d = _f32(rng.standard_normal(300)); mm = _f32(rng.standard_normal(300)); r3 = np.empty(3, np.float32)
+    L.or_block_ratios(P(d), P(mm), 300, P(r3))
+    ref = [np.linalg.norm(d[i * 128:(i + 1) * 128].astype(np.float64)) /
+           np.linalg.norm(mm[i * 128:(i + 1) * 128].astype(np.float64)) for i in range(3)]
+    assert np.allclose(r3, ref, rtol=1e-6)
+
+
+def _thr(r, null_pct=0.10, amp_pct=0.90):
+    r = _f32(r)
+    lo, hi = O.ranks(r.size, null_pct, amp_pct)
+    t0 = np.zeros(1, np.float32); t1 = np.zeros(1, np.float32)
+    L.or_thresholds(P(r), r.size, lo, hi, P(t0), P(t1))
+    return t0[0], t1[0]
+
+
+def test_thresholds_order_statistics():
+    t0, t1 = _thr(np.linspace(0, 1, 1000))
+    # reference test: |tau0 - 0.1| < 0.02; exactly: sorted[int(0.1*1000)-1] = sorted[99]
+    assert t0 == np.float32(np.linspace(0, 1, 1000)[99]) and t1 == np.float32(np.linspace(0, 1, 1000)[900])
+    assert _thr(np.full(128, 0.5)) == (0.5, 0.5)
+    assert _thr([0.42]) == (np.float32(0.42), np.float32(0.42))
+    rng = np.random.default_rng(7)
+    for nb in [2, 5, 10, 11, 4608, 10000]:
+        r = rng.choice([0.0, 0.25, 0.5, 1.0, 2.0], size=nb) * rng.random(nb).round(1)  # many ties and zeros
+        s = np.sort(_f32(r))
+        lo, hi = max(0, int(0.1 * nb) - 1), min(nb - 1, int(0.9 * nb))
+        assert _thr(r) == (s[lo], s[hi])
+    # probe 6 of the survey: n = 4608 -> ranks 459 and 4147
+    assert O.ranks(4608, 0.10, 0.90) == (459, 4147)
+
+
+def test_classify_boundaries():
+    r = _f32([0.01, 0.1, 0.5, 0.9, 1.5])
+    lab = np.empty(5, np.uint8)
+    L.or_classify(P(r), 5, ctypes.c_float(0.1), ctypes.c_float(0.9), P(lab))
+    assert lab.tolist() == [0, 1, 1, 2, 2]
+
+
+def test_sign_packing_every_byte():
+    # element 8j+k -> byte j, bit 7-k (MSB first), trailing bits of the last byte are 0
+    vals = np.array([(b >> (7 - k)) & 1 for b in range(256) for k in range(8)], np.float32)
+    delta = _f32(np.where(vals > 0, -1.0, 1.0))
+    n = delta.size
+    signs = np.zeros(n // 8, np.uint8); norms = np.zeros(n // 128, np.float32); amp = np.zeros(n // 128, np.uint16)
+    L.or_encode(P(delta), n, ctypes.c_float(np.float32(math.sqrt(128))), P(signs), P(norms), P(amp))
+    assert signs.tolist() == list(range(256))
+    # ragged: 13 elements -> 2 bytes, padding bits zero
+    d = _f32(-np.ones(13)); s2 = np.zeros(2, np.uint8); n2 = np.zeros(1, np.float32); a2 = np.zeros(1, np.uint16)
+    L.or_encode(P(d), 13, ctypes.c_float(np.float32(math.sqrt(128))), P(s2), P(n2), P(a2))
+    assert s2.tolist() == [0xFF, 0xF8]
+
+
+def test_encode_norms_and_amplitudes():
+    rng = np.random.default_rng(8)
+    d = _f32(rng.standard_normal(384) * 1e-3)
+    q = np.float32(math.sqrt(128))
+    s = np.zeros(48, np.uint8); nrm = np.zeros(3, np.float32); amp = np.zeros(3, np.uint16)
+    L.or_encode(P(d), 384, ctypes.c_float(q), P(s), P(nrm), P(amp))
+    for b in range(3):
+        exact = math.sqrt(float(sum(Fraction(float(v)) ** 2 for v in d[b * 128:(b + 1) * 128])))
+        assert abs(nrm[b] - exact) <= abs(np.spacing(nrm[b]))
+        assert amp[b] == np.float16(np.float32(nrm[b] / q)).view(np.uint16)
+
+
+def test_decode_formulas_per_label():
+    rng = np.random.default_rng(9)
+    n = 384
+    g = _f32(rng.standard_normal(n))
+    signs = rng.integers(0, 256, n // 8, dtype=np.uint8)
+    labels = np.array([0, 1, 2], np.uint8)
+    norms = _f32([3.0, 5.5, 7.25])
+    amp = np.array([np.float16(0.5), np.float16(0.125), np.float16(0.3)], np.float16).view(np.uint16)
+    out = np.empty(n, np.float32)
+    q = np.float32(math.sqrt(128))
+    alpha = np.float32(1.5)
+    L.or_decode_blocks(P(labels), P(signs), P(norms), P(amp), ctypes.c_float(alpha), P(g), n, ctypes.c_float(q),
+                       P(out))
+    bits = np.unpackbits(signs)  # MSB first
+    sgn = (1.0 - 2.0 * bits).astype(np.float32)
+    scale = np.repeat(_f32([0.0, norms[1] / q, np.float16(0.3)]), 128)
+    want = _f32(_f32(alpha * g) + _f32(scale * sgn))
+    assert np.array_equal(out, want)
+
+
+def test_first_costate_step_is_one_minus_beta1_times_g():
+    rng = np.random.default_rng(10)
+    n = 4096
+    p = _f32(rng.standard_normal(n) * 0.02)
+    g = _f32(rng.standard_normal(n))
+    opt = O.OracleTurboAdam([p], lr=0.0, compress_v=False)
+    opt.step([g])
+    st = opt.state[0]
+    # after step 1: alpha = (m.g)/(g.g) with m = f32(0.1)*g -> alpha is 0.1 up to dot rounding
+    assert abs(st["alpha"][0] - np.float32(0.1)) < 1e-6
+
+
+def test_weight_decay_only_closed_form():
+    # reference tests/test_optimizer.py:645-660: zero gradient, lr=1e-2, wd=0.1 -> x = 1*(1-1e-3)
+    p = np.ones(100, np.float32)
+    opt = O.OracleTurboAdam([p], lr=1e-2, weight_decay=0.1)
+    opt.step([np.zeros(100, np.float32)])
+    assert np.all(p == np.float32(np.float32(1.0) * np.float32(1.0 - 1e-2 * 0.1)))
+
+
+def test_no_compression_equals_torch_adam():
+    # reference tests/test_optimizer.py:250-285 (atol 1e-6); the oracle is tighter
+    torch.manual_seed(7)
+    grads = [[torch.randn(10, 10), torch.randn(20)] for _ in range(10)]
+    tp = [torch.nn.Parameter(torch.ones(10, 10)), torch.nn.Parameter(torch.ones(20))]
+    adam = torch.optim.Adam(tp, lr=1e-3, betas=(0.9, 0.999))
+    op = [np.ones(100, np.float32), np.ones(20, np.float32)]
+    orc = O.OracleTurboAdam(op, lr=1e-3, compress_m=False, compress_v=False)
+    for gs in grads:
+        for p, g in zip(tp, gs):
+            p.grad = g.clone()
+        adam.step()
+        orc.step([g.reshape(-1).numpy().copy() for g in gs])
+    for p, o in zip(tp, op):
+        assert np.allclose(p.detach().reshape(-1).numpy(), o, atol=1e-6, rtol=0)
+
+
+def test_v_update_invariants_and_unbiased_rounding():
+    rng = np.random.default_rng(11)
+    n = 128 * 64
+    g = _f32(rng.standard_normal(n) * 1e-3)
+    for bits in (2, 3, 4, 6, 8):
+        idx = np.zeros(n, np.uint8)
+        sc = np.full(2 * (n // 128), O.V_INIT_SCALE_BITS, np.uint16)
+        v = np.empty(n, np.float32)
+        L.or_fused_v_update(P(idx), P(sc), P(g), n, bits, ctypes.c_float(np.float32(0.999)),
+                            ctypes.c_float(np.float32(0.001)), 3, 1, 99, P(v))
+        assert idx.max() < 2**bits
+        s = sc.view(np.float16).astype(np.float32).reshape(-1, 2)
+        assert (s[:, 0] <= s[:, 1]).all()
+        assert (v > 0).all()
+    # unbiased stochastic rounding: average index over many Philox streams -> continuous position
+    g = _f32(rng.standard_normal(128) * 1e-3)
+    acc = np.zeros(128)
+    T = 400
+    for step in range(T):
+        idx = np.zeros(128, np.uint8)
+        sc = np.full(2, O.V_INIT_SCALE_BITS, np.uint16)
+        v = np.empty(128, np.float32)
+        L.or_fused_v_update(P(idx), P(sc), P(g), 128, 4, ctypes.c_float(np.float32(0.999)),
+                            ctypes.c_float(np.float32(0.001)), 0, step + 1, 5, P(v))
+        acc += idx
+    lv = np.log(np.maximum(v, np.float32(1e-38)).astype(np.float64))
+    s = sc.view(np.float16)
+    lo = np.min(lv); hi = np.max(lv)
+    cont = np.minimum((lv - lo) / (hi - lo) * 16, 15)
+    assert abs((acc / T - cont).mean()) < 0.05

@@ -1,0 +1,49 @@
+"""Build recipe for the gfx950 library (and, for tests, the CPU oracle).
+
+``python -m turboadam_amd.build`` compiles ``csrc/tam_step.hip`` with hipcc
+into ``turboadam_amd/_build/libturboadam_amd.so``.  Flags:
+  -ffp-contract=off      no implicit fma: every fma in the kernels is explicit,
+                         matching where the reference's torch ops fuse;
+  -packed-fp32-ops off   no v_pk_*_f32 (hipcc would otherwise form them);
+  default fp32 div/sqrt  hipcc's correctly rounded divide and square root.
+"""
+
+import os
+import subprocess
+import sys
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+REPO_DIR = os.path.dirname(PKG_DIR)
+BUILD_DIR = os.path.join(PKG_DIR, "_build")
+LIB_PATH = os.path.join(BUILD_DIR, "libturboadam_amd.so")
+SOURCES = [os.path.join(PKG_DIR, "csrc", "tam_step.hip")]
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = "gfx950"
+
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-shared",
+    "-ffp-contract=off",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-I", os.path.join(REPO_DIR, "include"),
+]
+
+
+def build_library(verbose: bool = False) -> str:
+    os.makedirs(BUILD_DIR, exist_ok=True)
+    tmp = LIB_PATH + ".tmp"
+    cmd = [HIPCC, *HIP_FLAGS, "-o", tmp, *SOURCES]
+    if verbose:
+        print(" ".join(cmd))
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stderr}")
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    print(build_library(verbose="-v" in sys.argv))

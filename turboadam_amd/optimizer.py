@@ -1,0 +1,390 @@
+"""TurboAdam: Adam/AdamW with CoState-compressed m and 1Q-compressed v, stepped
+by fused gfx950 kernels.
+
+Drop-in for the reference class (davidkny22/turboadam,
+src/turboadam/optimizer.py:19-292): same constructor keywords and
+validation, same step(closure) contract, same per-parameter state keys.
+Behind step() every parameter with a gradient is described in one table and
+updated by four kernel launches per device (libturboadam_amd,
+include/turboadam_amd.h), instead of the reference's per-parameter Python
+loop.  Parameters must live on a HIP device; there is no CPU path.
+"""
+
+import ctypes
+import math
+
+import torch
+from torch.optim import Optimizer
+
+from . import _lib
+from .costate import CoStateManager
+from .oneq import init_v_state
+from .utils import BLOCK_SIZE, num_blocks
+
+# Key of the Philox4x32-10 stream that drives stochastic rounding.  The
+# counter is (element/4, tensor_id, step, 0), so a step is reproducible from
+# (seed, parameter order, step number) alone.
+DEFAULT_SEED = 0x7A3D_5EED_0BAD_C0DE
+
+_DTYPES = {
+    torch.float32: _lib.TAM_DTYPE_F32,
+    torch.bfloat16: _lib.TAM_DTYPE_BF16,
+    torch.float16: _lib.TAM_DTYPE_F16,
+}
+
+_F32 = ctypes.c_float
+
+
+def _f32(x: float) -> float:
+    """Round a Python float (double) to fp32, as torch does for a scalar operand."""
+    return _F32(x).value
+
+
+class _DeviceBuffers:
+    """Per-device descriptor and workspace buffers, grown on demand."""
+
+    def __init__(self, device):
+        self.device = device
+        self.desc = None
+        self.ws = None
+
+    def desc_buffer(self, nbytes: int) -> torch.Tensor:
+        if self.desc is None or self.desc.numel() < nbytes:
+            self.desc = torch.empty(max(nbytes, 4096), dtype=torch.uint8, device=self.device)
+        return self.desc
+
+    def workspace(self, nbytes: int) -> torch.Tensor:
+        if self.ws is None or self.ws.numel() < nbytes:
+            self.ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=self.device)
+        return self.ws
+
+
+class TurboAdam(Optimizer):
+    """Adam optimizer with compressed first and second moment storage.
+
+    Args (reference optimizer.py:32-60):
+        params, lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0,
+        block_size=128, v_bits in {2,3,4,6,8} (default 4), compress_m=True,
+        compress_v=True, null_pct=0.10, amp_pct=0.90, error_feedback=False,
+        capturable=False, min_m_compress_elements=4096.
+    """
+
+    def __init__(
+        self,
+        params,
+        lr: float = 1e-3,
+        betas: tuple = (0.9, 0.999),
+        eps: float = 1e-8,
+        weight_decay: float = 0.0,
+        block_size: int = 128,
+        v_bits: int = 4,
+        compress_m: bool = True,
+        compress_v: bool = True,
+        null_pct: float = 0.10,
+        amp_pct: float = 0.90,
+        error_feedback: bool = False,
+        capturable: bool = False,
+        min_m_compress_elements: int = 4096,
+    ):
+        if v_bits not in (2, 3, 4, 6, 8):
+            raise ValueError(f"v_bits must be one of {{2, 3, 4, 6, 8}}, got {v_bits}")
+        if capturable:
+            raise NotImplementedError("CUDA graph capture is not yet supported. Set capturable=False.")
+        defaults = dict(
+            lr=lr,
+            betas=betas,
+            eps=eps,
+            weight_decay=weight_decay,
+            block_size=block_size,
+            v_bits=v_bits,
+            compress_m=compress_m,
+            compress_v=compress_v,
+            null_pct=null_pct,
+            amp_pct=amp_pct,
+            error_feedback=error_feedback,
+            min_m_compress_elements=min_m_compress_elements,
+        )
+        super().__init__(params, defaults)
+        self._group_step_tensors = {}
+        self.philox_seed = DEFAULT_SEED
+        self._buffers = {}
+        self._bc_values = {}
+        # Optional callable(pass_index, "begin"|"end") run around each of the four
+        # launches (the step is then issued pass by pass); used to time kernels.
+        self._pass_hook = None
+
+    # ------------------------------------------------------------------
+    # lazy state initialisation (reference optimizer.py:238-286)
+    # ------------------------------------------------------------------
+    def _init_state(self, p, group, group_idx, state):
+        if p.device.type != "cuda":
+            raise RuntimeError(
+                f"turboadam_amd.TurboAdam steps parameters on an MI355X (HIP) device; got a parameter on {p.device}"
+            )
+        if p.numel() == 0:
+            raise RuntimeError("turboadam_amd.TurboAdam: cannot optimise a parameter with no elements")
+        block_size = group["block_size"]
+        state["step"] = 0
+        compress_this_m = group["compress_m"] and p.numel() >= group["min_m_compress_elements"]
+        state["_compress_m"] = compress_this_m
+        if compress_this_m:
+            mgr = CoStateManager(
+                block_size=block_size,
+                null_pct=group["null_pct"],
+                amp_pct=group["amp_pct"],
+                error_feedback=group["error_feedback"],
+            )
+            mgr.allocate(p.numel(), p.device)
+            state["m_mgr"] = mgr
+        else:
+            state["exp_avg"] = torch.zeros_like(p, dtype=torch.float32, memory_format=torch.contiguous_format)
+        if not group["compress_v"]:
+            state["exp_avg_sq"] = torch.zeros_like(p, dtype=torch.float32, memory_format=torch.contiguous_format)
+        self._link_bias_tensors(p, group_idx, state)
+
+    def _link_bias_tensors(self, p, group_idx, state):
+        device_key = (group_idx, p.device.type, p.device.index)
+        if device_key not in self._group_step_tensors:
+            self._group_step_tensors[device_key] = {
+                "bc1": torch.empty(1, dtype=torch.float32, device=p.device),
+                "bc2": torch.empty(1, dtype=torch.float32, device=p.device),
+            }
+        t = self._group_step_tensors[device_key]
+        state["_bc1"] = t["bc1"]
+        state["_bc2"] = t["bc2"]
+
+    # ------------------------------------------------------------------
+    # bias corrections (reference optimizer.py:172-188)
+    # ------------------------------------------------------------------
+    def _prepare_step_scalars(self):
+        """Bias corrections for the coming step, per (group, device).
+
+        The reference fills one shared 1-element tensor per (group, device) once
+        per parameter in the group, so the value every parameter uses is the one
+        of the last parameter with state; the same value is computed here and
+        written to the shared tensors.
+        """
+        self._bc_values = {}
+        for group_idx, group in enumerate(self.param_groups):
+            beta1, beta2 = group["betas"]
+            for p in group["params"]:
+                if p not in self.state:
+                    continue
+                next_step = self.state[p]["step"] + 1
+                key = (group_idx, p.device.type, p.device.index)
+                self._bc_values[key] = (1.0 - beta1**next_step, 1.0 - beta2**next_step)
+        for key, (bc1, bc2) in self._bc_values.items():
+            t = self._group_step_tensors.get(key)
+            if t is not None:
+                t["bc1"].fill_(bc1)
+                t["bc2"].fill_(bc2)
+
+    # ------------------------------------------------------------------
+    # state dict (reference optimizer.py:194-218)
+    # ------------------------------------------------------------------
+    _PACKED_V = {"indices": torch.uint8, "scales": torch.float16}
+
+    def load_state_dict(self, state_dict):
+        """Load optimizer state.
+
+        torch's loader casts every state tensor to the parameter dtype (which
+        would round the f16 v scales of a bf16 parameter to bf16).  The packed
+        tensors are kept aside and restored unchanged, so a resumed run
+        continues bit for bit; CoStateManager tensors are moved to the
+        parameter's device as in the reference; a reference checkpoint's
+        `rand_buf` is dropped (this implementation draws from Philox).
+        """
+        saved_v = {}
+        for pid, st in state_dict.get("state", {}).items():
+            cv = st.get("compressed_v") if isinstance(st, dict) else None
+            if isinstance(cv, dict):
+                saved_v[pid] = {k: cv[k] for k in self._PACKED_V if isinstance(cv.get(k), torch.Tensor)}
+        super().load_state_dict(state_dict)
+        id_to_param = {}
+        idx = 0
+        for group in self.param_groups:
+            for p in group["params"]:
+                id_to_param[idx] = p
+                idx += 1
+        for group_idx, group in enumerate(self.param_groups):
+            for p in group["params"]:
+                if p not in self.state:
+                    continue
+                state = self.state[p]
+                device = p.device
+                cv = state.get("compressed_v")
+                if isinstance(cv, dict):
+                    cv.pop("rand_buf", None)
+                    pid = next((k for k, v in id_to_param.items() if v is p), None)
+                    for k, dt in self._PACKED_V.items():
+                        src = saved_v.get(pid, {}).get(k, cv.get(k))
+                        if isinstance(src, torch.Tensor):
+                            cv[k] = src.to(device=device, dtype=dt).clone().contiguous()
+                mgr = state.get("m_mgr")
+                if mgr is not None:
+                    if isinstance(mgr._alpha, torch.Tensor):
+                        mgr._alpha = mgr._alpha.to(device=device, dtype=torch.float32).clone()
+                    else:
+                        mgr._alpha = torch.tensor(float(mgr._alpha), dtype=torch.float32, device=device)
+                    if mgr._encoded is not None:
+                        canon = {"labels": torch.uint8, "sign_packed": torch.uint8,
+                                 "block_norms": torch.float32, "scales": torch.float16}
+                        for key, dt in canon.items():
+                            if key in mgr._encoded:
+                                mgr._encoded[key] = mgr._encoded[key].to(device=device, dtype=dt).clone()
+                    else:
+                        mgr.allocate(p.numel(), device)
+                    if mgr._ef_residual is not None:
+                        mgr._ef_residual = mgr._ef_residual.to(device=device)
+                for key in ("exp_avg", "exp_avg_sq"):
+                    if key in state:
+                        state[key] = state[key].to(device=device, dtype=torch.float32).clone()
+                self._link_bias_tensors(p, group_idx, state)
+
+    # ------------------------------------------------------------------
+    # the step
+    # ------------------------------------------------------------------
+    def _full_step_kernel(self):
+        """One fused step of every parameter with a gradient (reference optimizer.py:88-170)."""
+        per_device = {}
+        tensor_id = 0
+        for group_idx, group in enumerate(self.param_groups):
+            for p in group["params"]:
+                tid = tensor_id
+                tensor_id += 1
+                if p.grad is None:
+                    continue
+                state = self.state[p]
+                state["step"] += 1
+                per_device.setdefault(p.device, []).append((p, state, group, group_idx, tid))
+        for device, items in per_device.items():
+            self._launch(device, items)
+
+    def _describe(self, p, state, group, group_idx, tid) -> _lib.TamTensor:
+        if group["block_size"] != BLOCK_SIZE:
+            raise NotImplementedError("turboadam_amd kernels use 128-element blocks (block_size=128)")
+        if group["error_feedback"] and state["_compress_m"]:
+            raise NotImplementedError("turboadam_amd: CoState error feedback is not implemented")
+        g = p.grad
+        if g.is_sparse:
+            raise RuntimeError("turboadam_amd.TurboAdam does not support sparse gradients")
+        if p.dtype not in _DTYPES:
+            raise NotImplementedError(f"turboadam_amd: unsupported parameter dtype {p.dtype}")
+        if g.dtype != p.dtype or g.device != p.device:
+            raise RuntimeError("turboadam_amd: gradient dtype/device must match the parameter")
+        if not p.is_contiguous():
+            raise RuntimeError("turboadam_amd: parameters must be contiguous")
+        if not g.is_contiguous():
+            g = g.contiguous()
+            state["_grad_keepalive"] = g
+        t = _lib.TamTensor()
+        n = p.numel()
+        nb = num_blocks(n)
+        t.param = p.data_ptr()
+        t.grad = g.data_ptr()
+        t.n = n
+        t.dtype = _DTYPES[p.dtype]
+        flags = 0
+        lr = group["lr"]
+        beta1, beta2 = group["betas"]
+        wd = group["weight_decay"]
+        if group["compress_v"]:
+            cv = state["compressed_v"]
+            if cv["indices"].dtype != torch.uint8 or cv["scales"].dtype != torch.float16:
+                raise RuntimeError("turboadam_amd: compressed_v tensors have unexpected dtypes")
+            if cv["indices"].numel() != nb * BLOCK_SIZE or cv["scales"].numel() != nb * 2:
+                raise RuntimeError("turboadam_amd: compressed_v does not match the parameter size")
+            flags |= _lib.TAM_FLAG_COMPRESS_V
+            t.v_idx = cv["indices"].data_ptr()
+            t.v_scales = cv["scales"].data_ptr()
+            t.v_bits = cv["n_bits"]
+        else:
+            t.exp_avg_sq = state["exp_avg_sq"].data_ptr()
+        if state["_compress_m"]:
+            mgr = state["m_mgr"]
+            enc = mgr._encoded
+            flags |= _lib.TAM_FLAG_COSTATE
+            if mgr._has_state:
+                flags |= _lib.TAM_FLAG_HAS_STATE
+            t.signs = enc["sign_packed"].data_ptr()
+            t.labels = enc["labels"].data_ptr()
+            t.norms = enc["block_norms"].data_ptr()
+            t.amp = enc["scales"].data_ptr()
+            t.alpha = mgr._alpha.data_ptr()
+            t.k_lo, t.k_hi = mgr.ranks(nb)
+        else:
+            t.exp_avg = state["exp_avg"].data_ptr()
+        if wd != 0.0:
+            flags |= _lib.TAM_FLAG_WD
+        t.flags = flags
+        t.tensor_id = tid & 0xFFFFFFFF
+        t.step = state["step"] & 0xFFFFFFFF
+        bc1, bc2 = self._bc_values[(group_idx, p.device.type, p.device.index)]
+        t.c_wd = _f32(1.0 - lr * wd)
+        t.beta1 = _f32(beta1)
+        t.one_minus_beta1 = _f32(1.0 - beta1)
+        t.beta2 = _f32(beta2)
+        t.one_minus_beta2 = _f32(1.0 - beta2)
+        t.bias_correction1 = _f32(bc1)
+        t.bias_correction2 = _f32(bc2)
+        t.eps = _f32(group["eps"])
+        t.neg_lr = _f32(-lr)
+        t.sqrt_block = _f32(math.sqrt(BLOCK_SIZE))
+        return t
+
+    def _launch(self, device, items):
+        lib = _lib.load()
+        n = len(items)
+        arr = (_lib.TamTensor * n)()
+        for i, (p, state, group, group_idx, tid) in enumerate(items):
+            arr[i] = self._describe(p, state, group, group_idx, tid)
+        info = _lib.TamStepInfo()
+        _lib.check(lib.tam_prepare(arr, n, ctypes.byref(info)), "tam_prepare")
+        bufs = self._buffers.get(device)
+        if bufs is None:
+            bufs = self._buffers[device] = _DeviceBuffers(device)
+        nbytes = ctypes.sizeof(arr)
+        host = torch.empty(nbytes, dtype=torch.uint8, pin_memory=True)
+        ctypes.memmove(host.data_ptr(), ctypes.addressof(arr), nbytes)
+        desc = bufs.desc_buffer(nbytes)
+        ws = bufs.workspace(info.ws_bytes)
+        with torch.cuda.device(device):
+            desc[:nbytes].copy_(host, non_blocking=True)
+            stream = _lib.stream_of(device)
+            if self._pass_hook is None:
+                rc = lib.tam_multi_tensor_step(desc.data_ptr(), arr, ctypes.byref(info), self.philox_seed,
+                                               ws.data_ptr(), ws.numel(), stream)
+                _lib.check(rc, "tam_multi_tensor_step")
+            else:
+                for k in range(4):
+                    self._pass_hook(k, "begin")
+                    rc = lib.tam_step_pass(k, desc.data_ptr(), ctypes.byref(info), self.philox_seed,
+                                           ws.data_ptr(), ws.numel(), stream)
+                    _lib.check(rc, f"tam_step_pass({k})")
+                    self._pass_hook(k, "end")
+        for p, state, group, group_idx, tid in items:
+            state.pop("_grad_keepalive", None)
+            if state["_compress_m"]:
+                mgr = state["m_mgr"]
+                mgr._has_state = True
+                mgr._original_numel = p.numel()
+
+    @torch.no_grad()
+    def step(self, closure=None):
+        """Perform a single optimization step (reference optimizer.py:224-292)."""
+        loss = None
+        if closure is not None:
+            with torch.enable_grad():
+                loss = closure()
+        for group_idx, group in enumerate(self.param_groups):
+            for p in group["params"]:
+                if p.grad is None:
+                    continue
+                state = self.state[p]
+                if len(state) == 0:
+                    self._init_state(p, group, group_idx, state)
+                if group["compress_v"] and "compressed_v" not in state:
+                    state["compressed_v"] = init_v_state(p, group["v_bits"], group["block_size"])
+        self._prepare_step_scalars()
+        self._full_step_kernel()
+        return loss
