@@ -141,13 +141,38 @@ def cpu_baseline(shapes, dtype, kw, log_sigma, budget_s=12.0):
                       f"same workload, {len(times)} steps, median of steps 2+; scalar C oracle, 1 thread"}
 
 
+# ---------------------------------------------------------------- copy reference
+def copy_reference(args):
+    """Plain device-to-device copy of 2^30 fp32 (4 GiB read + 4 GiB written).
+
+    Calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE (known bytes per dispatch)
+    and measures the bandwidth a streaming kernel actually reaches.
+    """
+    dev = torch.device("cuda:0")
+    x = torch.ones(1 << 30, dtype=torch.float32, device=dev)
+    y = torch.empty_like(x)
+    for _ in range(args.warmup):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(args.steps):
+        y.copy_(x)
+    b.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / args.steps
+    nbytes = 2 * x.numel() * 4
+    print(json.dumps({"workload": "copy 2^30 fp32", "ms_per_copy": ms, "bytes_per_copy": nbytes,
+                      "GBps": nbytes / (ms * 1e-3) / 1e9}), flush=True)
+
+
 # ---------------------------------------------------------------- main
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="c3", choices=sorted(WORKLOADS))
+    ap.add_argument("--workload", default="c3", choices=sorted(WORKLOADS) + ["copy"])
     ap.add_argument("--grad-sets", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
@@ -159,6 +184,9 @@ def main():
     from turboadam_amd import TurboAdam, _lib
 
     _lib.load()
+    if args.workload == "copy":
+        copy_reference(args)
+        return
     shapes_fn, dtype, kw, log_sigma, desc = WORKLOADS[args.workload]
     shapes = shapes_fn()
     dev = torch.device("cuda:0")

@@ -73,7 +73,7 @@ typedef struct TamTensor {
   uint32_t tensor_id;   /* [in] Philox counter word 1                        */
   uint32_t step;        /* [in] 1-based step number (Philox counter word 2)  */
   uint32_t k_lo, k_hi;  /* [in] COSTATE: ranks of the P_null / P_amp ratios  */
-  uint32_t pad1;
+  float inv_bc2_f32;    /* [in] f32(1 / bias_correction2)                    */
   float c_wd;           /* [in] f32(1 - lr*wd)                               */
   float beta1, one_minus_beta1, beta2, one_minus_beta2; /* [in] f32 of the doubles */
   float bias_correction1, bias_correction2;             /* [in] f32(1-beta^step)   */
@@ -84,6 +84,7 @@ typedef struct TamTensor {
   uint32_t ntiles;      /* [derived] ceil(nb/16)                             */
   uint32_t pad0;
   uint64_t ratio_off;   /* [derived] COSTATE: offset of its ratios (blocks)  */
+  double inv_bc2;       /* [in] 1 / (double)bias_correction2 (correctly rounded) */
 } TamTensor;
 
 /* Launch summary and workspace layout, filled by tam_prepare(). */

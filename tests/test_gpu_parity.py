@@ -80,6 +80,19 @@ def test_device_half_and_bf16_rounding():
     assert np.array_equal(gotbf.view(np.uint32), wantbf.view(np.uint32))
 
 
+def test_device_hardware_bf16_rounding_equals_software():
+    # the certified bf16 update path uses v_cvt_pk_bf16_f32; it must agree with
+    # round-to-nearest-even on every non-NaN input (subnormals, ties, overflow)
+    rng = np.random.default_rng(5)
+    x = np.concatenate([_edge_floats(rng, 1 << 21), -_edge_floats(rng, 1 << 19),
+                        (np.arange(0, 1 << 16, dtype=np.uint32) << 16 | 0x8000).view(np.float32),
+                        (np.arange(0, 1 << 16, dtype=np.uint32) << 16 | 0x7FFF).view(np.float32)])
+    x = x[~np.isnan(x)]
+    hw = _eval(5, x)
+    sw = _eval(3, x)
+    assert np.array_equal(hw.view(np.uint32), sw.view(np.uint32))
+
+
 def test_device_sqrt_is_correctly_rounded():
     rng = np.random.default_rng(4)
     x = _edge_floats(rng, 1 << 20)

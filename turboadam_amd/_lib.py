@@ -46,7 +46,7 @@ class TamTensor(ctypes.Structure):
         ("step", ctypes.c_uint32),
         ("k_lo", ctypes.c_uint32),
         ("k_hi", ctypes.c_uint32),
-        ("pad1", ctypes.c_uint32),
+        ("inv_bc2_f32", ctypes.c_float),
         ("c_wd", ctypes.c_float),
         ("beta1", ctypes.c_float),
         ("one_minus_beta1", ctypes.c_float),
@@ -62,6 +62,7 @@ class TamTensor(ctypes.Structure):
         ("ntiles", ctypes.c_uint32),
         ("pad0", ctypes.c_uint32),
         ("ratio_off", ctypes.c_uint64),
+        ("inv_bc2", ctypes.c_double),
     ]
 
 

@@ -99,6 +99,9 @@ TAM_HD uint16_t tam_f32_to_bf16(float x) {
   return (uint16_t)(r >> 16);
 }
 TAM_HD float tam_bf16_to_f32(uint16_t b) { return tam_u2f((uint32_t)b << 16); }
+// Hardware round-to-nearest-even to bf16 (v_cvt_pk_bf16_f32 on gfx950).  Equal
+// to tam_f32_to_bf16 for every non-NaN input; callers pass no NaN.
+TAM_HD uint16_t tam_f32_to_bf16_rne(float x) { return __builtin_bit_cast(uint16_t, (__bf16)x); }
 
 // ---------------------------------------------------------------------------
 // double-double helpers (slow paths)

@@ -141,51 +141,70 @@ __device__ __forceinline__ void tam_store8_f32(float* base, uint64_t e0, uint64_
 }
 
 // ---------------------------------------------------------------------------
-// reductions
+// reductions over the 16 lanes of a block (one DPP row)
 // ---------------------------------------------------------------------------
+// gfx9 DPP controls: quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror
+// (lane i <-> 7-i within each half row), row_mirror (lane i <-> 15-i).
+#define TAM_DPP_XOR1 0xB1
+#define TAM_DPP_XOR2 0x4E
+#define TAM_DPP_HALF_MIRROR 0x141
+#define TAM_DPP_MIRROR 0x140
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t tam_dpp(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float tam_dppf(float v) {
+  return tam_u2f(tam_dpp<CTRL>(tam_f2u(v)));
+}
+template <int CTRL>
+__device__ __forceinline__ double tam_dppd(double v) {
+  const uint64_t u = tam_d2u(v);
+  const uint32_t lo = tam_dpp<CTRL>((uint32_t)u), hi = tam_dpp<CTRL>((uint32_t)(u >> 32));
+  return tam_u2d(((uint64_t)hi << 32) | lo);
+}
+
 // Balanced pairwise sum of 8 values (adjacent pairing).
 __device__ __forceinline__ double tam_pair8(const double* x) {
   return ((x[0] + x[1]) + (x[2] + x[3])) + ((x[4] + x[5]) + (x[6] + x[7]));
 }
 
-// Sum over the 16 lanes of a block, adjacent pairing (xor 1, 2, 4, 8); every
-// lane of the group ends with the same value.
+// Sum over the 16 lanes of a block with adjacent pairing.  After the two quad
+// steps every lane of a quad holds the same value, so the mirrors pair quad 0
+// with quad 1 and half 0 with half 1 exactly as a balanced tree does (and
+// a + b == b + a), and every lane ends with the same value.
 __device__ __forceinline__ double tam_block_sum(double v) {
-  v = v + __shfl_xor(v, 1, 16);
-  v = v + __shfl_xor(v, 2, 16);
-  v = v + __shfl_xor(v, 4, 16);
-  v = v + __shfl_xor(v, 8, 16);
+  v = v + tam_dppd<TAM_DPP_XOR1>(v);
+  v = v + tam_dppd<TAM_DPP_XOR2>(v);
+  v = v + tam_dppd<TAM_DPP_HALF_MIRROR>(v);
+  v = v + tam_dppd<TAM_DPP_MIRROR>(v);
   return v;
 }
-
-// NaN-propagating min / max (torch.min / torch.max semantics).
-__device__ __forceinline__ float tam_minp(float a, float b) {
-  if (tam_isnan(a)) return a;
-  if (tam_isnan(b)) return b;
-  return b < a ? b : a;
-}
-__device__ __forceinline__ float tam_maxp(float a, float b) {
-  if (tam_isnan(a)) return a;
-  if (tam_isnan(b)) return b;
-  return b > a ? b : a;
-}
-__device__ __forceinline__ float tam_block_min(float v) {
-  v = tam_minp(v, __shfl_xor(v, 1, 16));
-  v = tam_minp(v, __shfl_xor(v, 2, 16));
-  v = tam_minp(v, __shfl_xor(v, 4, 16));
-  v = tam_minp(v, __shfl_xor(v, 8, 16));
+__device__ __forceinline__ float tam_block_fmin(float v) {  // IEEE minNum; NaN tracked separately
+  v = __builtin_fminf(v, tam_dppf<TAM_DPP_XOR1>(v));
+  v = __builtin_fminf(v, tam_dppf<TAM_DPP_XOR2>(v));
+  v = __builtin_fminf(v, tam_dppf<TAM_DPP_HALF_MIRROR>(v));
+  v = __builtin_fminf(v, tam_dppf<TAM_DPP_MIRROR>(v));
   return v;
 }
-__device__ __forceinline__ float tam_block_max(float v) {
-  v = tam_maxp(v, __shfl_xor(v, 1, 16));
-  v = tam_maxp(v, __shfl_xor(v, 2, 16));
-  v = tam_maxp(v, __shfl_xor(v, 4, 16));
-  v = tam_maxp(v, __shfl_xor(v, 8, 16));
+__device__ __forceinline__ float tam_block_fmax(float v) {
+  v = __builtin_fmaxf(v, tam_dppf<TAM_DPP_XOR1>(v));
+  v = __builtin_fmaxf(v, tam_dppf<TAM_DPP_XOR2>(v));
+  v = __builtin_fmaxf(v, tam_dppf<TAM_DPP_HALF_MIRROR>(v));
+  v = __builtin_fmaxf(v, tam_dppf<TAM_DPP_MIRROR>(v));
+  return v;
+}
+__device__ __forceinline__ uint32_t tam_block_or(uint32_t v) {
+  v |= tam_dpp<TAM_DPP_XOR1>(v);
+  v |= tam_dpp<TAM_DPP_XOR2>(v);
+  v |= tam_dpp<TAM_DPP_HALF_MIRROR>(v);
+  v |= tam_dpp<TAM_DPP_MIRROR>(v);
   return v;
 }
 
 // ---------------------------------------------------------------------------
-// shared per-element pieces (identical in K1 and K3 so both see the same m)
+// shared per-element pieces (identical in pass 1 and pass 2 so both see the same m)
 // ---------------------------------------------------------------------------
 // CoState first moment of elements e0..e0+7 (reference costate.py:398-416):
 //   m_hat = has_state ? fl(fl(alpha*g) + s_b*sgn) : 0,  m = fl(fl(b1*m_hat) + fl(ob1*g))
@@ -204,8 +223,8 @@ __device__ __forceinline__ void tam_costate_m(const TamTensor& d, uint32_t b, ui
   for (int i = 0; i < TAM_EPL; ++i) {
     float mh = 0.0f;
     if (has) {
-      const float sgn = 1.0f - 2.0f * (float)((byte >> (7 - i)) & 1u);  // costate.py:207-209
-      mh = alpha_prev * g[i] + s * sgn;
+      const float sd = ((byte >> (7 - i)) & 1u) ? -s : s;  // s * (1 - 2*bit), costate.py:207-209, :317-319
+      mh = alpha_prev * g[i] + sd;
     }
     m[i] = d.beta1 * mh + d.one_minus_beta1 * g[i];
   }
@@ -213,8 +232,8 @@ __device__ __forceinline__ void tam_costate_m(const TamTensor& d, uint32_t b, ui
 
 // Block of a tile and element offset of this thread.
 struct TamLane {
-  uint32_t bl;     // block within the tile (0..15)
-  uint32_t l16;    // lane within the block (0..15)
+  uint32_t bl;   // block within the tile (0..15)
+  uint32_t l16;  // lane within the block (0..15)
 };
 
 __device__ __forceinline__ TamLane tam_lane() {
@@ -232,6 +251,220 @@ __device__ __forceinline__ int tam_find_tensor(const TamTensor* __restrict__ T, 
     if (T[mid].tile0 <= tile) lo = mid; else hi = mid - 1;
   }
   return lo;
+}
+
+// ---------------------------------------------------------------------------
+// 1Q second moment of one lane's 8 elements (reference quantize.py:222-299)
+// ---------------------------------------------------------------------------
+// Index of an element: with c = fl(fl(l - lmin)/sp) * 2^bits and u its
+// uniform, the reference computes floor(c) + (u < c - floor(c)) clamped to
+// [0, 2^bits - 1]; for real c and u in [0,1) that equals ceil(c - u).  The fast
+// path evaluates c from the hardware log2 (v_log_f32, whose error against the
+// correctly rounded ln is below 2^-21 |ln| for every normal input -- checked
+// exhaustively on gfx950) and accepts ceil(c~ - u) only when the whole error
+// interval [c~ - u - B, c~ - u + B] lies between the same integers (or clamps
+// to the same end); otherwise the element takes the exact path (correctly
+// rounded log and division).  lmin and lmax are the correctly rounded logs of
+// the block's smallest and largest v (log is monotone, so they equal the min
+// and max of the per-element logs).
+__device__ __forceinline__ void tam_vpath(const TamTensor& d, uint32_t b, bool bvalid, uint64_t e0,
+                                          const TamLane& L, const float* g, float* v, float (*lut)[64],
+                                          uint32_t seed_lo, uint32_t seed_hi) {
+  const uint32_t bits = d.v_bits;
+  const uint32_t nbk = 1u << bits;
+  const float fnb = (float)nbk;
+  const float inv_nbk = 1.0f / fnb;  // exact power of two
+  float lmin0 = 0.0f, span0 = 0.0f;
+  uint32_t iw0 = 0, iw1 = 0;
+  if (bvalid) {
+    const uint32_t sc = ((const uint32_t*)d.v_scales)[b];
+    lmin0 = tam_f16_to_f32((uint16_t)(sc & 0xffffu));
+    span0 = tam_f16_to_f32((uint16_t)(sc >> 16)) - lmin0;  // quantize.py:253-255
+    const uint2 iw = *(const uint2*)(d.v_idx + e0);
+    iw0 = iw.x;
+    iw1 = iw.y;
+  }
+  // decode (quantize.py:256): per-block table of the 2^bits values
+  float vo[TAM_EPL];
+  if (nbk <= 64u) {
+    if (bvalid) {
+      for (uint32_t k = L.l16; k < nbk; k += 16u) lut[L.bl][k] = tam_expf(lmin0 + ((float)k + 0.5f) * inv_nbk * span0);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < TAM_EPL; ++i) {
+      const uint32_t idx = ((i < 4 ? iw0 : iw1) >> (8 * (i & 3))) & 0xffu;
+      vo[i] = bvalid ? lut[L.bl][idx & 63u] : 0.0f;
+    }
+    __syncthreads();
+  } else {
+#pragma unroll
+    for (int i = 0; i < TAM_EPL; ++i) {
+      const uint32_t idx = ((i < 4 ? iw0 : iw1) >> (8 * (i & 3))) & 0xffu;
+      vo[i] = tam_expf(lmin0 + ((float)idx + 0.5f) * inv_nbk * span0);
+    }
+  }
+  // EMA (quantize.py:259-270) and the clamp of :275
+  float vc[TAM_EPL];
+  float vmn = tam_inf(), vmx = -tam_inf();
+  uint32_t nan_seen = 0;
+#pragma unroll
+  for (int i = 0; i < TAM_EPL; ++i) {
+    const bool valid = e0 + i < d.n;
+    const float g2 = valid ? g[i] * g[i] : 0.0f;
+    v[i] = __builtin_fmaf(d.one_minus_beta2, g2, vo[i] * d.beta2);
+    vc[i] = v[i] < 1e-38f ? 1e-38f : v[i];
+    if (valid && bvalid) {
+      nan_seen |= tam_isnan(vc[i]) ? 1u : 0u;
+      vmn = __builtin_fminf(vmn, vc[i]);
+      vmx = __builtin_fmaxf(vmx, vc[i]);
+    }
+  }
+  vmn = tam_block_fmin(vmn);
+  vmx = tam_block_fmax(vmx);
+  nan_seen = tam_block_or(nan_seen);
+  // correctly rounded logs of the extremes: even lanes log(vmin), odd lanes log(vmax)
+  const float lx = tam_logf((L.l16 & 1u) ? vmx : vmn);
+  const float ly = tam_dppf<TAM_DPP_XOR1>(lx);
+  float lmn = (L.l16 & 1u) ? ly : lx;
+  float lmx = (L.l16 & 1u) ? lx : ly;
+  if (nan_seen) lmn = lmx = tam_qnan();  // torch.min / torch.max propagate NaN
+  if (!bvalid) return;
+  float sp = lmx - lmn;  // quantize.py:283
+  sp = sp < 1e-10f ? 1e-10f : sp;
+  if (L.l16 == 0) {
+    ((uint32_t*)d.v_scales)[b] = (uint32_t)tam_f32_to_f16(lmn) | ((uint32_t)tam_f32_to_f16(lmx) << 16);
+  }
+  // certified stochastic rounding
+  const double dnb = (double)nbk;
+  const double inv_sp = 1.0 / (double)sp;
+  const double K = 0x1.62e42fefa39efp-1 * dnb * inv_sp;  // c~ = log2(v) * K + C
+  const double C = -(double)lmn * dnb * inv_sp;
+  const double K2 = K * (0x1p-21 + 0x1p-50);
+  const double Cerr = __builtin_fabs(C) * 0x1p-50 + 0x1p-40;
+  const uint64_t quad0 = e0 >> 2;
+  const TamU4 r0 = tam_philox_quad(quad0, d.tensor_id, d.step, seed_lo, seed_hi);
+  const TamU4 r1 = tam_philox_quad(quad0 + 1, d.tensor_id, d.step, seed_lo, seed_hi);
+  const uint32_t rw[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
+  uint32_t qb[TAM_EPL];
+  uint32_t amb = 0;
+#pragma unroll
+  for (int i = 0; i < TAM_EPL; ++i) {
+    const double ud = (double)(rw[i] >> 8) * 0x1p-24;
+    double q = 0.0;
+    bool ok = false;
+    if (vc[i] >= 0x1p-126f) {  // normal input (false for NaN)
+      const double l2 = (double)__builtin_amdgcn_logf(vc[i]);
+      const double ct = __builtin_fma(l2, K, C);
+      const double dd = ct - ud;
+      const double B = __builtin_fma(__builtin_fabs(l2), K2, __builtin_fma(__builtin_fabs(ct), 0x1p-22, Cerr));
+      const double ql = __builtin_ceil(dd - B);
+      ok = ql >= dd + B;  // no integer in (dd - B, dd + B): ceil is the same over the interval
+      q = ql;
+    }
+    amb |= ok ? 0u : (1u << i);
+    const int qi = (int)q;
+    qb[i] = (uint32_t)(qi < 0 ? 0 : (qi > (int)(nbk - 1) ? (int)(nbk - 1) : qi));
+  }
+  if (amb) {
+    // exact path: the reference's own sequence with correctly rounded log and division
+#pragma unroll
+    for (int i = 0; i < TAM_EPL; ++i) {
+      if (amb & (1u << i)) {
+        const float l = tam_logf(vc[i]);
+        const float c = ((l - lmn) / sp) * fnb;  // quantize.py:284-285
+        const float f = __builtin_floorf(c);
+        const float fr = c - f;
+        const float u = (float)(rw[i] >> 8) * 0x1p-24f;
+        float q = f + (u < fr ? 1.0f : 0.0f);  // quantize.py:288-294
+        q = q < 0.0f ? 0.0f : q;
+        q = q > fnb - 1.0f ? fnb - 1.0f : q;
+        qb[i] = tam_isnan(q) ? 0u : (uint32_t)q;
+      }
+    }
+  }
+  const uint32_t ow0 = qb[0] | (qb[1] << 8) | (qb[2] << 16) | (qb[3] << 24);
+  const uint32_t ow1 = qb[4] | (qb[5] << 8) | (qb[6] << 16) | (qb[7] << 24);
+  *(uint2*)(d.v_idx + e0) = make_uint2(ow0, ow1);
+}
+
+// ---------------------------------------------------------------------------
+// parameter update (reference optimizer.py:106-107, :163, :170)
+// ---------------------------------------------------------------------------
+// Exact sequence: q1 = fl(v/bc2), s = fl(sqrt(q1)), den = fl(s + eps),
+// t2 = fl(den*bc1), a = fl(-lr*m), upd = fl(a/t2), p = R_p(fl(p + upd)).
+// fp32 parameters: q1 comes from the fp64 reciprocal of bc2 when a rounding
+// test proves the fp32 rounding, else from the division.  bf16 / fp16
+// parameters: a fast sequence with the hardware rsq / rcp gives u~ with
+// |u~ - upd| <= 2^-19 |u~| + 2^-148 (the exact sequence's six roundings and
+// the fast sequence's five are each 2^-24 relative, both hardware seeds are
+// within 2^-23 -- checked exhaustively on gfx950).  With s~ = fl(p + u~),
+// fl(p + upd) lies within E = 2^-19 |u~| + 2^-22 |s~| + 2^-148 of s~, so
+// R_p(fl(p + upd)) is accepted when R_p(fl(s~ - E)) == R_p(fl(s~ + E)) (R_p and
+// fl are monotone); otherwise the exact sequence runs.  The result of a
+// 16-bit parameter is returned as its bit pattern in pb.
+__device__ __forceinline__ void tam_update(const TamTensor& d, uint32_t dtype, float* p, const float* m,
+                                           const float* v, uint16_t* pb) {
+  const bool wd = (d.flags & TAM_FLAG_WD) != 0;
+  if (dtype == TAM_DTYPE_F32) {
+#pragma unroll
+    for (int i = 0; i < TAM_EPL; ++i) {
+      const double y = (double)v[i] * d.inv_bc2;
+      const double e = __builtin_fabs(y) * 0x1p-51;
+      float q1 = (float)(y - e);
+      if (!(q1 == (float)(y + e))) q1 = v[i] / d.bias_correction2;
+      const float den = __builtin_sqrtf(q1) + d.eps;
+      const float pv = wd ? p[i] * d.c_wd : p[i];
+      p[i] = pv + (d.neg_lr * m[i]) / (den * d.bias_correction1);
+    }
+    return;
+  }
+  const bool bf = dtype == TAM_DTYPE_BF16;
+  uint32_t amb = 0;
+  float pw[TAM_EPL];
+#pragma unroll
+  for (int i = 0; i < TAM_EPL; ++i) {
+    pw[i] = wd ? tam_round_p(p[i] * d.c_wd, dtype) : p[i];
+    const float q = v[i] * d.inv_bc2_f32;
+    const float s = q * __builtin_amdgcn_rsqf(q);
+    const float t2 = (s + d.eps) * d.bias_correction1;
+    const float a = d.neg_lr * m[i];
+    const float u = a * __builtin_amdgcn_rcpf(t2);
+    const float st = pw[i] + u;
+    const float E = __builtin_fmaf(__builtin_fabsf(u), 0x1p-19f, __builtin_fmaf(__builtin_fabsf(st), 0x1p-22f, 0x1p-148f));
+    const float lo = st - E, hi = st + E;
+    // finite, normal hardware inputs and outputs; NaN fails every comparison
+    const bool ok0 = (q >= 0x1p-126f) && (t2 < 0x1p125f) && (__builtin_fabsf(st) < 0x1p126f);
+    const float lc = ok0 ? lo : 0.0f, hc = ok0 ? hi : 1.0f;
+    const uint16_t rl = bf ? tam_f32_to_bf16_rne(lc) : tam_f32_to_f16(lc);
+    const uint16_t rh = bf ? tam_f32_to_bf16_rne(hc) : tam_f32_to_f16(hc);
+    const bool ok = ok0 && rl == rh;
+    pb[i] = rl;
+    amb |= ok ? 0u : (1u << i);
+  }
+  if (amb) {
+#pragma unroll
+    for (int i = 0; i < TAM_EPL; ++i) {
+      if (amb & (1u << i)) {
+        const float den = __builtin_sqrtf(v[i] / d.bias_correction2) + d.eps;
+        pb[i] = tam_round16(pw[i] + (d.neg_lr * m[i]) / (den * d.bias_correction1), dtype);
+      }
+    }
+  }
+}
+
+// Stores 8 16-bit parameter patterns (elements [e0, e0+8), none beyond n).
+__device__ __forceinline__ void tam_store8_bits(void* base, uint64_t e0, uint64_t n, bool vec_ok, const uint16_t* b) {
+  if (vec_ok && e0 + TAM_EPL <= n) {
+    uint32_t w[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) w[k] = (uint32_t)b[2 * k] | ((uint32_t)b[2 * k + 1] << 16);
+    *(uint4*)((uint16_t*)base + e0) = make_uint4(w[0], w[1], w[2], w[3]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < TAM_EPL; ++i)
+      if (e0 + i < n) ((uint16_t*)base)[e0 + i] = b[i];
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -260,7 +493,7 @@ __global__ __launch_bounds__(TAM_WG) void tam_k1_main(const TamTensor* __restric
       tam_load8(d.param, dtype, e0, d.n, vec_p, p);
     } else {
 #pragma unroll
-      for (int i = 0; i < TAM_EPL; ++i) g[i] = p[i] = 0.0f;
+      for (int i = 0; i < TAM_EPL; ++i) g[i] = p[i] = m[i] = v[i] = 0.0f;
     }
 
     // ---- first moment ---------------------------------------------------
@@ -300,88 +533,7 @@ __global__ __launch_bounds__(TAM_WG) void tam_k1_main(const TamTensor* __restric
 
     // ---- second moment --------------------------------------------------
     if (d.flags & TAM_FLAG_COMPRESS_V) {
-      const uint32_t bits = d.v_bits;
-      const uint32_t nbk = 1u << bits;
-      const float inv_nbk = 1.0f / (float)nbk;  // exact power of two
-      float lmin = 0.0f, span = 0.0f;
-      uint32_t iw0 = 0, iw1 = 0;
-      if (bvalid) {
-        const uint32_t sc = ((const uint32_t*)d.v_scales)[b];
-        lmin = tam_f16_to_f32((uint16_t)(sc & 0xffffu));
-        const float lmax = tam_f16_to_f32((uint16_t)(sc >> 16));
-        span = lmax - lmin;  // quantize.py:253-255
-        const uint2 iw = *(const uint2*)(d.v_idx + e0);
-        iw0 = iw.x;
-        iw1 = iw.y;
-      }
-      float vo[TAM_EPL];
-      if (nbk <= 64u) {
-        // per-block table of the 2^bits decoded values (quantize.py:256)
-        if (bvalid) {
-          for (uint32_t k = L.l16; k < nbk; k += 16u) {
-            const float lv = lmin + ((float)k + 0.5f) * inv_nbk * span;
-            lut[L.bl][k] = tam_expf(lv);
-          }
-        }
-        __syncthreads();
-#pragma unroll
-        for (int i = 0; i < TAM_EPL; ++i) {
-          const uint32_t idx = ((i < 4 ? iw0 : iw1) >> (8 * (i & 3))) & 0xffu;
-          vo[i] = bvalid ? lut[L.bl][idx & 63u] : 0.0f;
-        }
-        __syncthreads();
-      } else {
-#pragma unroll
-        for (int i = 0; i < TAM_EPL; ++i) {
-          const uint32_t idx = ((i < 4 ? iw0 : iw1) >> (8 * (i & 3))) & 0xffu;
-          vo[i] = tam_expf(lmin + ((float)idx + 0.5f) * inv_nbk * span);
-        }
-      }
-      // EMA and log (quantize.py:259-275)
-      float lg[TAM_EPL];
-      float lmn = tam_inf(), lmx = -tam_inf();
-      const float clamp_min = 1e-38f;
-#pragma unroll
-      for (int i = 0; i < TAM_EPL; ++i) {
-        const bool valid = e0 + i < d.n;
-        const float g2 = valid ? g[i] * g[i] : 0.0f;
-        v[i] = __builtin_fmaf(d.one_minus_beta2, g2, vo[i] * d.beta2);
-        const float vc = v[i] < clamp_min ? clamp_min : v[i];
-        lg[i] = tam_logf(vc);
-        if (valid && bvalid) {
-          lmn = tam_minp(lmn, lg[i]);
-          lmx = tam_maxp(lmx, lg[i]);
-        }
-      }
-      lmn = tam_block_min(lmn);  // quantize.py:276-280
-      lmx = tam_block_max(lmx);
-      if (bvalid) {
-        float sp = lmx - lmn;  // quantize.py:283
-        sp = sp < 1e-10f ? 1e-10f : sp;
-        const float fnb = (float)nbk;
-        const uint64_t quad0 = e0 >> 2;
-        const TamU4 r0 = tam_philox_quad(quad0, d.tensor_id, d.step, seed_lo, seed_hi);
-        const TamU4 r1 = tam_philox_quad(quad0 + 1, d.tensor_id, d.step, seed_lo, seed_hi);
-        const uint32_t rw[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
-        uint32_t ow0 = 0, ow1 = 0;
-#pragma unroll
-        for (int i = 0; i < TAM_EPL; ++i) {
-          const float c = ((lg[i] - lmn) / sp) * fnb;  // quantize.py:284-285
-          const float f = __builtin_floorf(c);
-          const float fr = c - f;
-          const float u = tam_u01(rw[i]);
-          float q = f + (u < fr ? 1.0f : 0.0f);  // quantize.py:288-294
-          q = q < 0.0f ? 0.0f : q;
-          q = q > fnb - 1.0f ? fnb - 1.0f : q;
-          const uint32_t qi = tam_isnan(q) ? 0u : (uint32_t)q;
-          if (i < 4) ow0 |= qi << (8 * i); else ow1 |= qi << (8 * (i - 4));
-        }
-        *(uint2*)(d.v_idx + e0) = make_uint2(ow0, ow1);
-        if (L.l16 == 0) {
-          const uint32_t sc = (uint32_t)tam_f32_to_f16(lmn) | ((uint32_t)tam_f32_to_f16(lmx) << 16);
-          ((uint32_t*)d.v_scales)[b] = sc;
-        }
-      }
+      tam_vpath(d, b, bvalid, e0, L, g, v, lut, seed_lo, seed_hi);
     } else if (bvalid) {
       // fp32 exp_avg_sq (optimizer.py:166): v = fma(fl((1-b2)*g), g, fl(v*b2))
       float es[TAM_EPL];
@@ -391,22 +543,15 @@ __global__ __launch_bounds__(TAM_WG) void tam_k1_main(const TamTensor* __restric
       tam_store8_f32(d.exp_avg_sq, e0, d.n, v);
     }
 
-    // ---- parameter update (optimizer.py:106-107, :163, :170) -------------
+    // ---- parameter update -----------------------------------------------
     if (bvalid) {
-      const bool wd = (d.flags & TAM_FLAG_WD) != 0;
-#pragma unroll
-      for (int i = 0; i < TAM_EPL; ++i) {
-        const float den = __builtin_sqrtf(v[i] / d.bias_correction2) + d.eps;
-        float pv = p[i];
-        if (wd) pv = tam_round_p(pv * d.c_wd, dtype);
-        const float upd = (d.neg_lr * m[i]) / (den * d.bias_correction1);
-        p[i] = pv + upd;
-      }
-      tam_store8(d.param, dtype, e0, d.n, vec_p, p);
+      uint16_t pb[TAM_EPL];
+      tam_update(d, dtype, p, m, v, pb);
+      if (dtype == TAM_DTYPE_F32) tam_store8(d.param, dtype, e0, d.n, vec_p, p);
+      else tam_store8_bits(d.param, e0, d.n, vec_p, pb);
     }
   }
 }
-
 
 // ---------------------------------------------------------------------------
 // K2: alpha of every CoState tensor (costate.py:37-41)
@@ -447,16 +592,22 @@ __device__ double2 tam_wg_pairwise2(const double2* __restrict__ x, uint32_t coun
     if (tid == 0) chunks[c] = sh[0];
     __syncthreads();
   }
-  for (uint32_t w = nchunks / 2; w >= 1; w >>= 1) {
+  for (uint32_t w = nchunks / 2; w >= 1; w >>= 1) {  // w <= 1024: at most 4 pairs per thread
     double2 s[4];
-    int cnt = 0;
-    for (uint32_t i = tid; i < w; i += TAM_WG) {
-      const double2 l = chunks[2 * i], r = chunks[2 * i + 1];
-      s[cnt++] = make_double2(l.x + r.x, l.y + r.y);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t i = tid + j * TAM_WG;
+      if (i < w) {
+        const double2 l = chunks[2 * i], r = chunks[2 * i + 1];
+        s[j] = make_double2(l.x + r.x, l.y + r.y);
+      }
     }
     __syncthreads();
-    cnt = 0;
-    for (uint32_t i = tid; i < w; i += TAM_WG) chunks[i] = s[cnt++];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t i = tid + j * TAM_WG;
+      if (i < w) chunks[i] = s[j];
+    }
     __syncthreads();
   }
   return chunks[0];
@@ -534,6 +685,12 @@ __global__ __launch_bounds__(TAM_WG) void tam_k2_encode(const TamTensor* __restr
 // K4: order statistics of the ratios (costate.py:114-118), labels
 // (costate.py:146-148), alpha write-back (costate.py:443-454)
 // ---------------------------------------------------------------------------
+// Ratios are >= +0 or NaN, so their fp32 bit patterns order like torch.sort
+// (NaN last).  The selection is an MSD radix select on those patterns: a
+// min/max pass finds the bits all keys share, then 11-bit digits below the
+// highest differing bit are histogrammed in LDS (keys of similar magnitude
+// spread over the bins instead of piling into a few), at most three passes.
+
 // Exclusive prefix sum over the 1024 threads of the workgroup.
 __device__ uint32_t tam_wg_excl_scan(uint32_t v, uint32_t* wsum) {
   const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
@@ -559,6 +716,43 @@ __device__ uint32_t tam_wg_excl_scan(uint32_t v, uint32_t* wsum) {
   return r;
 }
 
+__device__ uint32_t tam_wg_reduce_u32(uint32_t v, bool is_max, uint32_t* wsum) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const uint32_t t = __shfl_xor(v, off);
+    v = is_max ? (t > v ? t : v) : (t < v ? t : v);
+  }
+  if ((threadIdx.x & 63u) == 0) wsum[threadIdx.x >> 6] = v;
+  __syncthreads();
+  uint32_t r = wsum[0];
+  for (int i = 1; i < TAM_SEL_WG / 64; ++i) r = is_max ? (wsum[i] > r ? wsum[i] : r) : (wsum[i] < r ? wsum[i] : r);
+  __syncthreads();
+  return r;
+}
+
+// Visits every key of a tensor: 16 keys per thread in flight (four uint4
+// loads), then the < 4 trailing keys.  `keys` is 16-byte aligned.
+template <typename F>
+__device__ __forceinline__ void tam_for_keys(const uint32_t* __restrict__ keys, uint32_t nb, F&& f) {
+  const uint4* k4 = (const uint4*)keys;
+  const uint32_t n4 = nb >> 2;
+  const uint32_t stride = TAM_SEL_WG;
+  uint32_t i = threadIdx.x;
+  for (; i + 3 * stride < n4; i += 4 * stride) {
+    const uint4 a = k4[i], b = k4[i + stride], c = k4[i + 2 * stride], e = k4[i + 3 * stride];
+    f(a.x); f(a.y); f(a.z); f(a.w);
+    f(b.x); f(b.y); f(b.z); f(b.w);
+    f(c.x); f(c.y); f(c.z); f(c.w);
+    f(e.x); f(e.y); f(e.z); f(e.w);
+  }
+  for (; i < n4; i += stride) {
+    const uint4 a = k4[i];
+    f(a.x); f(a.y); f(a.z); f(a.w);
+  }
+  const uint32_t t = (n4 << 2) + threadIdx.x;
+  if (t < nb) f(keys[t]);
+}
+
 __global__ __launch_bounds__(TAM_SEL_WG) void tam_k3_select(const TamTensor* __restrict__ T,
                                                             const float* __restrict__ alpha_new,
                                                             const float* __restrict__ ratios) {
@@ -570,29 +764,41 @@ __global__ __launch_bounds__(TAM_SEL_WG) void tam_k3_select(const TamTensor* __r
   const uint32_t nb = d.nb;
   const uint32_t* keys = (const uint32_t*)(ratios + d.ratio_off);
   const uint32_t tid = threadIdx.x;
+  uint32_t kmin = 0xffffffffu, kmax = 0u;
+  tam_for_keys(keys, nb, [&](uint32_t k) {
+    kmin = k < kmin ? k : kmin;
+    kmax = k > kmax ? k : kmax;
+  });
+  kmin = tam_wg_reduce_u32(kmin, false, wsum);
+  kmax = tam_wg_reduce_u32(kmax, true, wsum);
   if (tid == 0) {
-    sel_prefix[0] = sel_prefix[1] = 0;
+    sel_prefix[0] = sel_prefix[1] = kmin;  // bits above the highest differing bit
     sel_k[0] = d.k_lo;
     sel_k[1] = d.k_hi;
   }
-  uint32_t mask = 0;
-  const int shifts[3] = {21, 10, 0};
-  const uint32_t widths[3] = {11, 11, 10};
-  for (int pass = 0; pass < 3; ++pass) {
-    const int sh = shifts[pass];
-    const uint32_t dmask = (1u << widths[pass]) - 1u;
+  __syncthreads();
+  const uint32_t diff = kmin ^ kmax;
+  int top = diff ? 31 - __builtin_clz(diff) : -1;  // highest differing bit
+  uint32_t mask = top >= 31 ? 0u : (0xffffffffu << (top + 1));
+  if (top >= 0 && tid == 0) sel_prefix[0] = sel_prefix[1] = kmin & mask;
+  __syncthreads();
+  while (top >= 0) {
+    const int sh = top >= 10 ? top - 10 : 0;
+    const uint32_t dmask = (1u << (top - sh + 1)) - 1u;
     for (uint32_t i = tid; i < 2048; i += TAM_SEL_WG) hist[0][i] = hist[1][i] = 0;
     __syncthreads();
     const uint32_t p0 = sel_prefix[0], p1 = sel_prefix[1];
-    for (uint32_t i = tid; i < nb; i += TAM_SEL_WG) {
-      const uint32_t key = keys[i];
+    const bool same = p0 == p1;
+    tam_for_keys(keys, nb, [&](uint32_t key) {
       const uint32_t dg = (key >> sh) & dmask;
-      if ((key & mask) == p0) atomicAdd(&hist[0][dg], 1u);
-      if ((key & mask) == p1) atomicAdd(&hist[1][dg], 1u);
-    }
+      const uint32_t km = key & mask;
+      if (km == p0) atomicAdd(&hist[0][dg], 1u);
+      if (!same && km == p1) atomicAdd(&hist[1][dg], 1u);
+    });
     __syncthreads();
     for (int t = 0; t < 2; ++t) {
-      const uint32_t h0 = hist[t][2 * tid], h1 = hist[t][2 * tid + 1];
+      const int src = same ? 0 : t;
+      const uint32_t h0 = hist[src][2 * tid], h1 = hist[src][2 * tid + 1];
       const uint32_t pre = tam_wg_excl_scan(h0 + h1, wsum);
       const uint32_t k = sel_k[t];
       __syncthreads();
@@ -605,6 +811,7 @@ __global__ __launch_bounds__(TAM_SEL_WG) void tam_k3_select(const TamTensor* __r
       __syncthreads();
     }
     mask |= dmask << sh;
+    top = sh - 1;
   }
   const float tau0 = tam_u2f(sel_prefix[0]);
   const float tau1 = tam_u2f(sel_prefix[1]);
@@ -652,6 +859,7 @@ __global__ void tam_k_math_eval(int fn, const float* __restrict__ in, float* __r
     case 2: y = tam_f16_to_f32(tam_f32_to_f16(x)); break;
     case 3: y = tam_bf16_to_f32(tam_f32_to_bf16(x)); break;
     case 4: y = __builtin_sqrtf(x); break;
+    case 5: y = tam_bf16_to_f32(tam_f32_to_bf16_rne(x)); break;
     default: y = x; break;
   }
   out[i] = y;
@@ -714,7 +922,7 @@ int tam_prepare(TamTensor* tensors, int n_tensors, TamStepInfo* info) {
         return tam_fail(TAM_E_INVALID, "%stensor %ld: null CoState state", "", i);
       if (t.k_lo >= nb || t.k_hi >= nb) return tam_fail(TAM_E_INVALID, "%stensor %ld: rank out of range", "", i);
       t.ratio_off = ratio_blocks;
-      ratio_blocks += nb;
+      ratio_blocks += (nb + 3) & ~3ull;  // 16-byte aligned per tensor
       ++ncs;
     } else if (!t.exp_avg || ((uintptr_t)t.exp_avg & 15u)) {
       return tam_fail(TAM_E_INVALID, "%stensor %ld: exp_avg null or misaligned", "", i);
@@ -823,7 +1031,7 @@ int tam_philox_uniforms(uint32_t tensor_id, uint32_t step, uint64_t seed, uint64
 int tam_math_eval(int fn, const float* in, float* out, uint64_t n, void* stream) {
   tam_err_buf[0] = 0;
   if (!in || !out) return tam_fail(TAM_E_INVALID, "%snull argument", "");
-  if (fn < 0 || fn > 4) return tam_fail(TAM_E_INVALID, "%sunknown function %ld", "", fn);
+  if (fn < 0 || fn > 5) return tam_fail(TAM_E_INVALID, "%sunknown function %ld", "", fn);
   if (n == 0) return TAM_OK;
   const uint64_t blocks = (n + 255) / 256;
   hipLaunchKernelGGL(tam_k_math_eval, dim3((uint32_t)blocks), dim3(256), 0, (hipStream_t)stream, fn, in, out, n);

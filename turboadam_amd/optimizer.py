@@ -327,6 +327,8 @@ class TurboAdam(Optimizer):
         t.one_minus_beta2 = _f32(1.0 - beta2)
         t.bias_correction1 = _f32(bc1)
         t.bias_correction2 = _f32(bc2)
+        t.inv_bc2 = 1.0 / t.bias_correction2
+        t.inv_bc2_f32 = _f32(t.inv_bc2)
         t.eps = _f32(group["eps"])
         t.neg_lr = _f32(-lr)
         t.sqrt_block = _f32(math.sqrt(BLOCK_SIZE))
