@@ -8,8 +8,8 @@ BASELINE.json): the Llama-3-8B-shaped parameter set (291 tensors,
 8,030,261,248 parameters) in bf16, m+v compression, v_bits=4.  Prints one
 JSON line with throughput (parameters updated per second), the roofline of
 the dominant kernel (pass 1) timed live with HIP events on the launch stream,
-and a CPU baseline: the CPU oracle (a scalar restatement of the reference's
-CPU step) timed on a bounded sample on this host.
+and a CPU baseline: the reference's CPU step (restated op for op in torch,
+oracle/torch_mirror.py) timed on a bounded sample on this host.
 """
 
 import argparse
@@ -100,45 +100,62 @@ def bytes_per_param(dtype_bytes: int, costate: bool, compress_v: bool = True):
 
 
 # ---------------------------------------------------------------- CPU baseline
-def cpu_baseline(shapes, dtype, kw, log_sigma, budget_s=12.0):
-    """Time the CPU oracle on a bounded sample of the workload's tensors."""
-    from oracle import oracle as O
+def cpu_baseline(shapes, dtype, kw, log_sigma, budget_s=20.0):
+    """Time the reference's CPU step on a bounded sample of the workload.
 
-    dt = {torch.float32: O.DT_F32, torch.bfloat16: O.DT_BF16, torch.float16: O.DT_F16}[dtype]
-    rng = np.random.default_rng(7)
-    # sample: tensors in workload order until ~24M parameters
+    Runs oracle/torch_mirror.py in faithful mode -- the reference CPU path
+    restated op for op in torch (it reproduces the reference's outputs bit for
+    bit, tests/test_golden.py) -- on the host cores, with the same parameter
+    shapes and dtype, on the workload's tensors in order (skipping any above
+    20M parameters) until about 20M parameters.
+    """
+    from oracle import torch_mirror as TM
+
+    threads = max(1, min(16, os.cpu_count() or 1))
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    gen = torch.Generator().manual_seed(7)
     sample, total = [], 0
     for name, shp in shapes:
         n = int(np.prod(shp))
-        if n > 20_000_000 and sample:
+        if n > 20_000_000:
             continue
-        sample.append((name, n))
+        sample.append((name, shp))
         total += n
         if total >= 20_000_000:
             break
-
-    def enc(x):
-        x = x.astype(np.float32)
-        if dt == O.DT_F32:
-            return x
-        return torch.from_numpy(x).to(dtype).view(torch.int16).numpy().view(np.uint16).copy()
-
-    params = [enc(rng.standard_normal(n) * 0.02) for _, n in sample]
-    opt = O.OracleTurboAdam(params, dtypes=[dt] * len(params), seed=1, **kw)
+    params = [(torch.randn(shp, generator=gen) * 0.02).to(dtype) for _, shp in sample]
+    opt = TM.MirrorTurboAdam(params, ops=TM.FaithfulOps, seed=1, **kw)
     times = []
     t_end = time.perf_counter() + budget_s
-    while time.perf_counter() < t_end or len(times) < 2:
-        grads = [enc(rng.standard_normal(n) * math.exp(log_sigma)) for _, n in sample]
+    while len(times) < 2 or (time.perf_counter() < t_end and len(times) < 6):
+        grads = [(torch.randn(p.shape, generator=gen) * math.exp(log_sigma)).to(dtype) for p in params]
         t0 = time.perf_counter()
         opt.step(grads)
         times.append(time.perf_counter() - t0)
-        if len(times) >= 5:
-            break
-    steady = times[1:] if len(times) > 1 else times
-    t = float(np.median(steady))
-    return {"value": total / t, "unit": "params/s", "cores": 1, "kind": "port",
-            "sample": f"{len(sample)} tensors ({total} params: {', '.join(n for n, _ in sample[:4])}...) of the "
-                      f"same workload, {len(times)} steps, median of steps 2+; scalar C oracle, 1 thread"}
+    torch.set_num_threads(prev)
+    t = float(np.median(times[1:]))
+    names = ", ".join(n for n, _ in sample[:4])
+    return {"value": total / t, "unit": "params/s", "cores": threads, "kind": "port",
+            "sample": f"{len(sample)} tensors of the workload ({names}; {total} params, {str(dtype)[6:]}), "
+                      f"{len(times)} steps, median of steps 2+; reference CPU step restated in torch ops "
+                      f"(faithful mirror, bit-identical to the reference), {threads} threads"}
+
+
+# ---------------------------------------------------------------- HBM traffic
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "tam_k1_main_c3_fetch_write.md")
+
+
+def measured_traffic(workload: str):
+    """HBM bytes per pass-1 launch from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary (counters scaled by their plain-copy calibration), or
+    None when no summary covers this workload."""
+    if workload != "c3" or not os.path.exists(TRAFFIC_PROFILE):
+        return None
+    for line in open(TRAFFIC_PROFILE):
+        if line.startswith("traffic_bytes_per_launch"):
+            return float(line.split("=")[1])
+    return None
 
 
 # ---------------------------------------------------------------- copy reference
@@ -286,7 +303,8 @@ def main():
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": k1_gbps / HBM_PEAK_GBPS,
-            "traffic": None,
+            "traffic": measured_traffic(args.workload),
+            "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE x2.0 + WRITE_SIZE x1.0)",
             "ms_per_launch": k1_avg,
             "bytes_alg_per_launch": k1_bytes,
         },

@@ -150,7 +150,8 @@ int tam_philox_uniforms(uint32_t tensor_id, uint32_t step, uint64_t seed,
                         uint64_t count, float* out, void* stream);
 
 /* Self-check of the device arithmetic: out[i] = f(in[i]) with f selected by
- * `fn` (0 log, 1 exp, 2 f32->f16->f32, 3 f32->bf16->f32).  No counterpart in
+ * `fn` (0 log, 1 exp, 2 f32->f16->f32, 3 f32->bf16->f32 in software, 4 sqrt,
+ * 5 f32->bf16->f32 by the hardware conversion).  No counterpart in
  * the reference: it lets a caller confirm the device math equals the host. */
 int tam_math_eval(int fn, const float* in, float* out, uint64_t n, void* stream);
 
