@@ -69,7 +69,7 @@ def test_prepare_layout():
     assert info.total_tiles == 21 and info.n_costate == 2 and info.ratio_blocks == 40 + 260
     assert arr[0].ratio_off == 0 and arr[2].ratio_off == 40
     assert info.off_partials == 0
-    assert info.off_alpha >= 21 * 16 and info.off_ratios >= info.off_alpha + 3 * 4
+    assert info.off_alpha >= 21 * 4 * 16 and info.off_ratios >= info.off_alpha + 3 * 4
     assert info.ws_bytes >= info.off_ratios + 300 * 4
     assert info.off_alpha % 256 == 0 and info.off_ratios % 256 == 0
 

@@ -6,8 +6,9 @@
 // consecutive blocks (2048 elements) of one tensor, aligned on 16-block
 // boundaries inside the tensor.  A 256-thread workgroup processes one tile
 // at a time: thread t owns elements [8t, 8t+8) of the tile, so the 16 lanes
-// t = 16k..16k+15 of one wave64 own block k of the tile.  Tiles of all
-// tensors are numbered consecutively (tensor i owns tiles
+// t = 16k..16k+15 of one wave64 own block k of the tile and each wave owns a
+// quarter tile (4 blocks); the waves never synchronise with each other.
+// Tiles of all tensors are numbered consecutively (tensor i owns tiles
 // [tile0_i, tile0_i + ntiles_i)) and persistent workgroups stride over them,
 // so one launch covers the whole parameter list.
 //
@@ -15,7 +16,8 @@
 //   K1 tam_k1_main    every tile: CoState decode + EMA (or fp32 exp_avg EMA),
 //                     1Q decode + EMA + stochastic re-quantisation (or fp32
 //                     exp_avg_sq), denominator, decoupled weight decay,
-//                     parameter update; per-tile fp64 partials of g.g, m.g.
+//                     parameter update; per-quarter-tile fp64 partials of
+//                     g.g, m.g.
 //   K2 tam_k_alpha    one workgroup per CoState tensor: alpha = m.g / g.g.
 //   K3 tam_k2_encode  CoState tiles: recompute m, delta = m - alpha*g, sign
 //                     bits, block norms, fp16 amplitudes, block ratios.
@@ -54,90 +56,107 @@ static int tam_fail(int code, const char* fmt, const char* a = "", long b = 0) {
   } while (0)
 
 // ---------------------------------------------------------------------------
-// element loads / stores (8 consecutive elements per lane)
+// global-memory access
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float tam_load_scalar(const void* base, uint32_t dtype, uint64_t i) {
-  if (dtype == TAM_DTYPE_F32) return ((const float*)base)[i];
-  const uint16_t h = ((const uint16_t*)base)[i];
-  return dtype == TAM_DTYPE_BF16 ? tam_bf16_to_f32(h) : tam_f16_to_f32(h);
+// Device pointers read from a TamTensor are generic (flat) pointers; casting
+// them to the global address space lets the compiler emit global_load /
+// global_store, which wait on the vector-memory counter only (flat accesses
+// also hold the LDS counter, so every LDS wait would wait on them as well).
+#define TAM_GLOBAL __attribute__((address_space(1)))
+typedef float TamF4 __attribute__((ext_vector_type(4)));
+typedef uint32_t TamW4 __attribute__((ext_vector_type(4)));
+typedef uint32_t TamW2 __attribute__((ext_vector_type(2)));
+typedef double TamD2 __attribute__((ext_vector_type(2)));
+template <typename T>
+__device__ __forceinline__ TAM_GLOBAL T* tam_g(T* p) {
+  return (TAM_GLOBAL T*)p;
+}
+template <typename T>
+__device__ __forceinline__ const TAM_GLOBAL T* tam_g(const T* p) {
+  return (const TAM_GLOBAL T*)p;
 }
 
-__device__ __forceinline__ void tam_unpack8_16(uint4 w, uint32_t dtype, float* out) {
-  const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const uint16_t lo = (uint16_t)(ws[k] & 0xffffu), hi = (uint16_t)(ws[k] >> 16);
-    if (dtype == TAM_DTYPE_BF16) {
-      out[2 * k] = tam_bf16_to_f32(lo);
-      out[2 * k + 1] = tam_bf16_to_f32(hi);
-    } else {
-      out[2 * k] = tam_f16_to_f32(lo);
-      out[2 * k + 1] = tam_f16_to_f32(hi);
-    }
-  }
+// 16-bit element bits -> fp32 (exact)
+template <uint32_t DT>
+__device__ __forceinline__ float tam_h2f(uint32_t h) {
+  return DT == TAM_DTYPE_BF16 ? tam_u2f(h << 16) : tam_f16_to_f32((uint16_t)h);
 }
 
-// Loads elements [e0, e0+8) (zero beyond n).
-__device__ __forceinline__ void tam_load8(const void* base, uint32_t dtype, uint64_t e0, uint64_t n,
-                                          bool vec_ok, float* out) {
-  if (vec_ok && e0 + TAM_EPL <= n) {
-    if (dtype == TAM_DTYPE_F32) {
-      const float4* p = (const float4*)((const float*)base + e0);
-      const float4 a = p[0], b = p[1];
+// Rounds to the parameter dtype (round to nearest even); NaN gives a quiet NaN.
+template <uint32_t DT>
+__device__ __forceinline__ uint16_t tam_round16_hw(float x) {
+  return DT == TAM_DTYPE_BF16 ? tam_f32_to_bf16_rne(x) : tam_f32_to_f16(x);
+}
+
+// Elements [e0, e0+8) of a parameter or gradient.  FULL: all 8 exist and the
+// array is 16-byte aligned; otherwise only the first nv exist (the rest read 0).
+template <uint32_t DT, bool FULL>
+__device__ __forceinline__ void tam_ld8(const void* base, uint64_t e0, uint32_t nv, float* out) {
+  if (DT == TAM_DTYPE_F32) {
+    const float* b = (const float*)base + e0;
+    if (FULL) {
+      const TamF4 a = tam_g((const TamF4*)b)[0], c = tam_g((const TamF4*)b)[1];
       out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
-      out[4] = b.x; out[5] = b.y; out[6] = b.z; out[7] = b.w;
+      out[4] = c.x; out[5] = c.y; out[6] = c.z; out[7] = c.w;
     } else {
-      const uint4 w = *(const uint4*)((const uint16_t*)base + e0);
-      tam_unpack8_16(w, dtype, out);
+#pragma unroll
+      for (int i = 0; i < TAM_EPL; ++i) out[i] = (uint32_t)i < nv ? tam_g(b)[i] : 0.0f;
     }
   } else {
+    const uint16_t* b = (const uint16_t*)base + e0;
+    if (FULL) {
+      const TamW4 w = tam_g((const TamW4*)b)[0];
+      const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-    for (int i = 0; i < TAM_EPL; ++i) out[i] = (e0 + i < n) ? tam_load_scalar(base, dtype, e0 + i) : 0.0f;
+      for (int k = 0; k < 4; ++k) {
+        out[2 * k] = tam_h2f<DT>(ws[k] & 0xffffu);
+        out[2 * k + 1] = tam_h2f<DT>(ws[k] >> 16);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < TAM_EPL; ++i) out[i] = (uint32_t)i < nv ? tam_h2f<DT>(tam_g(b)[i]) : 0.0f;
+    }
   }
 }
 
+// fp32 state arrays (exp_avg / exp_avg_sq, 16-byte aligned)
+template <bool FULL>
+__device__ __forceinline__ void tam_ld8_f32(const float* base, uint64_t e0, uint32_t nv, float* out) {
+  tam_ld8<TAM_DTYPE_F32, FULL>(base, e0, nv, out);
+}
+template <bool FULL>
+__device__ __forceinline__ void tam_st8_f32(float* base, uint64_t e0, uint32_t nv, const float* v) {
+  float* b = base + e0;
+  if (FULL) {
+    tam_g((TamF4*)b)[0] = TamF4{v[0], v[1], v[2], v[3]};
+    tam_g((TamF4*)b)[1] = TamF4{v[4], v[5], v[6], v[7]};
+  } else {
+#pragma unroll
+    for (int i = 0; i < TAM_EPL; ++i)
+      if ((uint32_t)i < nv) tam_g(b)[i] = v[i];
+  }
+}
+
+// 16-bit parameter bit patterns
+template <bool FULL>
+__device__ __forceinline__ void tam_st8_bits(void* base, uint64_t e0, uint32_t nv, const uint16_t* pb) {
+  uint16_t* b = (uint16_t*)base + e0;
+  if (FULL) {
+    uint32_t w[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) w[k] = (uint32_t)pb[2 * k] | ((uint32_t)pb[2 * k + 1] << 16);
+    tam_g((TamW4*)b)[0] = TamW4{w[0], w[1], w[2], w[3]};
+  } else {
+#pragma unroll
+    for (int i = 0; i < TAM_EPL; ++i)
+      if ((uint32_t)i < nv) tam_g(b)[i] = pb[i];
+  }
+}
+
+// Rounds a value to a 16-bit parameter dtype (software round to nearest even,
+// NaN -> canonical quiet NaN, as torch's conversion).
 __device__ __forceinline__ uint16_t tam_round16(float x, uint32_t dtype) {
   return dtype == TAM_DTYPE_BF16 ? tam_f32_to_bf16(x) : tam_f32_to_f16(x);
-}
-
-// Rounds a value to the parameter dtype and back (R_p).
-__device__ __forceinline__ float tam_round_p(float x, uint32_t dtype) {
-  if (dtype == TAM_DTYPE_F32) return x;
-  if (dtype == TAM_DTYPE_BF16) return tam_bf16_to_f32(tam_f32_to_bf16(x));
-  return tam_f16_to_f32(tam_f32_to_f16(x));
-}
-
-__device__ __forceinline__ void tam_store8(void* base, uint32_t dtype, uint64_t e0, uint64_t n, bool vec_ok,
-                                           const float* v) {
-  if (vec_ok && e0 + TAM_EPL <= n) {
-    if (dtype == TAM_DTYPE_F32) {
-      float4* p = (float4*)((float*)base + e0);
-      p[0] = make_float4(v[0], v[1], v[2], v[3]);
-      p[1] = make_float4(v[4], v[5], v[6], v[7]);
-    } else {
-      uint32_t w[4];
-#pragma unroll
-      for (int k = 0; k < 4; ++k)
-        w[k] = (uint32_t)tam_round16(v[2 * k], dtype) | ((uint32_t)tam_round16(v[2 * k + 1], dtype) << 16);
-      *(uint4*)((uint16_t*)base + e0) = make_uint4(w[0], w[1], w[2], w[3]);
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < TAM_EPL; ++i) {
-      if (e0 + i < n) {
-        if (dtype == TAM_DTYPE_F32) ((float*)base)[e0 + i] = v[i];
-        else ((uint16_t*)base)[e0 + i] = tam_round16(v[i], dtype);
-      }
-    }
-  }
-}
-
-// fp32 loads/stores of state arrays that may have a ragged end.
-__device__ __forceinline__ void tam_load8_f32(const float* base, uint64_t e0, uint64_t n, float* out) {
-  tam_load8(base, TAM_DTYPE_F32, e0, n, true, out);
-}
-__device__ __forceinline__ void tam_store8_f32(float* base, uint64_t e0, uint64_t n, const float* v) {
-  tam_store8(base, TAM_DTYPE_F32, e0, n, true, v);
 }
 
 // ---------------------------------------------------------------------------
@@ -203,106 +222,150 @@ __device__ __forceinline__ uint32_t tam_block_or(uint32_t v) {
   return v;
 }
 
-// ---------------------------------------------------------------------------
-// shared per-element pieces (identical in pass 1 and pass 2 so both see the same m)
-// ---------------------------------------------------------------------------
-// CoState first moment of elements e0..e0+7 (reference costate.py:398-416):
-//   m_hat = has_state ? fl(fl(alpha*g) + s_b*sgn) : 0,  m = fl(fl(b1*m_hat) + fl(ob1*g))
-__device__ __forceinline__ void tam_costate_m(const TamTensor& d, uint32_t b, uint64_t e0, float alpha_prev,
-                                              const float* g, float* m) {
-  const bool has = (d.flags & TAM_FLAG_HAS_STATE) != 0;
-  float s = 0.0f;
-  uint32_t byte = 0;
-  if (has) {
-    const uint32_t label = d.labels[b];
-    if (label == 1u) s = d.norms[b] / d.sqrt_block;  // costate.py:306 (true division)
-    else if (label == 2u) s = tam_f16_to_f32(d.amp[b]);
-    if (e0 < d.n) byte = d.signs[e0 >> 3];
-  }
-#pragma unroll
-  for (int i = 0; i < TAM_EPL; ++i) {
-    float mh = 0.0f;
-    if (has) {
-      const float sd = ((byte >> (7 - i)) & 1u) ? -s : s;  // s * (1 - 2*bit), costate.py:207-209, :317-319
-      mh = alpha_prev * g[i] + sd;
-    }
-    m[i] = d.beta1 * mh + d.one_minus_beta1 * g[i];
-  }
+// Orders this wave's LDS accesses before and after the call (LDS operations of
+// one wave execute in order, so no s_barrier is needed between lanes of a wave).
+__device__ __forceinline__ void tam_wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Block of a tile and element offset of this thread.
-struct TamLane {
-  uint32_t bl;   // block within the tile (0..15)
-  uint32_t l16;  // lane within the block (0..15)
+// ---------------------------------------------------------------------------
+// one wave's share of a tile
+// ---------------------------------------------------------------------------
+// A wave owns 4 consecutive blocks (512 elements) of a tile: lane l holds
+// elements [8*(l%16), 8*(l%16)+8) of block 4*wq + l/16 of its tensor, where wq
+// is the wave's quarter-tile index within the tensor.  `full` quarters lie
+// entirely inside the tensor (and its arrays are 16-byte aligned): no
+// per-element bounds.  Other quarters check every element against n.
+struct TamWave {
+  uint32_t lane;  // 0..63
+  uint32_t l16;   // lane within the block
+  uint32_t b;     // block within the tensor
+  uint64_t e0;    // first element of the lane
+  uint32_t nv;    // elements of the lane inside the tensor (0..8)
+  bool bvalid;    // block b exists (b < nb)
 };
 
-__device__ __forceinline__ TamLane tam_lane() {
-  TamLane L;
-  L.bl = threadIdx.x >> 4;
-  L.l16 = threadIdx.x & 15u;
-  return L;
-}
-
-// Tensor owning global tile `tile` (binary search over tile0).
-__device__ __forceinline__ int tam_find_tensor(const TamTensor* __restrict__ T, int nT, uint32_t tile) {
-  int lo = 0, hi = nT - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (T[mid].tile0 <= tile) lo = mid; else hi = mid - 1;
+__device__ __forceinline__ TamWave tam_wave(const TamTensor& d, uint32_t wq, uint32_t lane, bool full) {
+  TamWave W;
+  W.lane = lane;
+  W.l16 = lane & 15u;
+  W.b = wq * 4u + (lane >> 4);
+  W.e0 = (uint64_t)W.b * TAM_BLOCK_SIZE + W.l16 * TAM_EPL;
+  if (full) {
+    W.nv = TAM_EPL;
+    W.bvalid = true;
+  } else {
+    const uint64_t n = d.n;
+    W.nv = W.e0 >= n ? 0u : (n - W.e0 >= TAM_EPL ? (uint32_t)TAM_EPL : (uint32_t)(n - W.e0));
+    W.bvalid = W.b < d.nb;
   }
-  return lo;
+  return W;
 }
 
-// ---------------------------------------------------------------------------
-// 1Q second moment of one lane's 8 elements (reference quantize.py:222-299)
-// ---------------------------------------------------------------------------
+// CoState first moment of the lane's 8 elements (reference costate.py:398-416):
+//   m_hat = has_state ? fl(fl(alpha*g) + s_b*sgn) : 0,  m = fl(fl(b1*m_hat) + fl(ob1*g))
+// with s_b = norm_b / sqrt(128) for phase blocks (costate.py:306, true
+// division), the fp16 amplitude for amplitude blocks, 0 for null blocks.
+template <bool FULL>
+__device__ __forceinline__ void tam_costate_m(const TamTensor& d, const TamWave& W, float alpha_prev,
+                                              const float* g, float* m) {
+  const bool has = (d.flags & TAM_FLAG_HAS_STATE) != 0;  // uniform over the launch
+  if (has) {
+    float s = 0.0f;
+    uint32_t byte = 0;
+    if (FULL || W.bvalid) {
+      // the three per-block values are loaded together (no load waits on the label)
+      const uint32_t label = tam_g(d.labels)[W.b];
+      const float nrm = tam_g(d.norms)[W.b];
+      const uint16_t am = tam_g(d.amp)[W.b];
+      if (FULL || W.nv > 0) byte = tam_g(d.signs)[W.e0 >> 3];
+      const float sph = nrm / d.sqrt_block;
+      s = label == 1u ? sph : (label == 2u ? tam_f16_to_f32(am) : 0.0f);
+    }
+#pragma unroll
+    for (int i = 0; i < TAM_EPL; ++i) {
+      const float sd = ((byte >> (7 - i)) & 1u) ? -s : s;  // s * (1 - 2*bit), costate.py:207-209, :317-319
+      const float mh = alpha_prev * g[i] + sd;
+      m[i] = d.beta1 * mh + d.one_minus_beta1 * g[i];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < TAM_EPL; ++i) m[i] = d.beta1 * 0.0f + d.one_minus_beta1 * g[i];
+  }
+}
+
+// 1Q second moment of the lane's 8 elements (reference quantize.py:222-299).
+//
+// Decode (quantize.py:256): the 2^bits values exp(lmin + ((k+0.5)/2^bits)*span)
+// of a block are computed once per block: for 2^bits <= 16 lane k of the block
+// computes value k and elements fetch theirs with ds_bpermute; for 64 levels
+// through a per-wave LDS table; 8-bit indices evaluate per element.
+//
 // Index of an element: with c = fl(fl(l - lmin)/sp) * 2^bits and u its
 // uniform, the reference computes floor(c) + (u < c - floor(c)) clamped to
 // [0, 2^bits - 1]; for real c and u in [0,1) that equals ceil(c - u).  The fast
-// path evaluates c from the hardware log2 (v_log_f32, whose error against the
+// path evaluates c~ = log2(v)*K + C in fp32 (K = ln2*2^bits/sp, C =
+// -lmin*2^bits/sp) from the hardware log2 (v_log_f32, whose error against the
 // correctly rounded ln is below 2^-21 |ln| for every normal input -- checked
-// exhaustively on gfx950) and accepts ceil(c~ - u) only when the whole error
-// interval [c~ - u - B, c~ - u + B] lies between the same integers (or clamps
-// to the same end); otherwise the element takes the exact path (correctly
+// exhaustively on gfx950) and bounds |(c - u) - d| <= B for d = fl(c~ - u):
+//   B = |log2 v| K (2^-21 + 2^-22) + |c~| 2^-21 + |C| 2^-22 + 2^-22
+// (hardware log error, the two fp32 roundings of c, the roundings of K, C, the
+// fma and the subtraction, each with margin).  ceil(d) is accepted when
+// [d - B, d + B] lies in (ceil(d) - 1, ceil(d)], or at or below 0, or above
+// 2^bits - 2 (the clamp gives the same index); q - d and d - (q - 1) are exact
+// there (Sterbenz).  Otherwise the element takes the exact path (correctly
 // rounded log and division).  lmin and lmax are the correctly rounded logs of
 // the block's smallest and largest v (log is monotone, so they equal the min
 // and max of the per-element logs).
-__device__ __forceinline__ void tam_vpath(const TamTensor& d, uint32_t b, bool bvalid, uint64_t e0,
-                                          const TamLane& L, const float* g, float* v, float (*lut)[64],
-                                          uint32_t seed_lo, uint32_t seed_hi) {
+template <bool FULL>
+__device__ __forceinline__ void tam_vpath(const TamTensor& d, const TamWave& W, const float* g, float* v,
+                                          float* lutw, uint32_t seed_lo, uint32_t seed_hi) {
   const uint32_t bits = d.v_bits;
   const uint32_t nbk = 1u << bits;
   const float fnb = (float)nbk;
   const float inv_nbk = 1.0f / fnb;  // exact power of two
+  const bool bvalid = FULL || W.bvalid;
   float lmin0 = 0.0f, span0 = 0.0f;
   uint32_t iw0 = 0, iw1 = 0;
   if (bvalid) {
-    const uint32_t sc = ((const uint32_t*)d.v_scales)[b];
+    const uint32_t sc = tam_g((const uint32_t*)d.v_scales)[W.b];
     lmin0 = tam_f16_to_f32((uint16_t)(sc & 0xffffu));
     span0 = tam_f16_to_f32((uint16_t)(sc >> 16)) - lmin0;  // quantize.py:253-255
-    const uint2 iw = *(const uint2*)(d.v_idx + e0);
+    const TamW2 iw = tam_g((const TamW2*)(d.v_idx + W.e0))[0];
     iw0 = iw.x;
     iw1 = iw.y;
   }
-  // decode (quantize.py:256): per-block table of the 2^bits values
+  uint32_t idx[TAM_EPL];
+#pragma unroll
+  for (int i = 0; i < TAM_EPL; ++i) idx[i] = ((i < 4 ? iw0 : iw1) >> (8 * (i & 3))) & 0xffu;
   float vo[TAM_EPL];
-  if (nbk <= 64u) {
-    if (bvalid) {
-      for (uint32_t k = L.l16; k < nbk; k += 16u) lut[L.bl][k] = tam_expf(lmin0 + ((float)k + 0.5f) * inv_nbk * span0);
-    }
-    __syncthreads();
+  if (nbk <= 16u) {
+    // every lane of the wave takes part in the permutes
+    const uint32_t k = W.l16 & (nbk - 1u);
+    const float val = tam_expf(lmin0 + ((float)k + 0.5f) * inv_nbk * span0);
+    const uint32_t row = W.lane & 48u;
 #pragma unroll
     for (int i = 0; i < TAM_EPL; ++i) {
-      const uint32_t idx = ((i < 4 ? iw0 : iw1) >> (8 * (i & 3))) & 0xffu;
-      vo[i] = bvalid ? lut[L.bl][idx & 63u] : 0.0f;
+      const int src = (int)((row + (idx[i] & (nbk - 1u))) << 2);
+      const float x = tam_u2f((uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)tam_f2u(val)));
+      vo[i] = bvalid ? x : 0.0f;
     }
-    __syncthreads();
+  } else if (nbk == 64u) {
+    float* tab = lutw + (W.lane >> 4) * 64u;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t k = W.l16 + 16u * (uint32_t)j;
+      tab[k] = tam_expf(lmin0 + ((float)k + 0.5f) * inv_nbk * span0);
+    }
+    tam_wave_lds_sync();
+#pragma unroll
+    for (int i = 0; i < TAM_EPL; ++i) vo[i] = bvalid ? tab[idx[i] & 63u] : 0.0f;
+    tam_wave_lds_sync();  // the next tile rewrites the table
   } else {
 #pragma unroll
-    for (int i = 0; i < TAM_EPL; ++i) {
-      const uint32_t idx = ((i < 4 ? iw0 : iw1) >> (8 * (i & 3))) & 0xffu;
-      vo[i] = tam_expf(lmin0 + ((float)idx + 0.5f) * inv_nbk * span0);
-    }
+    for (int i = 0; i < TAM_EPL; ++i) vo[i] = tam_expf(lmin0 + ((float)idx[i] + 0.5f) * inv_nbk * span0);
   }
   // EMA (quantize.py:259-270) and the clamp of :275
   float vc[TAM_EPL];
@@ -310,7 +373,7 @@ __device__ __forceinline__ void tam_vpath(const TamTensor& d, uint32_t b, bool b
   uint32_t nan_seen = 0;
 #pragma unroll
   for (int i = 0; i < TAM_EPL; ++i) {
-    const bool valid = e0 + i < d.n;
+    const bool valid = FULL || (uint32_t)i < W.nv;
     const float g2 = valid ? g[i] * g[i] : 0.0f;
     v[i] = __builtin_fmaf(d.one_minus_beta2, g2, vo[i] * d.beta2);
     vc[i] = v[i] < 1e-38f ? 1e-38f : v[i];
@@ -324,25 +387,25 @@ __device__ __forceinline__ void tam_vpath(const TamTensor& d, uint32_t b, bool b
   vmx = tam_block_fmax(vmx);
   nan_seen = tam_block_or(nan_seen);
   // correctly rounded logs of the extremes: even lanes log(vmin), odd lanes log(vmax)
-  const float lx = tam_logf((L.l16 & 1u) ? vmx : vmn);
+  const float lx = tam_logf((W.l16 & 1u) ? vmx : vmn);
   const float ly = tam_dppf<TAM_DPP_XOR1>(lx);
-  float lmn = (L.l16 & 1u) ? ly : lx;
-  float lmx = (L.l16 & 1u) ? lx : ly;
+  float lmn = (W.l16 & 1u) ? ly : lx;
+  float lmx = (W.l16 & 1u) ? lx : ly;
   if (nan_seen) lmn = lmx = tam_qnan();  // torch.min / torch.max propagate NaN
   if (!bvalid) return;
   float sp = lmx - lmn;  // quantize.py:283
   sp = sp < 1e-10f ? 1e-10f : sp;
-  if (L.l16 == 0) {
-    ((uint32_t*)d.v_scales)[b] = (uint32_t)tam_f32_to_f16(lmn) | ((uint32_t)tam_f32_to_f16(lmx) << 16);
+  if (W.l16 == 0) {
+    tam_g((uint32_t*)d.v_scales)[W.b] = (uint32_t)tam_f32_to_f16(lmn) | ((uint32_t)tam_f32_to_f16(lmx) << 16);
   }
   // certified stochastic rounding
-  const double dnb = (double)nbk;
   const double inv_sp = 1.0 / (double)sp;
-  const double K = 0x1.62e42fefa39efp-1 * dnb * inv_sp;  // c~ = log2(v) * K + C
-  const double C = -(double)lmn * dnb * inv_sp;
-  const double K2 = K * (0x1p-21 + 0x1p-50);
-  const double Cerr = __builtin_fabs(C) * 0x1p-50 + 0x1p-40;
-  const uint64_t quad0 = e0 >> 2;
+  const float K = (float)(0x1.62e42fefa39efp-1 * (double)nbk * inv_sp);
+  const float C = (float)(-(double)lmn * (double)nbk * inv_sp);
+  const float KB = K * (0x1p-21f + 0x1p-22f);
+  const float CB = __builtin_fmaf(__builtin_fabsf(C), 0x1p-22f, 0x1p-22f);
+  const float hi_clamp = fnb - 2.0f;
+  const uint64_t quad0 = W.e0 >> 2;
   const TamU4 r0 = tam_philox_quad(quad0, d.tensor_id, d.step, seed_lo, seed_hi);
   const TamU4 r1 = tam_philox_quad(quad0 + 1, d.tensor_id, d.step, seed_lo, seed_hi);
   const uint32_t rw[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
@@ -350,21 +413,20 @@ __device__ __forceinline__ void tam_vpath(const TamTensor& d, uint32_t b, bool b
   uint32_t amb = 0;
 #pragma unroll
   for (int i = 0; i < TAM_EPL; ++i) {
-    const double ud = (double)(rw[i] >> 8) * 0x1p-24;
-    double q = 0.0;
-    bool ok = false;
-    if (vc[i] >= 0x1p-126f) {  // normal input (false for NaN)
-      const double l2 = (double)__builtin_amdgcn_logf(vc[i]);
-      const double ct = __builtin_fma(l2, K, C);
-      const double dd = ct - ud;
-      const double B = __builtin_fma(__builtin_fabs(l2), K2, __builtin_fma(__builtin_fabs(ct), 0x1p-22, Cerr));
-      const double ql = __builtin_ceil(dd - B);
-      ok = ql >= dd + B;  // no integer in (dd - B, dd + B): ceil is the same over the interval
-      q = ql;
-    }
+    const float u = (float)(rw[i] >> 8) * 0x1p-24f;
+    const float l2 = __builtin_amdgcn_logf(vc[i]);
+    const float ct = __builtin_fmaf(l2, K, C);
+    const float dd = ct - u;
+    const float B = __builtin_fmaf(__builtin_fabsf(l2), KB, __builtin_fmaf(__builtin_fabsf(ct), 0x1p-21f, CB));
+    const float q = __builtin_ceilf(dd);
+    const bool inside = (q - dd >= B) && (dd - (q - 1.0f) > B);
+    const bool low = -dd >= B;
+    const bool high = dd - hi_clamp > B;
+    // B < 1/4 keeps the three comparisons exact or decided by a wide margin
+    const bool ok = (vc[i] >= 0x1p-126f) && (B < 0.25f) && (inside || low || high);  // false for NaN
     amb |= ok ? 0u : (1u << i);
-    const int qi = (int)q;
-    qb[i] = (uint32_t)(qi < 0 ? 0 : (qi > (int)(nbk - 1) ? (int)(nbk - 1) : qi));
+    const float qc = __builtin_fminf(__builtin_fmaxf(q, 0.0f), fnb - 1.0f);
+    qb[i] = ok ? (uint32_t)qc : 0u;
   }
   if (amb) {
     // exact path: the reference's own sequence with correctly rounded log and division
@@ -385,7 +447,7 @@ __device__ __forceinline__ void tam_vpath(const TamTensor& d, uint32_t b, bool b
   }
   const uint32_t ow0 = qb[0] | (qb[1] << 8) | (qb[2] << 16) | (qb[3] << 24);
   const uint32_t ow1 = qb[4] | (qb[5] << 8) | (qb[6] << 16) | (qb[7] << 24);
-  *(uint2*)(d.v_idx + e0) = make_uint2(ow0, ow1);
+  tam_g((TamW2*)(d.v_idx + W.e0))[0] = TamW2{ow0, ow1};
 }
 
 // ---------------------------------------------------------------------------
@@ -403,10 +465,11 @@ __device__ __forceinline__ void tam_vpath(const TamTensor& d, uint32_t b, bool b
 // R_p(fl(p + upd)) is accepted when R_p(fl(s~ - E)) == R_p(fl(s~ + E)) (R_p and
 // fl are monotone); otherwise the exact sequence runs.  The result of a
 // 16-bit parameter is returned as its bit pattern in pb.
-__device__ __forceinline__ void tam_update(const TamTensor& d, uint32_t dtype, float* p, const float* m,
-                                           const float* v, uint16_t* pb) {
+template <uint32_t DT>
+__device__ __forceinline__ void tam_update(const TamTensor& d, float* p, const float* m, const float* v,
+                                           uint16_t* pb) {
   const bool wd = (d.flags & TAM_FLAG_WD) != 0;
-  if (dtype == TAM_DTYPE_F32) {
+  if (DT == TAM_DTYPE_F32) {
 #pragma unroll
     for (int i = 0; i < TAM_EPL; ++i) {
       const double y = (double)v[i] * d.inv_bc2;
@@ -419,12 +482,12 @@ __device__ __forceinline__ void tam_update(const TamTensor& d, uint32_t dtype, f
     }
     return;
   }
-  const bool bf = dtype == TAM_DTYPE_BF16;
   uint32_t amb = 0;
   float pw[TAM_EPL];
 #pragma unroll
   for (int i = 0; i < TAM_EPL; ++i) {
-    pw[i] = wd ? tam_round_p(p[i] * d.c_wd, dtype) : p[i];
+    // weight decay rounds to the parameter dtype (p.mul_ on a 16-bit tensor)
+    pw[i] = wd ? tam_h2f<DT>(tam_round16_hw<DT>(p[i] * d.c_wd)) : p[i];
     const float q = v[i] * d.inv_bc2_f32;
     const float s = q * __builtin_amdgcn_rsqf(q);
     const float t2 = (s + d.eps) * d.bias_correction1;
@@ -432,12 +495,10 @@ __device__ __forceinline__ void tam_update(const TamTensor& d, uint32_t dtype, f
     const float u = a * __builtin_amdgcn_rcpf(t2);
     const float st = pw[i] + u;
     const float E = __builtin_fmaf(__builtin_fabsf(u), 0x1p-19f, __builtin_fmaf(__builtin_fabsf(st), 0x1p-22f, 0x1p-148f));
-    const float lo = st - E, hi = st + E;
     // finite, normal hardware inputs and outputs; NaN fails every comparison
     const bool ok0 = (q >= 0x1p-126f) && (t2 < 0x1p125f) && (__builtin_fabsf(st) < 0x1p126f);
-    const float lc = ok0 ? lo : 0.0f, hc = ok0 ? hi : 1.0f;
-    const uint16_t rl = bf ? tam_f32_to_bf16_rne(lc) : tam_f32_to_f16(lc);
-    const uint16_t rh = bf ? tam_f32_to_bf16_rne(hc) : tam_f32_to_f16(hc);
+    const uint16_t rl = tam_round16_hw<DT>(st - E);
+    const uint16_t rh = tam_round16_hw<DT>(st + E);
     const bool ok = ok0 && rl == rh;
     pb[i] = rl;
     amb |= ok ? 0u : (1u << i);
@@ -447,108 +508,127 @@ __device__ __forceinline__ void tam_update(const TamTensor& d, uint32_t dtype, f
     for (int i = 0; i < TAM_EPL; ++i) {
       if (amb & (1u << i)) {
         const float den = __builtin_sqrtf(v[i] / d.bias_correction2) + d.eps;
-        pb[i] = tam_round16(pw[i] + (d.neg_lr * m[i]) / (den * d.bias_correction1), dtype);
+        pb[i] = tam_round16(pw[i] + (d.neg_lr * m[i]) / (den * d.bias_correction1), DT);
       }
     }
   }
 }
 
-// Stores 8 16-bit parameter patterns (elements [e0, e0+8), none beyond n).
-__device__ __forceinline__ void tam_store8_bits(void* base, uint64_t e0, uint64_t n, bool vec_ok, const uint16_t* b) {
-  if (vec_ok && e0 + TAM_EPL <= n) {
-    uint32_t w[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) w[k] = (uint32_t)b[2 * k] | ((uint32_t)b[2 * k + 1] << 16);
-    *(uint4*)((uint16_t*)base + e0) = make_uint4(w[0], w[1], w[2], w[3]);
-  } else {
-#pragma unroll
-    for (int i = 0; i < TAM_EPL; ++i)
-      if (e0 + i < n) ((uint16_t*)base)[e0 + i] = b[i];
+// Tensor owning global tile `tile` (binary search over tile0).
+__device__ __forceinline__ int tam_find_tensor(const TamTensor* __restrict__ T, int nT, uint32_t tile) {
+  int lo = 0, hi = nT - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (T[mid].tile0 <= tile) lo = mid; else hi = mid - 1;
   }
+  return lo;
+}
+
+// Whether a wave's quarter of tile `wq` lies inside the tensor with aligned arrays.
+__device__ __forceinline__ bool tam_quarter_full(const TamTensor& d, uint32_t wq) {
+  const bool aligned = (((uintptr_t)d.param | (uintptr_t)d.grad) & 15u) == 0;
+  return aligned && (uint64_t)(wq + 1u) * (4u * TAM_BLOCK_SIZE) <= d.n;
 }
 
 // ---------------------------------------------------------------------------
-// K1: the fused pass over every tile
+// K1: the fused pass
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(TAM_WG) void tam_k1_main(const TamTensor* __restrict__ T, int nT,
+// Per quarter tile: loads, first moment (CoState or fp32), second moment (1Q or
+// fp32), update, store; for CoState tensors the fp64 partial sums of g.g and
+// m.g over the quarter's 4 blocks (pairwise: blocks, then pairs of blocks).
+template <uint32_t DT, bool FULL>
+__device__ __forceinline__ void tam_k1_quarter(const TamTensor& d, uint32_t wq, uint32_t lane, float* lutw,
+                                               uint32_t seed_lo, uint32_t seed_hi, double2* __restrict__ part) {
+  const TamWave W = tam_wave(d, wq, lane, FULL);
+  const bool costate = (d.flags & TAM_FLAG_COSTATE) != 0;
+  float g[TAM_EPL], p[TAM_EPL], m[TAM_EPL], v[TAM_EPL];
+  if (FULL || W.bvalid) {
+    tam_ld8<DT, FULL>(d.grad, W.e0, W.nv, g);
+    tam_ld8<DT, FULL>(d.param, W.e0, W.nv, p);
+  } else {
+#pragma unroll
+    for (int i = 0; i < TAM_EPL; ++i) g[i] = p[i] = 0.0f;
+  }
+#pragma unroll
+  for (int i = 0; i < TAM_EPL; ++i) m[i] = v[i] = 0.0f;
+
+  // ---- first moment ---------------------------------------------------
+  if (costate) {
+    const float alpha_prev = (d.flags & TAM_FLAG_HAS_STATE) ? tam_g(d.alpha)[0] : 0.0f;
+    if (FULL || W.bvalid) tam_costate_m<FULL>(d, W, alpha_prev, g, m);
+    double gg[TAM_EPL], mg[TAM_EPL];
+#pragma unroll
+    for (int i = 0; i < TAM_EPL; ++i) {
+      const bool ok = FULL || (W.bvalid && (uint32_t)i < W.nv);
+      gg[i] = ok ? (double)g[i] * (double)g[i] : 0.0;
+      mg[i] = ok ? (double)m[i] * (double)g[i] : 0.0;
+    }
+    double sgg = tam_block_sum(tam_pair8(gg));
+    double smg = tam_block_sum(tam_pair8(mg));
+    // the wave's 4 blocks: adjacent pairs, then the two pairs
+    sgg = sgg + __shfl_xor(sgg, 16);
+    smg = smg + __shfl_xor(smg, 16);
+    sgg = sgg + __shfl_xor(sgg, 32);
+    smg = smg + __shfl_xor(smg, 32);
+    if (lane == 0) tam_g((TamD2*)part)[0] = TamD2{sgg, smg};
+  } else if (FULL || W.bvalid) {
+    // fp32 exp_avg (optimizer.py:113): m = fma(1-b1, g, fl(m*b1))
+    float ea[TAM_EPL];
+    tam_ld8_f32<FULL>(d.exp_avg, W.e0, W.nv, ea);
+#pragma unroll
+    for (int i = 0; i < TAM_EPL; ++i) m[i] = __builtin_fmaf(d.one_minus_beta1, g[i], ea[i] * d.beta1);
+    tam_st8_f32<FULL>(d.exp_avg, W.e0, W.nv, m);
+  }
+
+  // ---- second moment --------------------------------------------------
+  if (d.flags & TAM_FLAG_COMPRESS_V) {
+    tam_vpath<FULL>(d, W, g, v, lutw, seed_lo, seed_hi);
+  } else if (FULL || W.bvalid) {
+    // fp32 exp_avg_sq (optimizer.py:166): v = fma(fl((1-b2)*g), g, fl(v*b2))
+    float es[TAM_EPL];
+    tam_ld8_f32<FULL>(d.exp_avg_sq, W.e0, W.nv, es);
+#pragma unroll
+    for (int i = 0; i < TAM_EPL; ++i) v[i] = __builtin_fmaf(d.one_minus_beta2 * g[i], g[i], es[i] * d.beta2);
+    tam_st8_f32<FULL>(d.exp_avg_sq, W.e0, W.nv, v);
+  }
+
+  // ---- parameter update -----------------------------------------------
+  if (FULL || W.bvalid) {
+    uint16_t pb[TAM_EPL];
+    tam_update<DT>(d, p, m, v, pb);
+    if (DT == TAM_DTYPE_F32) tam_st8_f32<FULL>((float*)d.param, W.e0, W.nv, p);
+    else tam_st8_bits<FULL>(d.param, W.e0, W.nv, pb);
+  }
+}
+
+// Persistent workgroups stride over the tiles; the four waves of a workgroup
+// take the four quarters of each tile and never synchronise with each other.
+__global__ __launch_bounds__(TAM_WG) __attribute__((amdgpu_waves_per_eu(4, 4))) void tam_k1_main(const TamTensor* __restrict__ T, int nT,
                                                       uint32_t total_tiles, uint32_t seed_lo,
                                                       uint32_t seed_hi, double2* __restrict__ partials) {
-  __shared__ float lut[TAM_BPT][64];
-  __shared__ double2 wred[TAM_WG / 64];
-  const TamLane L = tam_lane();
+  __shared__ float lut[TAM_WG / 64][4 * 64];
+  const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+  float* lutw = lut[wave];
   int ti = tam_find_tensor(T, nT, blockIdx.x);
   for (uint32_t tile = blockIdx.x; tile < total_tiles; tile += gridDim.x) {
     while (tile >= T[ti].tile0 + T[ti].ntiles) ++ti;
     const TamTensor& d = T[ti];
-    const uint32_t b = (tile - d.tile0) * TAM_BPT + L.bl;  // block within the tensor
-    const bool bvalid = b < d.nb;
-    const uint64_t e0 = (uint64_t)b * TAM_BLOCK_SIZE + L.l16 * TAM_EPL;
-    const uint32_t dtype = d.dtype;
-    const bool costate = (d.flags & TAM_FLAG_COSTATE) != 0;
-    const bool vec_p = (((uintptr_t)d.param | (uintptr_t)d.grad) & 15u) == 0;
-
-    float g[TAM_EPL], p[TAM_EPL], m[TAM_EPL], v[TAM_EPL];
-    if (bvalid) {
-      tam_load8(d.grad, dtype, e0, d.n, vec_p, g);
-      tam_load8(d.param, dtype, e0, d.n, vec_p, p);
-    } else {
-#pragma unroll
-      for (int i = 0; i < TAM_EPL; ++i) g[i] = p[i] = m[i] = v[i] = 0.0f;
-    }
-
-    // ---- first moment ---------------------------------------------------
-    if (costate) {
-      const float alpha_prev = (d.flags & TAM_FLAG_HAS_STATE) ? *d.alpha : 0.0f;
-      if (bvalid) tam_costate_m(d, b, e0, alpha_prev, g, m);
-      double gg[TAM_EPL], mg[TAM_EPL];
-#pragma unroll
-      for (int i = 0; i < TAM_EPL; ++i) {
-        const bool ok = bvalid && (e0 + i < d.n);
-        gg[i] = ok ? (double)g[i] * (double)g[i] : 0.0;
-        mg[i] = ok ? (double)m[i] * (double)g[i] : 0.0;
-      }
-      double sgg = tam_block_sum(tam_pair8(gg));
-      double smg = tam_block_sum(tam_pair8(mg));
-      // blocks of one wave: adjacent pairs, then pairs of pairs
-      sgg = sgg + __shfl_xor(sgg, 16);
-      smg = smg + __shfl_xor(smg, 16);
-      sgg = sgg + __shfl_xor(sgg, 32);
-      smg = smg + __shfl_xor(smg, 32);
-      if ((threadIdx.x & 63u) == 0) wred[threadIdx.x >> 6] = make_double2(sgg, smg);
-      __syncthreads();
-      if (threadIdx.x == 0) {
-        const double a = (wred[0].x + wred[1].x) + (wred[2].x + wred[3].x);
-        const double c = (wred[0].y + wred[1].y) + (wred[2].y + wred[3].y);
-        partials[tile] = make_double2(a, c);
-      }
-      __syncthreads();  // wred is rewritten by the next tile
-    } else if (bvalid) {
-      // fp32 exp_avg (optimizer.py:113): m = fma(1-b1, g, fl(m*b1))
-      float ea[TAM_EPL];
-      tam_load8_f32(d.exp_avg, e0, d.n, ea);
-#pragma unroll
-      for (int i = 0; i < TAM_EPL; ++i) m[i] = __builtin_fmaf(d.one_minus_beta1, g[i], ea[i] * d.beta1);
-      tam_store8_f32(d.exp_avg, e0, d.n, m);
-    }
-
-    // ---- second moment --------------------------------------------------
-    if (d.flags & TAM_FLAG_COMPRESS_V) {
-      tam_vpath(d, b, bvalid, e0, L, g, v, lut, seed_lo, seed_hi);
-    } else if (bvalid) {
-      // fp32 exp_avg_sq (optimizer.py:166): v = fma(fl((1-b2)*g), g, fl(v*b2))
-      float es[TAM_EPL];
-      tam_load8_f32(d.exp_avg_sq, e0, d.n, es);
-#pragma unroll
-      for (int i = 0; i < TAM_EPL; ++i) v[i] = __builtin_fmaf(d.one_minus_beta2 * g[i], g[i], es[i] * d.beta2);
-      tam_store8_f32(d.exp_avg_sq, e0, d.n, v);
-    }
-
-    // ---- parameter update -----------------------------------------------
-    if (bvalid) {
-      uint16_t pb[TAM_EPL];
-      tam_update(d, dtype, p, m, v, pb);
-      if (dtype == TAM_DTYPE_F32) tam_store8(d.param, dtype, e0, d.n, vec_p, p);
-      else tam_store8_bits(d.param, e0, d.n, vec_p, pb);
+    const uint32_t wq = (tile - d.tile0) * 4u + wave;  // quarter tile within the tensor
+    double2* part = partials + (uint64_t)tile * 4u + wave;
+    const bool full = tam_quarter_full(d, wq);
+    switch (d.dtype) {
+      case TAM_DTYPE_BF16:
+        if (full) tam_k1_quarter<TAM_DTYPE_BF16, true>(d, wq, lane, lutw, seed_lo, seed_hi, part);
+        else tam_k1_quarter<TAM_DTYPE_BF16, false>(d, wq, lane, lutw, seed_lo, seed_hi, part);
+        break;
+      case TAM_DTYPE_F16:
+        if (full) tam_k1_quarter<TAM_DTYPE_F16, true>(d, wq, lane, lutw, seed_lo, seed_hi, part);
+        else tam_k1_quarter<TAM_DTYPE_F16, false>(d, wq, lane, lutw, seed_lo, seed_hi, part);
+        break;
+      default:
+        if (full) tam_k1_quarter<TAM_DTYPE_F32, true>(d, wq, lane, lutw, seed_lo, seed_hi, part);
+        else tam_k1_quarter<TAM_DTYPE_F32, false>(d, wq, lane, lutw, seed_lo, seed_hi, part);
+        break;
     }
   }
 }
@@ -557,27 +637,38 @@ __global__ __launch_bounds__(TAM_WG) void tam_k1_main(const TamTensor* __restric
 // K2: alpha of every CoState tensor (costate.py:37-41)
 // ---------------------------------------------------------------------------
 // Balanced pairwise sum of x[0..count) zero-padded to a power of two, by one
-// 256-thread workgroup.  Aligned chunks of 2048 values are summed in LDS; the
-// chunk sums (a power of two of them, at most 2048) are summed the same way.
+// 256-thread workgroup.  Each thread sums 32 consecutive values (a pairwise
+// subtree), aligned chunks of 8192 values are finished in LDS, and the chunk
+// sums (a power of two of them, at most 2048) are summed the same way.
+// Zero padding beyond the tensor's blocks does not change the sum: x + 0 == x,
+// and the caller adds +0.0 to the result, which also settles the sign of an
+// exact zero.
+#define TAM_PAIR_PER_THREAD 32
 __device__ double2 tam_wg_pairwise2(const double2* __restrict__ x, uint32_t count, double2* sh,
                                     double2* chunks) {
   uint32_t P = 1;
   while (P < count) P <<= 1;
-  const uint32_t CH = TAM_WG * 8;
+  const uint32_t CH = TAM_WG * TAM_PAIR_PER_THREAD;
   const uint32_t nchunks = P > CH ? P / CH : 1;
   const uint32_t lim = P > CH ? CH : P;
   const uint32_t tid = threadIdx.x;
   for (uint32_t c = 0; c < nchunks; ++c) {
-    double a[8], q[8];
+    double sa[4], sq[4];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t local = tid * 8 + i;
-      const uint32_t k = c * CH + local;
-      const double2 v = (local < lim && k < count) ? x[k] : make_double2(0.0, 0.0);
-      a[i] = v.x;
-      q[i] = v.y;
+    for (int h = 0; h < 4; ++h) {
+      double a[8], q[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t local = tid * TAM_PAIR_PER_THREAD + h * 8 + i;
+        const uint32_t k = c * CH + local;
+        const double2 v = (local < lim && k < count) ? x[k] : make_double2(0.0, 0.0);
+        a[i] = v.x;
+        q[i] = v.y;
+      }
+      sa[h] = tam_pair8(a);
+      sq[h] = tam_pair8(q);
     }
-    sh[tid] = make_double2(tam_pair8(a), tam_pair8(q));
+    sh[tid] = make_double2((sa[0] + sa[1]) + (sa[2] + sa[3]), (sq[0] + sq[1]) + (sq[2] + sq[3]));
     __syncthreads();
     for (uint32_t w = TAM_WG / 2; w >= 1; w >>= 1) {
       double2 s = make_double2(0.0, 0.0);
@@ -620,7 +711,8 @@ __global__ __launch_bounds__(TAM_WG) void tam_k_alpha(const TamTensor* __restric
   __shared__ double2 chunks[2048];
   const TamTensor& d = T[blockIdx.x];
   if (!(d.flags & TAM_FLAG_COSTATE)) return;
-  const double2 s = tam_wg_pairwise2(partials + d.tile0, d.ntiles, sh, chunks);
+  // the tensor's quarter-tile partials, 4 per tile
+  const double2 s = tam_wg_pairwise2(partials + (uint64_t)d.tile0 * 4u, d.ntiles * 4u, sh, chunks);
   if (threadIdx.x == 0) {
     // dot products round to fp32 once; +0.0 makes an exact-zero sum +0
     const float gg = (float)(s.x + 0.0);
@@ -632,51 +724,69 @@ __global__ __launch_bounds__(TAM_WG) void tam_k_alpha(const TamTensor* __restric
 // ---------------------------------------------------------------------------
 // K3: CoState encode (costate.py:419-425, :213-258) and block ratios (:51-86)
 // ---------------------------------------------------------------------------
+template <uint32_t DT, bool FULL>
+__device__ __forceinline__ void tam_k2_quarter(const TamTensor& d, uint32_t wq, uint32_t lane, float a,
+                                               float* __restrict__ ratios) {
+  const TamWave W = tam_wave(d, wq, lane, FULL);
+  double dd[TAM_EPL], mm[TAM_EPL];
+  uint32_t sbyte = 0;
+  if (FULL || W.bvalid) {
+    float g[TAM_EPL], m[TAM_EPL];
+    tam_ld8<DT, FULL>(d.grad, W.e0, W.nv, g);
+    const float alpha_prev = (d.flags & TAM_FLAG_HAS_STATE) ? tam_g(d.alpha)[0] : 0.0f;
+    tam_costate_m<FULL>(d, W, alpha_prev, g, m);
+#pragma unroll
+    for (int i = 0; i < TAM_EPL; ++i) {
+      const bool ok = FULL || (uint32_t)i < W.nv;
+      const float delta = ok ? m[i] - a * g[i] : 0.0f;  // costate.py:42
+      dd[i] = (double)delta * (double)delta;
+      mm[i] = ok ? (double)m[i] * (double)m[i] : 0.0;
+      sbyte |= (delta < 0.0f ? 1u : 0u) << (7 - i);  // costate.py:170-181
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < TAM_EPL; ++i) dd[i] = mm[i] = 0.0;
+  }
+  const double sd = tam_block_sum(tam_pair8(dd));
+  const double sm = tam_block_sum(tam_pair8(mm));
+  if (FULL || W.bvalid) {
+    if (FULL || W.nv > 0) tam_g(d.signs)[W.e0 >> 3] = (uint8_t)sbyte;
+    if (W.l16 == 0) {
+      const float nd = (float)__builtin_sqrt(sd);
+      const float nm = (float)__builtin_sqrt(sm);
+      tam_g(d.norms)[W.b] = nd;                                 // costate.py:241
+      tam_g(d.amp)[W.b] = tam_f32_to_f16(nd / d.sqrt_block);   // costate.py:248
+      tam_g(ratios)[d.ratio_off + W.b] = nm == 0.0f ? 0.0f : nd / nm;  // costate.py:81-84
+    }
+  }
+}
+
 __global__ __launch_bounds__(TAM_WG) void tam_k2_encode(const TamTensor* __restrict__ T, int nT,
                                                         uint32_t total_tiles,
                                                         const float* __restrict__ alpha_new,
                                                         float* __restrict__ ratios) {
-  const TamLane L = tam_lane();
+  const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
   int ti = tam_find_tensor(T, nT, blockIdx.x);
   for (uint32_t tile = blockIdx.x; tile < total_tiles; tile += gridDim.x) {
     while (tile >= T[ti].tile0 + T[ti].ntiles) ++ti;
     const TamTensor& d = T[ti];
     if (!(d.flags & TAM_FLAG_COSTATE)) continue;  // uniform over the workgroup
-    const uint32_t b = (tile - d.tile0) * TAM_BPT + L.bl;
-    const bool bvalid = b < d.nb;
-    const uint64_t e0 = (uint64_t)b * TAM_BLOCK_SIZE + L.l16 * TAM_EPL;
-    const bool vec_g = ((uintptr_t)d.grad & 15u) == 0;
-    float g[TAM_EPL], m[TAM_EPL];
-    double dd[TAM_EPL], mm[TAM_EPL];
-    uint32_t sbyte = 0;
-    if (bvalid) {
-      tam_load8(d.grad, d.dtype, e0, d.n, vec_g, g);
-      const float alpha_prev = (d.flags & TAM_FLAG_HAS_STATE) ? *d.alpha : 0.0f;
-      tam_costate_m(d, b, e0, alpha_prev, g, m);
-      const float a = alpha_new[ti];
-#pragma unroll
-      for (int i = 0; i < TAM_EPL; ++i) {
-        const bool ok = e0 + i < d.n;
-        const float delta = ok ? m[i] - a * g[i] : 0.0f;  // costate.py:42
-        dd[i] = (double)delta * (double)delta;
-        mm[i] = ok ? (double)m[i] * (double)m[i] : 0.0;
-        sbyte |= (delta < 0.0f ? 1u : 0u) << (7 - i);  // costate.py:170-181
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < TAM_EPL; ++i) dd[i] = mm[i] = 0.0;
-    }
-    const double sd = tam_block_sum(tam_pair8(dd));
-    const double sm = tam_block_sum(tam_pair8(mm));
-    if (bvalid) {
-      if (e0 < d.n) d.signs[e0 >> 3] = (uint8_t)sbyte;
-      if (L.l16 == 0) {
-        const float nd = (float)__builtin_sqrt(sd);
-        const float nm = (float)__builtin_sqrt(sm);
-        d.norms[b] = nd;                                   // costate.py:241
-        d.amp[b] = tam_f32_to_f16(nd / d.sqrt_block);     // costate.py:248
-        ratios[d.ratio_off + b] = nm == 0.0f ? 0.0f : nd / nm;  // costate.py:81-84
-      }
+    const uint32_t wq = (tile - d.tile0) * 4u + wave;
+    const float a = alpha_new[ti];
+    const bool full = tam_quarter_full(d, wq);
+    switch (d.dtype) {
+      case TAM_DTYPE_BF16:
+        if (full) tam_k2_quarter<TAM_DTYPE_BF16, true>(d, wq, lane, a, ratios);
+        else tam_k2_quarter<TAM_DTYPE_BF16, false>(d, wq, lane, a, ratios);
+        break;
+      case TAM_DTYPE_F16:
+        if (full) tam_k2_quarter<TAM_DTYPE_F16, true>(d, wq, lane, a, ratios);
+        else tam_k2_quarter<TAM_DTYPE_F16, false>(d, wq, lane, a, ratios);
+        break;
+      default:
+        if (full) tam_k2_quarter<TAM_DTYPE_F32, true>(d, wq, lane, a, ratios);
+        else tam_k2_quarter<TAM_DTYPE_F32, false>(d, wq, lane, a, ratios);
+        break;
     }
   }
 }
@@ -940,7 +1050,7 @@ int tam_prepare(TamTensor* tensors, int n_tensors, TamStepInfo* info) {
   info->ratio_blocks = ratio_blocks;
   uint64_t off = 0;
   info->off_partials = off;
-  off = tam_align_up(off + tiles * sizeof(double2), 256);
+  off = tam_align_up(off + tiles * 4u * sizeof(double2), 256);  // one partial per quarter tile
   info->off_alpha = off;
   off = tam_align_up(off + (uint64_t)n_tensors * sizeof(float), 256);
   info->off_ratios = off;
