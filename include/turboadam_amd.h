@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define TAM_ABI_VERSION 1
+#define TAM_ABI_VERSION 2
 #define TAM_BLOCK_SIZE 128 /* elements per quantisation / CoState block */
 
 /* error codes */
@@ -82,7 +82,7 @@ typedef struct TamTensor {
   uint32_t nb;          /* [derived] ceil(n/128)                             */
   uint32_t tile0;       /* [derived] first tile (16 blocks) of this tensor   */
   uint32_t ntiles;      /* [derived] ceil(nb/16)                             */
-  uint32_t pad0;
+  uint32_t chunk0;      /* [derived] COSTATE: first alpha-reduction chunk    */
   uint64_t ratio_off;   /* [derived] COSTATE: offset of its ratios (blocks)  */
   double inv_bc2;       /* [in] 1 / (double)bias_correction2 (correctly rounded) */
 } TamTensor;
@@ -92,12 +92,13 @@ typedef struct TamStepInfo {
   int32_t n_tensors;
   uint32_t total_tiles;
   uint32_t n_costate;
-  uint32_t pad0;
+  uint32_t total_chunks;   /* alpha-reduction chunks (8192 partial sums each) */
   uint64_t ratio_blocks;   /* sum of nb over CoState tensors */
   uint64_t off_partials;   /* workspace byte offsets */
   uint64_t off_alpha;
   uint64_t off_ratios;
   uint64_t ws_bytes;       /* required workspace size */
+  uint64_t off_chunks;
 } TamStepInfo;
 
 /* Version of this ABI (TAM_ABI_VERSION). */

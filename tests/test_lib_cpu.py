@@ -71,6 +71,9 @@ def test_prepare_layout():
     assert info.off_partials == 0
     assert info.off_alpha >= 21 * 4 * 16 and info.off_ratios >= info.off_alpha + 3 * 4
     assert info.ws_bytes >= info.off_ratios + 300 * 4
+    # one alpha-reduction chunk per CoState tensor here (at most 8192 quarter-tile partials)
+    assert info.total_chunks == 2 and [a.chunk0 for a in arr] == [0, 1, 1]
+    assert info.off_chunks >= info.off_ratios + 300 * 4 and info.ws_bytes >= info.off_chunks + 2 * 16
     assert info.off_alpha % 256 == 0 and info.off_ratios % 256 == 0
 
 

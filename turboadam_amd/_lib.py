@@ -22,7 +22,7 @@ TAM_FLAG_COMPRESS_V = 0x2
 TAM_FLAG_HAS_STATE = 0x4
 TAM_FLAG_WD = 0x8
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 
 class TamTensor(ctypes.Structure):
@@ -60,7 +60,7 @@ class TamTensor(ctypes.Structure):
         ("nb", ctypes.c_uint32),
         ("tile0", ctypes.c_uint32),
         ("ntiles", ctypes.c_uint32),
-        ("pad0", ctypes.c_uint32),
+        ("chunk0", ctypes.c_uint32),
         ("ratio_off", ctypes.c_uint64),
         ("inv_bc2", ctypes.c_double),
     ]
@@ -71,12 +71,13 @@ class TamStepInfo(ctypes.Structure):
         ("n_tensors", ctypes.c_int32),
         ("total_tiles", ctypes.c_uint32),
         ("n_costate", ctypes.c_uint32),
-        ("pad0", ctypes.c_uint32),
+        ("total_chunks", ctypes.c_uint32),
         ("ratio_blocks", ctypes.c_uint64),
         ("off_partials", ctypes.c_uint64),
         ("off_alpha", ctypes.c_uint64),
         ("off_ratios", ctypes.c_uint64),
         ("ws_bytes", ctypes.c_uint64),
+        ("off_chunks", ctypes.c_uint64),
     ]
 
 

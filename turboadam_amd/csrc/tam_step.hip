@@ -169,9 +169,12 @@ __device__ __forceinline__ uint16_t tam_round16(float x, uint32_t dtype) {
 #define TAM_DPP_HALF_MIRROR 0x141
 #define TAM_DPP_MIRROR 0x140
 
+// Every control used here reads a lane of the same row, so no lane is out of
+// range and bound_ctrl (read 0 from an invalid lane) never applies; with it
+// set the compiler needs no copy of an `old` value.
 template <int CTRL>
 __device__ __forceinline__ uint32_t tam_dpp(uint32_t v) {
-  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xF, 0xF, true);
 }
 template <int CTRL>
 __device__ __forceinline__ float tam_dppf(float v) {
@@ -181,6 +184,14 @@ template <int CTRL>
 __device__ __forceinline__ double tam_dppd(double v) {
   const uint64_t u = tam_d2u(v);
   const uint32_t lo = tam_dpp<CTRL>((uint32_t)u), hi = tam_dpp<CTRL>((uint32_t)(u >> 32));
+  return tam_u2d(((uint64_t)hi << 32) | lo);
+}
+
+// Value of `v` in lane `l` of the wave (uniform result).
+__device__ __forceinline__ double tam_readlane_d(double v, int l) {
+  const uint64_t u = tam_d2u(v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, l);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), l);
   return tam_u2d(((uint64_t)hi << 32) | lo);
 }
 
@@ -200,18 +211,20 @@ __device__ __forceinline__ double tam_block_sum(double v) {
   v = v + tam_dppd<TAM_DPP_MIRROR>(v);
   return v;
 }
-__device__ __forceinline__ float tam_block_fmin(float v) {  // IEEE minNum; NaN tracked separately
-  v = __builtin_fminf(v, tam_dppf<TAM_DPP_XOR1>(v));
-  v = __builtin_fminf(v, tam_dppf<TAM_DPP_XOR2>(v));
-  v = __builtin_fminf(v, tam_dppf<TAM_DPP_HALF_MIRROR>(v));
-  v = __builtin_fminf(v, tam_dppf<TAM_DPP_MIRROR>(v));
+// Minimum / maximum over the block of unsigned keys (bit patterns of
+// positive floats order like the floats).
+__device__ __forceinline__ uint32_t tam_block_umin(uint32_t v) {
+  v = __builtin_elementwise_min(v, tam_dpp<TAM_DPP_XOR1>(v));
+  v = __builtin_elementwise_min(v, tam_dpp<TAM_DPP_XOR2>(v));
+  v = __builtin_elementwise_min(v, tam_dpp<TAM_DPP_HALF_MIRROR>(v));
+  v = __builtin_elementwise_min(v, tam_dpp<TAM_DPP_MIRROR>(v));
   return v;
 }
-__device__ __forceinline__ float tam_block_fmax(float v) {
-  v = __builtin_fmaxf(v, tam_dppf<TAM_DPP_XOR1>(v));
-  v = __builtin_fmaxf(v, tam_dppf<TAM_DPP_XOR2>(v));
-  v = __builtin_fmaxf(v, tam_dppf<TAM_DPP_HALF_MIRROR>(v));
-  v = __builtin_fmaxf(v, tam_dppf<TAM_DPP_MIRROR>(v));
+__device__ __forceinline__ uint32_t tam_block_umax(uint32_t v) {
+  v = __builtin_elementwise_max(v, tam_dpp<TAM_DPP_XOR1>(v));
+  v = __builtin_elementwise_max(v, tam_dpp<TAM_DPP_XOR2>(v));
+  v = __builtin_elementwise_max(v, tam_dpp<TAM_DPP_HALF_MIRROR>(v));
+  v = __builtin_elementwise_max(v, tam_dpp<TAM_DPP_MIRROR>(v));
   return v;
 }
 __device__ __forceinline__ uint32_t tam_block_or(uint32_t v) {
@@ -221,6 +234,11 @@ __device__ __forceinline__ uint32_t tam_block_or(uint32_t v) {
   v |= tam_dpp<TAM_DPP_MIRROR>(v);
   return v;
 }
+
+// Compiler-only barrier: memory accesses are not moved across it (no
+// instruction is emitted).  Placed after a quarter's loads so that none of them
+// is sunk below the first use of another (each would then wait on its own).
+__device__ __forceinline__ void tam_compiler_fence() { asm volatile("" ::: "memory"); }
 
 // Orders this wave's LDS accesses before and after the call (LDS operations of
 // one wave execute in order, so no s_barrier is needed between lanes of a wave).
@@ -268,25 +286,40 @@ __device__ __forceinline__ TamWave tam_wave(const TamTensor& d, uint32_t wq, uin
 //   m_hat = has_state ? fl(fl(alpha*g) + s_b*sgn) : 0,  m = fl(fl(b1*m_hat) + fl(ob1*g))
 // with s_b = norm_b / sqrt(128) for phase blocks (costate.py:306, true
 // division), the fp16 amplitude for amplitude blocks, 0 for null blocks.
+// The CoState state of the lane's block (label, norm, amplitude) and its sign
+// byte, loaded before any of it is used (no load waits on the label).
+struct TamCsIn {
+  uint32_t label, amp, byte;
+  float nrm;
+};
 template <bool FULL>
-__device__ __forceinline__ void tam_costate_m(const TamTensor& d, const TamWave& W, float alpha_prev,
-                                              const float* g, float* m) {
+__device__ __forceinline__ TamCsIn tam_cs_load(const TamTensor& d, const TamWave& W) {
+  TamCsIn c = {0u, 0u, 0u, 0.0f};
+  if ((d.flags & TAM_FLAG_HAS_STATE) && (FULL || W.bvalid)) {
+    c.label = tam_g(d.labels)[W.b];
+    c.nrm = tam_g(d.norms)[W.b];
+    c.amp = tam_g(d.amp)[W.b];
+    if (FULL || W.nv > 0) c.byte = tam_g(d.signs)[W.e0 >> 3];
+  }
+  return c;
+}
+
+template <bool FULL>
+__device__ __forceinline__ void tam_costate_m(const TamTensor& d, const TamWave& W, const TamCsIn& cs,
+                                              float alpha_prev, const float* g, float* m) {
   const bool has = (d.flags & TAM_FLAG_HAS_STATE) != 0;  // uniform over the launch
   if (has) {
     float s = 0.0f;
-    uint32_t byte = 0;
+    const uint32_t byte = cs.byte;
     if (FULL || W.bvalid) {
-      // the three per-block values are loaded together (no load waits on the label)
-      const uint32_t label = tam_g(d.labels)[W.b];
-      const float nrm = tam_g(d.norms)[W.b];
-      const uint16_t am = tam_g(d.amp)[W.b];
-      if (FULL || W.nv > 0) byte = tam_g(d.signs)[W.e0 >> 3];
-      const float sph = nrm / d.sqrt_block;
-      s = label == 1u ? sph : (label == 2u ? tam_f16_to_f32(am) : 0.0f);
+      const float sph = cs.nrm / d.sqrt_block;
+      s = cs.label == 1u ? sph : (cs.label == 2u ? tam_f16_to_f32((uint16_t)cs.amp) : 0.0f);
     }
 #pragma unroll
     for (int i = 0; i < TAM_EPL; ++i) {
-      const float sd = ((byte >> (7 - i)) & 1u) ? -s : s;  // s * (1 - 2*bit), costate.py:207-209, :317-319
+      // s * (1 - 2*bit), costate.py:207-209, :317-319: s has a clear sign bit
+      // (a norm or an fp16 amplitude), so the bit becomes the sign of s
+      const float sd = tam_u2f((tam_f2u(s) & 0x7fffffffu) | ((byte << (24 + i)) & 0x80000000u));
       const float mh = alpha_prev * g[i] + sd;
       m[i] = d.beta1 * mh + d.one_minus_beta1 * g[i];
     }
@@ -310,33 +343,43 @@ __device__ __forceinline__ void tam_costate_m(const TamTensor& d, const TamWave&
 // -lmin*2^bits/sp) from the hardware log2 (v_log_f32, whose error against the
 // correctly rounded ln is below 2^-21 |ln| for every normal input -- checked
 // exhaustively on gfx950) and bounds |(c - u) - d| <= B for d = fl(c~ - u):
-//   B = |log2 v| K (2^-21 + 2^-22) + |c~| 2^-21 + |C| 2^-22 + 2^-22
-// (hardware log error, the two fp32 roundings of c, the roundings of K, C, the
+//   B = |log2 v| K 2^-20 + |c~| 2^-21 + |C| 2^-21 + 2^-22
+// (hardware log error, the two fp32 roundings of c, the errors of K and C, the
 // fma and the subtraction, each with margin).  ceil(d) is accepted when
-// [d - B, d + B] lies in (ceil(d) - 1, ceil(d)], or at or below 0, or above
-// 2^bits - 2 (the clamp gives the same index); q - d and d - (q - 1) are exact
-// there (Sterbenz).  Otherwise the element takes the exact path (correctly
-// rounded log and division).  lmin and lmax are the correctly rounded logs of
+// [d - B, d + B] lies in (q - 1, q], q = ceil(d): with r = q - d (exact by
+// Sterbenz, or at least 1/2 when q = 1), r >= B and 1 - r > B (1 - r is
+// exact for r >= 1/2 and above 1/2 otherwise).  The clamp to [0, 2^bits - 1]
+// then gives the reference's index.  Otherwise the element takes the exact
+// path (correctly rounded log and division).  lmin and lmax are the correctly rounded logs of
 // the block's smallest and largest v (log is monotone, so they equal the min
 // and max of the per-element logs).
+// The 1Q state of the lane: its block's fp16 (log_min, log_max) pair and its 8 indices.
+struct TamVIn {
+  uint32_t sc, iw0, iw1;
+};
 template <bool FULL>
-__device__ __forceinline__ void tam_vpath(const TamTensor& d, const TamWave& W, const float* g, float* v,
-                                          float* lutw, uint32_t seed_lo, uint32_t seed_hi) {
+__device__ __forceinline__ TamVIn tam_v_load(const TamTensor& d, const TamWave& W) {
+  TamVIn r = {0u, 0u, 0u};
+  if (FULL || W.bvalid) {
+    r.sc = tam_g((const uint32_t*)d.v_scales)[W.b];
+    const TamW2 iw = tam_g((const TamW2*)(d.v_idx + W.e0))[0];
+    r.iw0 = iw.x;
+    r.iw1 = iw.y;
+  }
+  return r;
+}
+
+template <bool FULL>
+__device__ __forceinline__ void tam_vpath(const TamTensor& d, const TamWave& W, const TamVIn& vin, const float* g,
+                                          float* v, float* lutw, uint32_t seed_lo, uint32_t seed_hi) {
   const uint32_t bits = d.v_bits;
   const uint32_t nbk = 1u << bits;
   const float fnb = (float)nbk;
   const float inv_nbk = 1.0f / fnb;  // exact power of two
   const bool bvalid = FULL || W.bvalid;
-  float lmin0 = 0.0f, span0 = 0.0f;
-  uint32_t iw0 = 0, iw1 = 0;
-  if (bvalid) {
-    const uint32_t sc = tam_g((const uint32_t*)d.v_scales)[W.b];
-    lmin0 = tam_f16_to_f32((uint16_t)(sc & 0xffffu));
-    span0 = tam_f16_to_f32((uint16_t)(sc >> 16)) - lmin0;  // quantize.py:253-255
-    const TamW2 iw = tam_g((const TamW2*)(d.v_idx + W.e0))[0];
-    iw0 = iw.x;
-    iw1 = iw.y;
-  }
+  const float lmin0 = tam_f16_to_f32((uint16_t)(vin.sc & 0xffffu));
+  const float span0 = tam_f16_to_f32((uint16_t)(vin.sc >> 16)) - lmin0;  // quantize.py:253-255
+  const uint32_t iw0 = vin.iw0, iw1 = vin.iw1;
   uint32_t idx[TAM_EPL];
 #pragma unroll
   for (int i = 0; i < TAM_EPL; ++i) idx[i] = ((i < 4 ? iw0 : iw1) >> (8 * (i & 3))) & 0xffu;
@@ -367,9 +410,11 @@ __device__ __forceinline__ void tam_vpath(const TamTensor& d, const TamWave& W, 
 #pragma unroll
     for (int i = 0; i < TAM_EPL; ++i) vo[i] = tam_expf(lmin0 + ((float)idx[i] + 0.5f) * inv_nbk * span0);
   }
-  // EMA (quantize.py:259-270) and the clamp of :275
+  // EMA (quantize.py:259-270) and the clamp of :275.  A clamped v is
+  // positive or NaN: the block extremes are taken on bit patterns (NaN
+  // patterns order above +inf and are handled by nan_seen).
   float vc[TAM_EPL];
-  float vmn = tam_inf(), vmx = -tam_inf();
+  uint32_t kmn = 0x7f800000u, kmx = 0u;
   uint32_t nan_seen = 0;
 #pragma unroll
   for (int i = 0; i < TAM_EPL; ++i) {
@@ -379,15 +424,15 @@ __device__ __forceinline__ void tam_vpath(const TamTensor& d, const TamWave& W, 
     vc[i] = v[i] < 1e-38f ? 1e-38f : v[i];
     if (valid && bvalid) {
       nan_seen |= tam_isnan(vc[i]) ? 1u : 0u;
-      vmn = __builtin_fminf(vmn, vc[i]);
-      vmx = __builtin_fmaxf(vmx, vc[i]);
+      kmn = __builtin_elementwise_min(kmn, tam_f2u(vc[i]));
+      kmx = __builtin_elementwise_max(kmx, tam_f2u(vc[i]));
     }
   }
-  vmn = tam_block_fmin(vmn);
-  vmx = tam_block_fmax(vmx);
+  kmn = tam_block_umin(kmn);
+  kmx = tam_block_umax(kmx);
   nan_seen = tam_block_or(nan_seen);
   // correctly rounded logs of the extremes: even lanes log(vmin), odd lanes log(vmax)
-  const float lx = tam_logf((W.l16 & 1u) ? vmx : vmn);
+  const float lx = tam_logf(tam_u2f((W.l16 & 1u) ? kmx : kmn));
   const float ly = tam_dppf<TAM_DPP_XOR1>(lx);
   float lmn = (W.l16 & 1u) ? ly : lx;
   float lmx = (W.l16 & 1u) ? lx : ly;
@@ -398,35 +443,55 @@ __device__ __forceinline__ void tam_vpath(const TamTensor& d, const TamWave& W, 
   if (W.l16 == 0) {
     tam_g((uint32_t*)d.v_scales)[W.b] = (uint32_t)tam_f32_to_f16(lmn) | ((uint32_t)tam_f32_to_f16(lmx) << 16);
   }
-  // certified stochastic rounding
-  const double inv_sp = 1.0 / (double)sp;
-  const float K = (float)(0x1.62e42fefa39efp-1 * (double)nbk * inv_sp);
-  const float C = (float)(-(double)lmn * (double)nbk * inv_sp);
-  const float KB = K * (0x1p-21f + 0x1p-22f);
-  const float CB = __builtin_fmaf(__builtin_fabsf(C), 0x1p-22f, 0x1p-22f);
-  const float hi_clamp = fnb - 2.0f;
+  // certified stochastic rounding.  K and C from the hardware reciprocal of
+  // sp (within 2^-23): K within 2^-22 of ln2*2^bits/sp, C within 2^-22.4 of
+  // -lmin*2^bits/sp; the bound below takes |log2 v| K 2^-20 and |C| 2^-21.
+  const float rsp = __builtin_amdgcn_rcpf(sp);
+  const float K = (0x1.62e430p-1f * fnb) * rsp;
+  const float C = (-lmn * fnb) * rsp;
+  const float KB = K * 0x1p-20f;
+  const float CB = __builtin_fmaf(__builtin_fabsf(C), 0x1p-21f, 0x1p-22f);
   const uint64_t quad0 = W.e0 >> 2;
   const TamU4 r0 = tam_philox_quad(quad0, d.tensor_id, d.step, seed_lo, seed_hi);
   const TamU4 r1 = tam_philox_quad(quad0 + 1, d.tensor_id, d.step, seed_lo, seed_hi);
   const uint32_t rw[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
   uint32_t qb[TAM_EPL];
   uint32_t amb = 0;
+  if (FULL) {
+    // Every element of a full block lies in [vmin, vmax] (normal, no NaN
+    // checked once here), so |log2 v| <= L and, when B < 1/4, |c~| <= 2^bits + 1
+    // (c lies in [0, 2^bits]); one bound B serves the block.  Accept when
+    // |(q - 1/2) - d| < H = 1/2 - (B + 2^-22): then r = q - d lies in (B, 1 - B)
+    // (q - 1/2 - d is exact, or above 1/4 and within 2^-26 of its value).
+    const float la = __builtin_amdgcn_logf(tam_u2f(kmn)), lb = __builtin_amdgcn_logf(tam_u2f(kmx));
+    const float L = __builtin_fmaxf(__builtin_fabsf(la), __builtin_fabsf(lb)) * (1.0f + 0x1p-18f) + 0x1p-20f;
+    const float Bb = __builtin_fmaf(L, KB, __builtin_fmaf(fnb + 1.0f, 0x1p-21f, CB));
+    const bool blk_ok = (tam_u2f(kmn) >= 0x1p-126f) && !nan_seen && (Bb < 0.25f);
+    const float H = blk_ok ? 0.5f - (Bb + 0x1p-22f) : -1.0f;
 #pragma unroll
-  for (int i = 0; i < TAM_EPL; ++i) {
-    const float u = (float)(rw[i] >> 8) * 0x1p-24f;
-    const float l2 = __builtin_amdgcn_logf(vc[i]);
-    const float ct = __builtin_fmaf(l2, K, C);
-    const float dd = ct - u;
-    const float B = __builtin_fmaf(__builtin_fabsf(l2), KB, __builtin_fmaf(__builtin_fabsf(ct), 0x1p-21f, CB));
-    const float q = __builtin_ceilf(dd);
-    const bool inside = (q - dd >= B) && (dd - (q - 1.0f) > B);
-    const bool low = -dd >= B;
-    const bool high = dd - hi_clamp > B;
-    // B < 1/4 keeps the three comparisons exact or decided by a wide margin
-    const bool ok = (vc[i] >= 0x1p-126f) && (B < 0.25f) && (inside || low || high);  // false for NaN
-    amb |= ok ? 0u : (1u << i);
-    const float qc = __builtin_fminf(__builtin_fmaxf(q, 0.0f), fnb - 1.0f);
-    qb[i] = ok ? (uint32_t)qc : 0u;
+    for (int i = 0; i < TAM_EPL; ++i) {
+      const float l2 = __builtin_amdgcn_logf(vc[i]);
+      const float ct = __builtin_fmaf(l2, K, C);
+      const float dd = __builtin_fmaf(-(float)(rw[i] >> 8), 0x1p-24f, ct);  // fl(ct - u), u exact
+      const float q = __builtin_ceilf(dd);
+      const float t = (q - 0.5f) - dd;
+      const bool ok = __builtin_fabsf(t) < H;
+      amb |= ok ? 0u : (1u << i);
+      qb[i] = (uint32_t)__builtin_amdgcn_fmed3f(q, 0.0f, fnb - 1.0f);  // the exact path overwrites !ok
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < TAM_EPL; ++i) {
+      const float l2 = __builtin_amdgcn_logf(vc[i]);
+      const float ct = __builtin_fmaf(l2, K, C);
+      const float dd = __builtin_fmaf(-(float)(rw[i] >> 8), 0x1p-24f, ct);  // fl(ct - u), u exact
+      const float B = __builtin_fmaf(__builtin_fabsf(l2), KB, __builtin_fmaf(__builtin_fabsf(ct), 0x1p-21f, CB));
+      const float q = __builtin_ceilf(dd);
+      const float r = q - dd;
+      const bool ok = (vc[i] >= 0x1p-126f) && (r >= B) && (1.0f - r > B);  // false for NaN
+      amb |= ok ? 0u : (1u << i);
+      qb[i] = (uint32_t)__builtin_amdgcn_fmed3f(q, 0.0f, fnb - 1.0f);  // the exact path overwrites !ok
+    }
   }
   if (amb) {
     // exact path: the reference's own sequence with correctly rounded log and division
@@ -457,10 +522,12 @@ __device__ __forceinline__ void tam_vpath(const TamTensor& d, const TamWave& W, 
 // t2 = fl(den*bc1), a = fl(-lr*m), upd = fl(a/t2), p = R_p(fl(p + upd)).
 // fp32 parameters: q1 comes from the fp64 reciprocal of bc2 when a rounding
 // test proves the fp32 rounding, else from the division.  bf16 / fp16
-// parameters: a fast sequence with the hardware rsq / rcp gives u~ with
+// parameters: a fast sequence, u~ = fl(fl(c*m) * rcp(fl(s~ + eps))) with
+// c = fl(-lr/bc1) and s~ = fl(q * rsq(q)), q = fl(v * fl(1/bc2)), gives
 // |u~ - upd| <= 2^-19 |u~| + 2^-148 (the exact sequence's six roundings and
-// the fast sequence's five are each 2^-24 relative, both hardware seeds are
-// within 2^-23 -- checked exhaustively on gfx950).  With s~ = fl(p + u~),
+// the fast sequence's seven are each 2^-24 relative, both hardware results
+// are within 2^-23 -- checked exhaustively on gfx950; 17 units of 2^-24 in
+// all, inside 2^-19).  With s~ = fl(p + u~),
 // fl(p + upd) lies within E = 2^-19 |u~| + 2^-22 |s~| + 2^-148 of s~, so
 // R_p(fl(p + upd)) is accepted when R_p(fl(s~ - E)) == R_p(fl(s~ + E)) (R_p and
 // fl are monotone); otherwise the exact sequence runs.  The result of a
@@ -484,19 +551,29 @@ __device__ __forceinline__ void tam_update(const TamTensor& d, float* p, const f
   }
   uint32_t amb = 0;
   float pw[TAM_EPL];
+  // weight decay rounds to the parameter dtype (p.mul_ on a 16-bit tensor)
+  if (wd) {
+#pragma unroll
+    for (int i = 0; i < TAM_EPL; ++i) pw[i] = tam_h2f<DT>(tam_round16_hw<DT>(p[i] * d.c_wd));
+  } else {
+#pragma unroll
+    for (int i = 0; i < TAM_EPL; ++i) pw[i] = p[i];
+  }
+  // -lr / bc1 (one more rounding in the fast sequence, inside the 2^-19 bound)
+  const float c_lr = d.neg_lr / d.bias_correction1;
 #pragma unroll
   for (int i = 0; i < TAM_EPL; ++i) {
-    // weight decay rounds to the parameter dtype (p.mul_ on a 16-bit tensor)
-    pw[i] = wd ? tam_h2f<DT>(tam_round16_hw<DT>(p[i] * d.c_wd)) : p[i];
     const float q = v[i] * d.inv_bc2_f32;
     const float s = q * __builtin_amdgcn_rsqf(q);
-    const float t2 = (s + d.eps) * d.bias_correction1;
-    const float a = d.neg_lr * m[i];
-    const float u = a * __builtin_amdgcn_rcpf(t2);
+    const float den = s + d.eps;
+    const float cm = c_lr * m[i];
+    const float u = cm * __builtin_amdgcn_rcpf(den);
     const float st = pw[i] + u;
     const float E = __builtin_fmaf(__builtin_fabsf(u), 0x1p-19f, __builtin_fmaf(__builtin_fabsf(st), 0x1p-22f, 0x1p-148f));
-    // finite, normal hardware inputs and outputs; NaN fails every comparison
-    const bool ok0 = (q >= 0x1p-126f) && (t2 < 0x1p125f) && (__builtin_fabsf(st) < 0x1p126f);
+    // finite, normal hardware inputs and outputs, and c*m exact zero or normal
+    // (its relative error bound); NaN fails every comparison
+    const bool ok0 = (q >= 0x1p-126f) && (den < 0x1p125f) && (__builtin_fabsf(st) < 0x1p126f) &&
+                     ((__builtin_fabsf(cm) >= 0x1p-126f) || (cm == 0.0f));
     const uint16_t rl = tam_round16_hw<DT>(st - E);
     const uint16_t rh = tam_round16_hw<DT>(st + E);
     const bool ok = ok0 && rl == rh;
@@ -541,7 +618,9 @@ __device__ __forceinline__ void tam_k1_quarter(const TamTensor& d, uint32_t wq, 
                                                uint32_t seed_lo, uint32_t seed_hi, double2* __restrict__ part) {
   const TamWave W = tam_wave(d, wq, lane, FULL);
   const bool costate = (d.flags & TAM_FLAG_COSTATE) != 0;
+  const bool compress_v = (d.flags & TAM_FLAG_COMPRESS_V) != 0;
   float g[TAM_EPL], p[TAM_EPL], m[TAM_EPL], v[TAM_EPL];
+  // every load of the quarter is issued before any result is used
   if (FULL || W.bvalid) {
     tam_ld8<DT, FULL>(d.grad, W.e0, W.nv, g);
     tam_ld8<DT, FULL>(d.param, W.e0, W.nv, p);
@@ -549,13 +628,16 @@ __device__ __forceinline__ void tam_k1_quarter(const TamTensor& d, uint32_t wq, 
 #pragma unroll
     for (int i = 0; i < TAM_EPL; ++i) g[i] = p[i] = 0.0f;
   }
+  const TamCsIn cs = costate ? tam_cs_load<FULL>(d, W) : TamCsIn{0u, 0u, 0u, 0.0f};
+  const TamVIn vin = compress_v ? tam_v_load<FULL>(d, W) : TamVIn{0u, 0u, 0u};
+  const float alpha_prev = (costate && (d.flags & TAM_FLAG_HAS_STATE)) ? tam_g(d.alpha)[0] : 0.0f;
+  tam_compiler_fence();
 #pragma unroll
   for (int i = 0; i < TAM_EPL; ++i) m[i] = v[i] = 0.0f;
 
   // ---- first moment ---------------------------------------------------
   if (costate) {
-    const float alpha_prev = (d.flags & TAM_FLAG_HAS_STATE) ? tam_g(d.alpha)[0] : 0.0f;
-    if (FULL || W.bvalid) tam_costate_m<FULL>(d, W, alpha_prev, g, m);
+    if (FULL || W.bvalid) tam_costate_m<FULL>(d, W, cs, alpha_prev, g, m);
     double gg[TAM_EPL], mg[TAM_EPL];
 #pragma unroll
     for (int i = 0; i < TAM_EPL; ++i) {
@@ -563,14 +645,14 @@ __device__ __forceinline__ void tam_k1_quarter(const TamTensor& d, uint32_t wq, 
       gg[i] = ok ? (double)g[i] * (double)g[i] : 0.0;
       mg[i] = ok ? (double)m[i] * (double)g[i] : 0.0;
     }
-    double sgg = tam_block_sum(tam_pair8(gg));
-    double smg = tam_block_sum(tam_pair8(mg));
-    // the wave's 4 blocks: adjacent pairs, then the two pairs
-    sgg = sgg + __shfl_xor(sgg, 16);
-    smg = smg + __shfl_xor(smg, 16);
-    sgg = sgg + __shfl_xor(sgg, 32);
-    smg = smg + __shfl_xor(smg, 32);
-    if (lane == 0) tam_g((TamD2*)part)[0] = TamD2{sgg, smg};
+    const double sgg = tam_block_sum(tam_pair8(gg));
+    const double smg = tam_block_sum(tam_pair8(mg));
+    // the wave's 4 blocks (block k in lanes 16k..16k+15): adjacent pairs, then the two pairs
+    const double tgg = (tam_readlane_d(sgg, 0) + tam_readlane_d(sgg, 16)) +
+                       (tam_readlane_d(sgg, 32) + tam_readlane_d(sgg, 48));
+    const double tmg = (tam_readlane_d(smg, 0) + tam_readlane_d(smg, 16)) +
+                       (tam_readlane_d(smg, 32) + tam_readlane_d(smg, 48));
+    if (lane == 0) tam_g((TamD2*)part)[0] = TamD2{tgg, tmg};
   } else if (FULL || W.bvalid) {
     // fp32 exp_avg (optimizer.py:113): m = fma(1-b1, g, fl(m*b1))
     float ea[TAM_EPL];
@@ -581,8 +663,8 @@ __device__ __forceinline__ void tam_k1_quarter(const TamTensor& d, uint32_t wq, 
   }
 
   // ---- second moment --------------------------------------------------
-  if (d.flags & TAM_FLAG_COMPRESS_V) {
-    tam_vpath<FULL>(d, W, g, v, lutw, seed_lo, seed_hi);
+  if (compress_v) {
+    tam_vpath<FULL>(d, W, vin, g, v, lutw, seed_lo, seed_hi);
   } else if (FULL || W.bvalid) {
     // fp32 exp_avg_sq (optimizer.py:166): v = fma(fl((1-b2)*g), g, fl(v*b2))
     float es[TAM_EPL];
@@ -636,83 +718,115 @@ __global__ __launch_bounds__(TAM_WG) __attribute__((amdgpu_waves_per_eu(4, 4))) 
 // ---------------------------------------------------------------------------
 // K2: alpha of every CoState tensor (costate.py:37-41)
 // ---------------------------------------------------------------------------
-// Balanced pairwise sum of x[0..count) zero-padded to a power of two, by one
-// 256-thread workgroup.  Each thread sums 32 consecutive values (a pairwise
-// subtree), aligned chunks of 8192 values are finished in LDS, and the chunk
-// sums (a power of two of them, at most 2048) are summed the same way.
-// Zero padding beyond the tensor's blocks does not change the sum: x + 0 == x,
-// and the caller adds +0.0 to the result, which also settles the sign of an
-// exact zero.
+// The dot products are balanced pairwise sums over the tensor's quarter-tile
+// partials zero-padded to a power of two P.  The padded array is cut into
+// aligned chunks of 8192 (one chunk of P when P <= 8192); chunk sums are
+// subtrees of the same tree.  K2a sums every chunk of every tensor (one
+// workgroup per chunk: 32 consecutive values per thread, then a tree in LDS);
+// K2b sums each tensor's chunk sums (at most 2048, a power of two) and forms
+// alpha.  Zero padding does not change the sum: x + 0 == x, and +0.0 added
+// to the result settles the sign of an exact zero.
 #define TAM_PAIR_PER_THREAD 32
-__device__ double2 tam_wg_pairwise2(const double2* __restrict__ x, uint32_t count, double2* sh,
-                                    double2* chunks) {
-  uint32_t P = 1;
-  while (P < count) P <<= 1;
-  const uint32_t CH = TAM_WG * TAM_PAIR_PER_THREAD;
-  const uint32_t nchunks = P > CH ? P / CH : 1;
-  const uint32_t lim = P > CH ? CH : P;
+#define TAM_CHUNK (TAM_WG * TAM_PAIR_PER_THREAD)
+
+__device__ __forceinline__ uint32_t tam_pow2_at_least(uint32_t x) {
+  uint32_t p = 1;
+  while (p < x) p <<= 1;
+  return p;
+}
+// Chunks of a tensor's padded partial array (0 for tensors without CoState).
+__host__ __device__ __forceinline__ uint32_t tam_alpha_chunks(uint32_t flags, uint32_t ntiles) {
+  if (!(flags & TAM_FLAG_COSTATE)) return 0;
+  uint32_t p = 1;
+  while (p < ntiles * 4u) p <<= 1;
+  return p > TAM_CHUNK ? p / TAM_CHUNK : 1u;
+}
+
+// Pairwise sum of sh[0..n) (n a power of two, n <= 2 * TAM_WG) in place; every
+// thread of the workgroup calls it.  Returns sh[0].
+__device__ double2 tam_wg_tree(double2* sh, uint32_t n) {
   const uint32_t tid = threadIdx.x;
-  for (uint32_t c = 0; c < nchunks; ++c) {
-    double sa[4], sq[4];
-#pragma unroll
-    for (int h = 0; h < 4; ++h) {
-      double a[8], q[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const uint32_t local = tid * TAM_PAIR_PER_THREAD + h * 8 + i;
-        const uint32_t k = c * CH + local;
-        const double2 v = (local < lim && k < count) ? x[k] : make_double2(0.0, 0.0);
-        a[i] = v.x;
-        q[i] = v.y;
-      }
-      sa[h] = tam_pair8(a);
-      sq[h] = tam_pair8(q);
+  for (uint32_t w = n / 2; w >= 1; w >>= 1) {
+    double2 s = make_double2(0.0, 0.0);
+    if (tid < w) {
+      const double2 l = sh[2 * tid], r = sh[2 * tid + 1];
+      s = make_double2(l.x + r.x, l.y + r.y);
     }
-    sh[tid] = make_double2((sa[0] + sa[1]) + (sa[2] + sa[3]), (sq[0] + sq[1]) + (sq[2] + sq[3]));
     __syncthreads();
-    for (uint32_t w = TAM_WG / 2; w >= 1; w >>= 1) {
-      double2 s = make_double2(0.0, 0.0);
-      if (tid < w) {
-        const double2 l = sh[2 * tid], r = sh[2 * tid + 1];
-        s = make_double2(l.x + r.x, l.y + r.y);
-      }
-      __syncthreads();
-      if (tid < w) sh[tid] = s;
-      __syncthreads();
-    }
-    if (tid == 0) chunks[c] = sh[0];
+    if (tid < w) sh[tid] = s;
     __syncthreads();
   }
-  for (uint32_t w = nchunks / 2; w >= 1; w >>= 1) {  // w <= 1024: at most 4 pairs per thread
-    double2 s[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint32_t i = tid + j * TAM_WG;
-      if (i < w) {
-        const double2 l = chunks[2 * i], r = chunks[2 * i + 1];
-        s[j] = make_double2(l.x + r.x, l.y + r.y);
-      }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint32_t i = tid + j * TAM_WG;
-      if (i < w) chunks[i] = s[j];
-    }
-    __syncthreads();
+  return sh[0];
+}
+
+__global__ __launch_bounds__(TAM_WG) void tam_k_alpha_chunks(const TamTensor* __restrict__ T, int nT,
+                                                             const double2* __restrict__ partials,
+                                                             double2* __restrict__ chunk_sums) {
+  __shared__ double2 sh[TAM_WG];
+  const uint32_t c = blockIdx.x;
+  // tensor owning chunk c: the first whose chunk range ends after c
+  int lo = 0, hi = nT - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (T[mid].chunk0 + tam_alpha_chunks(T[mid].flags, T[mid].ntiles) > c) hi = mid; else lo = mid + 1;
   }
-  return chunks[0];
+  const TamTensor& d = T[lo];
+  const uint32_t count = d.ntiles * 4u;                 // quarter-tile partials of the tensor
+  const uint32_t P = tam_pow2_at_least(count);
+  const uint32_t lim = P > TAM_CHUNK ? TAM_CHUNK : P;   // leaves of this chunk's subtree
+  const uint32_t base = (c - d.chunk0) * TAM_CHUNK;
+  const double2* x = partials + (uint64_t)d.tile0 * 4u;
+  const uint32_t tid = threadIdx.x;
+  double sa[4], sq[4];
+#pragma unroll
+  for (int h = 0; h < 4; ++h) {
+    double a[8], q[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t local = tid * TAM_PAIR_PER_THREAD + h * 8 + i;
+      const uint32_t k = base + local;
+      const double2 v = (local < lim && k < count) ? x[k] : make_double2(0.0, 0.0);
+      a[i] = v.x;
+      q[i] = v.y;
+    }
+    sa[h] = tam_pair8(a);
+    sq[h] = tam_pair8(q);
+  }
+  sh[tid] = make_double2((sa[0] + sa[1]) + (sa[2] + sa[3]), (sq[0] + sq[1]) + (sq[2] + sq[3]));
+  __syncthreads();
+  const double2 r = tam_wg_tree(sh, TAM_WG);
+  if (tid == 0) chunk_sums[c] = r;
 }
 
 __global__ __launch_bounds__(TAM_WG) void tam_k_alpha(const TamTensor* __restrict__ T,
-                                                      const double2* __restrict__ partials,
+                                                      const double2* __restrict__ chunk_sums,
                                                       float* __restrict__ alpha_new) {
-  __shared__ double2 sh[TAM_WG];
-  __shared__ double2 chunks[2048];
+  __shared__ double2 sh[2048];
   const TamTensor& d = T[blockIdx.x];
-  if (!(d.flags & TAM_FLAG_COSTATE)) return;
-  // the tensor's quarter-tile partials, 4 per tile
-  const double2 s = tam_wg_pairwise2(partials + (uint64_t)d.tile0 * 4u, d.ntiles * 4u, sh, chunks);
+  const uint32_t nch = tam_alpha_chunks(d.flags, d.ntiles);
+  if (nch == 0) return;
+  for (uint32_t i = threadIdx.x; i < nch; i += TAM_WG) sh[i] = chunk_sums[d.chunk0 + i];
+  __syncthreads();
+  // nch is a power of two <= 2048: fold it to at most 2 * TAM_WG with pairwise steps first
+  uint32_t n = nch;
+  while (n > 2 * TAM_WG) {
+    const uint32_t w = n / 2;
+    double2 s[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t i = threadIdx.x + j * TAM_WG;
+      if (i < w) s[j] = make_double2(sh[2 * i].x + sh[2 * i + 1].x, sh[2 * i].y + sh[2 * i + 1].y);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t i = threadIdx.x + j * TAM_WG;
+      if (i < w) sh[i] = s[j];
+    }
+    __syncthreads();
+    n = w;
+  }
+  const double2 s = tam_wg_tree(sh, n);
   if (threadIdx.x == 0) {
     // dot products round to fp32 once; +0.0 makes an exact-zero sum +0
     const float gg = (float)(s.x + 0.0);
@@ -733,8 +847,10 @@ __device__ __forceinline__ void tam_k2_quarter(const TamTensor& d, uint32_t wq, 
   if (FULL || W.bvalid) {
     float g[TAM_EPL], m[TAM_EPL];
     tam_ld8<DT, FULL>(d.grad, W.e0, W.nv, g);
+    const TamCsIn cs = tam_cs_load<FULL>(d, W);
     const float alpha_prev = (d.flags & TAM_FLAG_HAS_STATE) ? tam_g(d.alpha)[0] : 0.0f;
-    tam_costate_m<FULL>(d, W, alpha_prev, g, m);
+    tam_compiler_fence();
+    tam_costate_m<FULL>(d, W, cs, alpha_prev, g, m);
 #pragma unroll
     for (int i = 0; i < TAM_EPL; ++i) {
       const bool ok = FULL || (uint32_t)i < W.nv;
@@ -749,14 +865,22 @@ __device__ __forceinline__ void tam_k2_quarter(const TamTensor& d, uint32_t wq, 
   }
   const double sd = tam_block_sum(tam_pair8(dd));
   const double sm = tam_block_sum(tam_pair8(mm));
+  // Per-block results, shared between lane pairs so that each lane evaluates
+  // one square root and one division: even lanes the residual norm and the
+  // amplitude, odd lanes the norm of m and the ratio.
+  const bool odd = (W.l16 & 1u) != 0;
+  const float nx = (float)__builtin_sqrt(odd ? sm : sd);
+  const float ny = tam_dppf<TAM_DPP_XOR1>(nx);
+  const float nd = odd ? ny : nx;  // costate.py:241
+  const float nm = odd ? nx : ny;
+  const float qv = nd / (odd ? nm : d.sqrt_block);  // costate.py:248 / :81-84
   if (FULL || W.bvalid) {
     if (FULL || W.nv > 0) tam_g(d.signs)[W.e0 >> 3] = (uint8_t)sbyte;
     if (W.l16 == 0) {
-      const float nd = (float)__builtin_sqrt(sd);
-      const float nm = (float)__builtin_sqrt(sm);
-      tam_g(d.norms)[W.b] = nd;                                 // costate.py:241
-      tam_g(d.amp)[W.b] = tam_f32_to_f16(nd / d.sqrt_block);   // costate.py:248
-      tam_g(ratios)[d.ratio_off + W.b] = nm == 0.0f ? 0.0f : nd / nm;  // costate.py:81-84
+      tam_g(d.norms)[W.b] = nd;
+      tam_g(d.amp)[W.b] = tam_f32_to_f16(qv);
+    } else if (W.l16 == 1) {
+      tam_g(ratios)[d.ratio_off + W.b] = nm == 0.0f ? 0.0f : qv;
     }
   }
 }
@@ -1007,7 +1131,7 @@ const char* tam_last_error(void) { return tam_err_buf; }
 int tam_prepare(TamTensor* tensors, int n_tensors, TamStepInfo* info) {
   tam_err_buf[0] = 0;
   if (!info || n_tensors < 0 || (n_tensors > 0 && !tensors)) return tam_fail(TAM_E_INVALID, "%snull argument", "");
-  uint64_t tiles = 0, ratio_blocks = 0;
+  uint64_t tiles = 0, ratio_blocks = 0, chunks = 0;
   uint32_t ncs = 0;
   for (int i = 0; i < n_tensors; ++i) {
     TamTensor& t = tensors[i];
@@ -1040,13 +1164,16 @@ int tam_prepare(TamTensor* tensors, int n_tensors, TamStepInfo* info) {
     t.nb = (uint32_t)nb;
     t.ntiles = (uint32_t)nt;
     t.tile0 = (uint32_t)tiles;
+    t.chunk0 = (uint32_t)chunks;
     tiles += nt;
+    chunks += tam_alpha_chunks(t.flags, t.ntiles);
     if (tiles > 0xffffffffull) return tam_fail(TAM_E_INVALID, "%stoo many tiles", "", 0);
   }
   memset(info, 0, sizeof(*info));
   info->n_tensors = n_tensors;
   info->total_tiles = (uint32_t)tiles;
   info->n_costate = ncs;
+  info->total_chunks = (uint32_t)chunks;
   info->ratio_blocks = ratio_blocks;
   uint64_t off = 0;
   info->off_partials = off;
@@ -1055,6 +1182,8 @@ int tam_prepare(TamTensor* tensors, int n_tensors, TamStepInfo* info) {
   off = tam_align_up(off + (uint64_t)n_tensors * sizeof(float), 256);
   info->off_ratios = off;
   off = tam_align_up(off + ratio_blocks * sizeof(float), 256);
+  info->off_chunks = off;
+  off = tam_align_up(off + chunks * sizeof(double2), 256);
   info->ws_bytes = off;
   return TAM_OK;
 }
@@ -1071,6 +1200,7 @@ static int tam_launch_pass(int pass, const TamTensor* d_tensors, const TamStepIn
   double2* partials = (double2*)(ws + info->off_partials);
   float* alpha_new = (float*)(ws + info->off_alpha);
   float* ratios = (float*)(ws + info->off_ratios);
+  double2* chunk_sums = (double2*)(ws + info->off_chunks);
   const int cus = tam_device_cus();
   const uint32_t grid = info->total_tiles < (uint32_t)(cus * 8) ? info->total_tiles : (uint32_t)(cus * 8);
   switch (pass) {
@@ -1079,7 +1209,10 @@ static int tam_launch_pass(int pass, const TamTensor* d_tensors, const TamStepIn
                          info->total_tiles, (uint32_t)seed, (uint32_t)(seed >> 32), partials);
       break;
     case 1:
-      hipLaunchKernelGGL(tam_k_alpha, dim3(info->n_tensors), dim3(TAM_WG), 0, s, d_tensors, partials, alpha_new);
+      hipLaunchKernelGGL(tam_k_alpha_chunks, dim3(info->total_chunks), dim3(TAM_WG), 0, s, d_tensors,
+                         info->n_tensors, partials, chunk_sums);
+      TAM_HIP_CHECK(hipGetLastError());
+      hipLaunchKernelGGL(tam_k_alpha, dim3(info->n_tensors), dim3(TAM_WG), 0, s, d_tensors, chunk_sums, alpha_new);
       break;
     case 2:
       hipLaunchKernelGGL(tam_k2_encode, dim3(grid), dim3(TAM_WG), 0, s, d_tensors, info->n_tensors,
