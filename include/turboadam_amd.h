@@ -85,6 +85,8 @@ typedef struct TamTensor {
   uint32_t chunk0;      /* [derived] COSTATE: first alpha-reduction chunk    */
   uint64_t ratio_off;   /* [derived] COSTATE: offset of its ratios (blocks)  */
   double inv_bc2;       /* [in] 1 / (double)bias_correction2 (correctly rounded) */
+  uint32_t slice0;      /* [derived] COSTATE: first selection slice (8192 blocks each) */
+  uint32_t sel_pad;
 } TamTensor;
 
 /* Launch summary and workspace layout, filled by tam_prepare(). */
@@ -93,12 +95,16 @@ typedef struct TamStepInfo {
   uint32_t total_tiles;
   uint32_t n_costate;
   uint32_t total_chunks;   /* alpha-reduction chunks (8192 partial sums each) */
+  uint32_t total_slices;   /* selection slices (8192 block ratios each) */
+  uint32_t pad0;
   uint64_t ratio_blocks;   /* sum of nb over CoState tensors */
   uint64_t off_partials;   /* workspace byte offsets */
   uint64_t off_alpha;
   uint64_t off_ratios;
   uint64_t ws_bytes;       /* required workspace size */
   uint64_t off_chunks;
+  uint64_t off_sel;
+  uint64_t off_hist;
 } TamStepInfo;
 
 /* Version of this ABI (TAM_ABI_VERSION). */

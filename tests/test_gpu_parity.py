@@ -167,3 +167,11 @@ def test_gpt2_block_shapes_few_steps():
               (3072, 768), (768,)]
     sizes = [int(np.prod(s)) for s in shapes]
     _check(run_side_by_side(sizes, [F32] * len(sizes), steps=3, shapes=shapes, lr=6e-4, weight_decay=0.01))
+
+
+def test_large_tensors_multi_workgroup_reductions():
+    # 5M elements: 9768 quarter-tile partials (two alpha-reduction chunks of 8192);
+    # 2.1M elements: 16391 blocks (three selection slices of 8192 ratios)
+    log("bf16 5.0M + 2.1M elements, 3 steps (multi-chunk alpha, multi-slice selection)")
+    sizes = [5_000_000 + 333, 8192 * 128 * 2 + 777]
+    _check(run_side_by_side(sizes, [BF16] * 2, steps=3, lr=1e-3, weight_decay=0.1))

@@ -63,6 +63,8 @@ class TamTensor(ctypes.Structure):
         ("chunk0", ctypes.c_uint32),
         ("ratio_off", ctypes.c_uint64),
         ("inv_bc2", ctypes.c_double),
+        ("slice0", ctypes.c_uint32),
+        ("sel_pad", ctypes.c_uint32),
     ]
 
 
@@ -72,12 +74,16 @@ class TamStepInfo(ctypes.Structure):
         ("total_tiles", ctypes.c_uint32),
         ("n_costate", ctypes.c_uint32),
         ("total_chunks", ctypes.c_uint32),
+        ("total_slices", ctypes.c_uint32),
+        ("pad0", ctypes.c_uint32),
         ("ratio_blocks", ctypes.c_uint64),
         ("off_partials", ctypes.c_uint64),
         ("off_alpha", ctypes.c_uint64),
         ("off_ratios", ctypes.c_uint64),
         ("ws_bytes", ctypes.c_uint64),
         ("off_chunks", ctypes.c_uint64),
+        ("off_sel", ctypes.c_uint64),
+        ("off_hist", ctypes.c_uint64),
     ]
 
 

@@ -920,10 +920,167 @@ __global__ __launch_bounds__(TAM_WG) void tam_k2_encode(const TamTensor* __restr
 // (costate.py:146-148), alpha write-back (costate.py:443-454)
 // ---------------------------------------------------------------------------
 // Ratios are >= +0 or NaN, so their fp32 bit patterns order like torch.sort
-// (NaN last).  The selection is an MSD radix select on those patterns: a
-// min/max pass finds the bits all keys share, then 11-bit digits below the
-// highest differing bit are histogrammed in LDS (keys of similar magnitude
-// spread over the bins instead of piling into a few), at most three passes.
+// (NaN last).  The selection is an MSD radix select on those patterns, spread
+// over slices of 8192 keys so that large tensors use many workgroups:
+//   K4a  per tensor: reset the selection state and histograms;
+//   K4b  per slice: min / max of the keys (atomic min / max per tensor) -- the
+//        bits all keys share need no pass;
+//   K4c  per slice, three times: LDS histogram of the next 11-bit digit below
+//        the bits already fixed, for the keys that match the prefix of each of
+//        the two ranks (keys of similar magnitude spread over the bins), added
+//        into the tensor's histogram;
+//   K4d  per tensor, after each K4c: prefix sums of the histogram pick the
+//        digit holding each rank;
+//   K4e  per slice: labels from the two thresholds; alpha write-back.
+#define TAM_SLICE 8192u
+#define TAM_SEL_WG 1024
+
+// Selection state of one tensor (workspace).
+struct TamSel {
+  uint32_t kmin, kmax;  // key range (K4b)
+  uint32_t prefix[2];   // bits fixed so far of the k_lo-th and k_hi-th key
+  uint32_t k[2];        // rank within the keys sharing the prefix
+  uint32_t mask;        // bits fixed so far
+  int32_t top;          // highest bit not yet fixed (-1: done)
+};
+
+__host__ __device__ __forceinline__ uint32_t tam_sel_slices(uint32_t flags, uint32_t nb) {
+  return (flags & TAM_FLAG_COSTATE) ? (nb + TAM_SLICE - 1u) / TAM_SLICE : 0u;
+}
+
+// Tensor owning selection slice j: the first whose slice range ends after j.
+__device__ __forceinline__ int tam_slice_tensor(const TamTensor* __restrict__ T, int nT, uint32_t j) {
+  int lo = 0, hi = nT - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (T[mid].slice0 + tam_sel_slices(T[mid].flags, T[mid].nb) > j) hi = mid; else lo = mid + 1;
+  }
+  return lo;
+}
+
+// Keys [k0, k1) of a tensor's ratios, visited by the 256 threads of a
+// workgroup, 8 keys per thread per round (two 16-byte loads; k0 is a
+// multiple of 4 and the ratio array 16-byte aligned).
+template <typename F>
+__device__ __forceinline__ void tam_slice_keys(const uint32_t* __restrict__ keys, uint32_t k0, uint32_t k1, F&& f) {
+  for (uint32_t i = k0 + threadIdx.x * 8u; i < k1; i += TAM_WG * 8u) {
+    if (i + 8u <= k1) {
+      const TamW4 a = tam_g((const TamW4*)(keys + i))[0], b = tam_g((const TamW4*)(keys + i))[1];
+      f(a.x); f(a.y); f(a.z); f(a.w);
+      f(b.x); f(b.y); f(b.z); f(b.w);
+    } else {
+      for (uint32_t j = i; j < k1; ++j) f(tam_g(keys)[j]);
+    }
+  }
+}
+
+// Initial prefix state from the key range: bits above the highest differing
+// bit are shared by every key.
+__device__ __forceinline__ void tam_sel_start(const TamSel& s, uint32_t* prefix, uint32_t& mask, int& top) {
+  const uint32_t diff = s.kmin ^ s.kmax;
+  top = diff ? 31 - __builtin_clz(diff) : -1;
+  mask = top >= 31 ? 0u : (0xffffffffu << (top + 1));
+  prefix[0] = prefix[1] = s.kmin & mask;
+}
+
+__global__ __launch_bounds__(TAM_WG) void tam_k_sel_reset(const TamTensor* __restrict__ T, TamSel* __restrict__ sel,
+                                                          uint32_t* __restrict__ hist) {
+  const TamTensor& d = T[blockIdx.x];
+  if (!(d.flags & TAM_FLAG_COSTATE)) return;
+  uint32_t* h = hist + (uint64_t)blockIdx.x * 4096u;
+  for (uint32_t i = threadIdx.x; i < 4096u; i += TAM_WG) h[i] = 0u;
+  if (threadIdx.x == 0) {
+    TamSel z;
+    z.kmin = 0xffffffffu;
+    z.kmax = 0u;
+    z.prefix[0] = z.prefix[1] = 0u;
+    z.k[0] = d.k_lo;
+    z.k[1] = d.k_hi;
+    z.mask = 0u;
+    z.top = 32;  // not started
+    sel[blockIdx.x] = z;
+  }
+}
+
+__global__ __launch_bounds__(TAM_WG) void tam_k_sel_minmax(const TamTensor* __restrict__ T, int nT,
+                                                           const float* __restrict__ ratios, TamSel* __restrict__ sel) {
+  __shared__ uint32_t red[2][TAM_WG / 64];
+  const int t = tam_slice_tensor(T, nT, blockIdx.x);
+  const TamTensor& d = T[t];
+  const uint32_t k0 = (blockIdx.x - d.slice0) * TAM_SLICE;
+  const uint32_t k1 = k0 + TAM_SLICE < d.nb ? k0 + TAM_SLICE : d.nb;
+  uint32_t kmin = 0xffffffffu, kmax = 0u;
+  tam_slice_keys((const uint32_t*)(ratios + d.ratio_off), k0, k1, [&](uint32_t k) {
+    kmin = k < kmin ? k : kmin;
+    kmax = k > kmax ? k : kmax;
+  });
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const uint32_t a = __shfl_xor(kmin, off), b = __shfl_xor(kmax, off);
+    kmin = a < kmin ? a : kmin;
+    kmax = b > kmax ? b : kmax;
+  }
+  if ((threadIdx.x & 63u) == 0) {
+    red[0][threadIdx.x >> 6] = kmin;
+    red[1][threadIdx.x >> 6] = kmax;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < TAM_WG / 64; ++w) {
+      kmin = red[0][w] < kmin ? red[0][w] : kmin;
+      kmax = red[1][w] > kmax ? red[1][w] : kmax;
+    }
+    atomicMin(&sel[t].kmin, kmin);
+    atomicMax(&sel[t].kmax, kmax);
+  }
+}
+
+// Current digit window of a tensor: bits [sh, top] below the fixed prefix.
+__device__ __forceinline__ void tam_sel_window(int top, int& sh, uint32_t& dmask) {
+  sh = top >= 10 ? top - 10 : 0;
+  dmask = (1u << (top - sh + 1)) - 1u;
+}
+
+__global__ __launch_bounds__(TAM_WG) void tam_k_sel_hist(const TamTensor* __restrict__ T, int nT,
+                                                         const float* __restrict__ ratios,
+                                                         const TamSel* __restrict__ sel, uint32_t* __restrict__ hist) {
+  __shared__ uint32_t h[2][2048];
+  const int t = tam_slice_tensor(T, nT, blockIdx.x);
+  const TamTensor& d = T[t];
+  const TamSel st = sel[t];
+  uint32_t prefix[2], mask;
+  int top;
+  if (st.top == 32) {
+    tam_sel_start(st, prefix, mask, top);
+  } else {
+    prefix[0] = st.prefix[0];
+    prefix[1] = st.prefix[1];
+    mask = st.mask;
+    top = st.top;
+  }
+  if (top < 0) return;  // uniform over the workgroup
+  int sh;
+  uint32_t dmask;
+  tam_sel_window(top, sh, dmask);
+  for (uint32_t i = threadIdx.x; i < 4096u; i += TAM_WG) (&h[0][0])[i] = 0u;
+  __syncthreads();
+  const uint32_t p0 = prefix[0], p1 = prefix[1];
+  const bool same = p0 == p1;
+  const uint32_t k0 = (blockIdx.x - d.slice0) * TAM_SLICE;
+  const uint32_t k1 = k0 + TAM_SLICE < d.nb ? k0 + TAM_SLICE : d.nb;
+  tam_slice_keys((const uint32_t*)(ratios + d.ratio_off), k0, k1, [&](uint32_t key) {
+    const uint32_t dg = (key >> sh) & dmask;
+    const uint32_t km = key & mask;
+    if (km == p0) atomicAdd(&h[0][dg], 1u);
+    if (!same && km == p1) atomicAdd(&h[1][dg], 1u);
+  });
+  __syncthreads();
+  uint32_t* gh = hist + (uint64_t)t * 4096u;
+  for (uint32_t i = threadIdx.x; i < 4096u; i += TAM_WG) {
+    const uint32_t c = (&h[0][0])[i];
+    if (c) atomicAdd(&gh[i], c);
+  }
+}
 
 // Exclusive prefix sum over the 1024 threads of the workgroup.
 __device__ uint32_t tam_wg_excl_scan(uint32_t v, uint32_t* wsum) {
@@ -950,111 +1107,86 @@ __device__ uint32_t tam_wg_excl_scan(uint32_t v, uint32_t* wsum) {
   return r;
 }
 
-__device__ uint32_t tam_wg_reduce_u32(uint32_t v, bool is_max, uint32_t* wsum) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    const uint32_t t = __shfl_xor(v, off);
-    v = is_max ? (t > v ? t : v) : (t < v ? t : v);
-  }
-  if ((threadIdx.x & 63u) == 0) wsum[threadIdx.x >> 6] = v;
-  __syncthreads();
-  uint32_t r = wsum[0];
-  for (int i = 1; i < TAM_SEL_WG / 64; ++i) r = is_max ? (wsum[i] > r ? wsum[i] : r) : (wsum[i] < r ? wsum[i] : r);
-  __syncthreads();
-  return r;
-}
-
-// Visits every key of a tensor: 16 keys per thread in flight (four uint4
-// loads), then the < 4 trailing keys.  `keys` is 16-byte aligned.
-template <typename F>
-__device__ __forceinline__ void tam_for_keys(const uint32_t* __restrict__ keys, uint32_t nb, F&& f) {
-  const uint4* k4 = (const uint4*)keys;
-  const uint32_t n4 = nb >> 2;
-  const uint32_t stride = TAM_SEL_WG;
-  uint32_t i = threadIdx.x;
-  for (; i + 3 * stride < n4; i += 4 * stride) {
-    const uint4 a = k4[i], b = k4[i + stride], c = k4[i + 2 * stride], e = k4[i + 3 * stride];
-    f(a.x); f(a.y); f(a.z); f(a.w);
-    f(b.x); f(b.y); f(b.z); f(b.w);
-    f(c.x); f(c.y); f(c.z); f(c.w);
-    f(e.x); f(e.y); f(e.z); f(e.w);
-  }
-  for (; i < n4; i += stride) {
-    const uint4 a = k4[i];
-    f(a.x); f(a.y); f(a.z); f(a.w);
-  }
-  const uint32_t t = (n4 << 2) + threadIdx.x;
-  if (t < nb) f(keys[t]);
-}
-
-__global__ __launch_bounds__(TAM_SEL_WG) void tam_k3_select(const TamTensor* __restrict__ T,
-                                                            const float* __restrict__ alpha_new,
-                                                            const float* __restrict__ ratios) {
-  __shared__ uint32_t hist[2][2048];
+__global__ __launch_bounds__(TAM_SEL_WG) void tam_k_sel_pick(const TamTensor* __restrict__ T, TamSel* __restrict__ sel,
+                                                             uint32_t* __restrict__ hist) {
   __shared__ uint32_t wsum[TAM_SEL_WG / 64];
-  __shared__ uint32_t sel_prefix[2], sel_k[2];
+  __shared__ uint32_t new_prefix[2], new_k[2];
   const TamTensor& d = T[blockIdx.x];
   if (!(d.flags & TAM_FLAG_COSTATE)) return;
-  const uint32_t nb = d.nb;
-  const uint32_t* keys = (const uint32_t*)(ratios + d.ratio_off);
-  const uint32_t tid = threadIdx.x;
-  uint32_t kmin = 0xffffffffu, kmax = 0u;
-  tam_for_keys(keys, nb, [&](uint32_t k) {
-    kmin = k < kmin ? k : kmin;
-    kmax = k > kmax ? k : kmax;
-  });
-  kmin = tam_wg_reduce_u32(kmin, false, wsum);
-  kmax = tam_wg_reduce_u32(kmax, true, wsum);
-  if (tid == 0) {
-    sel_prefix[0] = sel_prefix[1] = kmin;  // bits above the highest differing bit
-    sel_k[0] = d.k_lo;
-    sel_k[1] = d.k_hi;
+  const TamSel st = sel[blockIdx.x];
+  uint32_t prefix[2], mask;
+  int top;
+  if (st.top == 32) {
+    tam_sel_start(st, prefix, mask, top);
+  } else {
+    prefix[0] = st.prefix[0];
+    prefix[1] = st.prefix[1];
+    mask = st.mask;
+    top = st.top;
   }
-  __syncthreads();
-  const uint32_t diff = kmin ^ kmax;
-  int top = diff ? 31 - __builtin_clz(diff) : -1;  // highest differing bit
-  uint32_t mask = top >= 31 ? 0u : (0xffffffffu << (top + 1));
-  if (top >= 0 && tid == 0) sel_prefix[0] = sel_prefix[1] = kmin & mask;
-  __syncthreads();
-  while (top >= 0) {
-    const int sh = top >= 10 ? top - 10 : 0;
-    const uint32_t dmask = (1u << (top - sh + 1)) - 1u;
-    for (uint32_t i = tid; i < 2048; i += TAM_SEL_WG) hist[0][i] = hist[1][i] = 0;
+  const uint32_t tid = threadIdx.x;
+  if (top >= 0) {
+    int sh;
+    uint32_t dmask;
+    tam_sel_window(top, sh, dmask);
+    uint32_t* gh = hist + (uint64_t)blockIdx.x * 4096u;
+    const bool same = prefix[0] == prefix[1];
+    if (tid < 2) {
+      new_prefix[tid] = prefix[tid];
+      new_k[tid] = st.k[tid];
+    }
     __syncthreads();
-    const uint32_t p0 = sel_prefix[0], p1 = sel_prefix[1];
-    const bool same = p0 == p1;
-    tam_for_keys(keys, nb, [&](uint32_t key) {
-      const uint32_t dg = (key >> sh) & dmask;
-      const uint32_t km = key & mask;
-      if (km == p0) atomicAdd(&hist[0][dg], 1u);
-      if (!same && km == p1) atomicAdd(&hist[1][dg], 1u);
-    });
-    __syncthreads();
-    for (int t = 0; t < 2; ++t) {
-      const int src = same ? 0 : t;
-      const uint32_t h0 = hist[src][2 * tid], h1 = hist[src][2 * tid + 1];
+    for (int r = 0; r < 2; ++r) {
+      const uint32_t* hr = gh + (same ? 0u : (uint32_t)r) * 2048u;
+      const uint32_t h0 = hr[2 * tid], h1 = hr[2 * tid + 1];
       const uint32_t pre = tam_wg_excl_scan(h0 + h1, wsum);
-      const uint32_t k = sel_k[t];
-      __syncthreads();
+      const uint32_t k = st.k[r];
       if (k >= pre && k < pre + h0 + h1) {
         const bool first = k < pre + h0;
         const uint32_t digit = 2 * tid + (first ? 0u : 1u);
-        sel_k[t] = k - (first ? pre : pre + h0);
-        sel_prefix[t] |= digit << sh;
+        new_k[r] = k - (first ? pre : pre + h0);
+        new_prefix[r] = prefix[r] | (digit << sh);
       }
       __syncthreads();
     }
-    mask |= dmask << sh;
-    top = sh - 1;
+    // clear the histogram for the next pass
+    for (uint32_t i = tid; i < 4096u; i += TAM_SEL_WG) gh[i] = 0u;
+    if (tid == 0) {
+      TamSel o = st;
+      o.prefix[0] = new_prefix[0];
+      o.prefix[1] = new_prefix[1];
+      o.k[0] = new_k[0];
+      o.k[1] = new_k[1];
+      o.mask = mask | (dmask << sh);
+      o.top = sh - 1;
+      sel[blockIdx.x] = o;
+    }
+  } else if (tid == 0 && st.top == 32) {
+    TamSel o = st;  // every key equal: both thresholds are that key
+    o.prefix[0] = prefix[0];
+    o.prefix[1] = prefix[1];
+    o.mask = mask;
+    o.top = -1;
+    sel[blockIdx.x] = o;
   }
-  const float tau0 = tam_u2f(sel_prefix[0]);
-  const float tau1 = tam_u2f(sel_prefix[1]);
+}
+
+__global__ __launch_bounds__(TAM_WG) void tam_k_sel_labels(const TamTensor* __restrict__ T, int nT,
+                                                           const float* __restrict__ alpha_new,
+                                                           const float* __restrict__ ratios,
+                                                           const TamSel* __restrict__ sel) {
+  const int t = tam_slice_tensor(T, nT, blockIdx.x);
+  const TamTensor& d = T[t];
+  const float tau0 = tam_u2f(sel[t].prefix[0]);
+  const float tau1 = tam_u2f(sel[t].prefix[1]);
+  const uint32_t k0 = (blockIdx.x - d.slice0) * TAM_SLICE;
+  const uint32_t k1 = k0 + TAM_SLICE < d.nb ? k0 + TAM_SLICE : d.nb;
   const float* r = ratios + d.ratio_off;
-  for (uint32_t i = tid; i < nb; i += TAM_SEL_WG) {
-    const float x = r[i];
-    d.labels[i] = x >= tau1 ? (uint8_t)2 : (x >= tau0 ? (uint8_t)1 : (uint8_t)0);
+  for (uint32_t i = k0 + threadIdx.x; i < k1; i += TAM_WG) {
+    const float x = tam_g(r)[i];
+    tam_g(d.labels)[i] = x >= tau1 ? (uint8_t)2 : (x >= tau0 ? (uint8_t)1 : (uint8_t)0);
   }
-  if (tid == 0) *d.alpha = alpha_new[blockIdx.x];
+  if (blockIdx.x == d.slice0 && threadIdx.x == 0) tam_g(d.alpha)[0] = alpha_new[t];
 }
 
 // ---------------------------------------------------------------------------
@@ -1131,7 +1263,7 @@ const char* tam_last_error(void) { return tam_err_buf; }
 int tam_prepare(TamTensor* tensors, int n_tensors, TamStepInfo* info) {
   tam_err_buf[0] = 0;
   if (!info || n_tensors < 0 || (n_tensors > 0 && !tensors)) return tam_fail(TAM_E_INVALID, "%snull argument", "");
-  uint64_t tiles = 0, ratio_blocks = 0, chunks = 0;
+  uint64_t tiles = 0, ratio_blocks = 0, chunks = 0, slices = 0;
   uint32_t ncs = 0;
   for (int i = 0; i < n_tensors; ++i) {
     TamTensor& t = tensors[i];
@@ -1165,8 +1297,11 @@ int tam_prepare(TamTensor* tensors, int n_tensors, TamStepInfo* info) {
     t.ntiles = (uint32_t)nt;
     t.tile0 = (uint32_t)tiles;
     t.chunk0 = (uint32_t)chunks;
+    t.slice0 = (uint32_t)slices;
+    t.sel_pad = 0;
     tiles += nt;
     chunks += tam_alpha_chunks(t.flags, t.ntiles);
+    slices += tam_sel_slices(t.flags, t.nb);
     if (tiles > 0xffffffffull) return tam_fail(TAM_E_INVALID, "%stoo many tiles", "", 0);
   }
   memset(info, 0, sizeof(*info));
@@ -1174,6 +1309,7 @@ int tam_prepare(TamTensor* tensors, int n_tensors, TamStepInfo* info) {
   info->total_tiles = (uint32_t)tiles;
   info->n_costate = ncs;
   info->total_chunks = (uint32_t)chunks;
+  info->total_slices = (uint32_t)slices;
   info->ratio_blocks = ratio_blocks;
   uint64_t off = 0;
   info->off_partials = off;
@@ -1184,6 +1320,10 @@ int tam_prepare(TamTensor* tensors, int n_tensors, TamStepInfo* info) {
   off = tam_align_up(off + ratio_blocks * sizeof(float), 256);
   info->off_chunks = off;
   off = tam_align_up(off + chunks * sizeof(double2), 256);
+  info->off_sel = off;
+  off = tam_align_up(off + (uint64_t)n_tensors * sizeof(TamSel), 256);
+  info->off_hist = off;
+  off = tam_align_up(off + (uint64_t)n_tensors * 4096u * sizeof(uint32_t), 256);
   info->ws_bytes = off;
   return TAM_OK;
 }
@@ -1201,6 +1341,8 @@ static int tam_launch_pass(int pass, const TamTensor* d_tensors, const TamStepIn
   float* alpha_new = (float*)(ws + info->off_alpha);
   float* ratios = (float*)(ws + info->off_ratios);
   double2* chunk_sums = (double2*)(ws + info->off_chunks);
+  TamSel* sel = (TamSel*)(ws + info->off_sel);
+  uint32_t* hist = (uint32_t*)(ws + info->off_hist);
   const int cus = tam_device_cus();
   const uint32_t grid = info->total_tiles < (uint32_t)(cus * 8) ? info->total_tiles : (uint32_t)(cus * 8);
   switch (pass) {
@@ -1219,8 +1361,20 @@ static int tam_launch_pass(int pass, const TamTensor* d_tensors, const TamStepIn
                          info->total_tiles, alpha_new, ratios);
       break;
     default:
-      hipLaunchKernelGGL(tam_k3_select, dim3(info->n_tensors), dim3(TAM_SEL_WG), 0, s, d_tensors, alpha_new,
-                         ratios);
+      hipLaunchKernelGGL(tam_k_sel_reset, dim3(info->n_tensors), dim3(TAM_WG), 0, s, d_tensors, sel, hist);
+      TAM_HIP_CHECK(hipGetLastError());
+      hipLaunchKernelGGL(tam_k_sel_minmax, dim3(info->total_slices), dim3(TAM_WG), 0, s, d_tensors,
+                         info->n_tensors, ratios, sel);
+      TAM_HIP_CHECK(hipGetLastError());
+      for (int r = 0; r < 3; ++r) {  // 11-bit digits: at most three rounds fix all 32 bits
+        hipLaunchKernelGGL(tam_k_sel_hist, dim3(info->total_slices), dim3(TAM_WG), 0, s, d_tensors,
+                           info->n_tensors, ratios, sel, hist);
+        TAM_HIP_CHECK(hipGetLastError());
+        hipLaunchKernelGGL(tam_k_sel_pick, dim3(info->n_tensors), dim3(TAM_SEL_WG), 0, s, d_tensors, sel, hist);
+        TAM_HIP_CHECK(hipGetLastError());
+      }
+      hipLaunchKernelGGL(tam_k_sel_labels, dim3(info->total_slices), dim3(TAM_WG), 0, s, d_tensors,
+                         info->n_tensors, alpha_new, ratios, sel);
       break;
   }
   TAM_HIP_CHECK(hipGetLastError());
