@@ -251,7 +251,10 @@ __host__ __device__ __attribute__((noinline)) inline float tam_logf_slow(int e, 
 }
 
 // Correctly rounded logf for every fp32 input (log(+0) = -inf, negative -> NaN).
-TAM_HD float tam_logf(float x) {
+// `tab(j)` returns entry j of the 129-entry table (a kernel may pass a copy
+// held in LDS); tam_logf below reads the constant-memory copy.
+template <typename Tab>
+TAM_HD float tam_logf_with(float x, Tab tab) {
   uint32_t u = tam_f2u(x);
   if (u >= 0x7f800000u || u == 0u) {
     if (u == 0x7f800000u) return x;                   // +inf
@@ -269,7 +272,7 @@ TAM_HD float tam_logf(float x) {
   const uint32_t mant = u & 0x7fffffu;
   const int j = (int)((mant + (1u << 15)) >> 16);  // round(128*(m-1)), 0..128
   const double m = (double)tam_u2f(mant | 0x3f800000u);
-  const TamLogEntry t = tam_log_entry(j);
+  const TamLogEntry t = tab(j);
   const double r = __builtin_fma(m, (double)t.c, -1.0);  // exact, |r| <= 2^-8
   // log1p(r) ~ r + r^2 * (-1/2 + r/3 - r^2/4 + r^3/5 - r^4/6)
   double q = __builtin_fma(r, -0x1.5555555555555p-3, 0x1.999999999999ap-3);
@@ -286,6 +289,10 @@ TAM_HD float tam_logf(float x) {
   const float b = (float)(y + err);
   if (a == b) return a;
   return tam_logf_slow(e, j, r);
+}
+
+TAM_HD float tam_logf(float x) {
+  return tam_logf_with(x, [](int j) { return tam_log_entry(j); });
 }
 
 // ---------------------------------------------------------------------------
@@ -321,8 +328,10 @@ __host__ __device__ __attribute__((noinline)) inline float tam_expf_slow(double 
   return tam_dd_to_f32(y);
 }
 
-// Correctly rounded expf for every fp32 input.
-TAM_HD float tam_expf(float xf) {
+// Correctly rounded expf for every fp32 input.  `tab(j)` returns entry j of the
+// 64-entry table of 2^(j/64) as double-doubles.
+template <typename Tab>
+TAM_HD float tam_expf_with(float xf, Tab tab) {
   if (tam_isnan(xf)) return xf;
   if (xf > 89.0f) return tam_inf();
   if (xf < -104.0f) return 0.0f;
@@ -337,7 +346,7 @@ TAM_HD float tam_expf(float xf) {
   q = __builtin_fma(r, q, 0.5);
   const double em1 = __builtin_fma(r * r, q, r);
   const int k = (int)kd;
-  const TamDD t = tam_exp_entry(k & 63);
+  const TamDD t = tab(k & 63);
   const double y = t.hi + __builtin_fma(t.hi, em1, t.lo);
   const double z = y * tam_pow2i(k >> 6);
   const double err = z * 0x1p-49;
@@ -345,4 +354,8 @@ TAM_HD float tam_expf(float xf) {
   const float b = (float)(z + err);
   if (a == b) return a;
   return tam_expf_slow(x, kd);
+}
+
+TAM_HD float tam_expf(float xf) {
+  return tam_expf_with(xf, [](int j) { return tam_exp_entry(j); });
 }

@@ -369,9 +369,28 @@ __device__ __forceinline__ TamVIn tam_v_load(const TamTensor& d, const TamWave& 
   return r;
 }
 
+// LDS copies of the log / exp tables (the correctly rounded log and exp of a
+// block read them at LDS latency instead of a dependent global load).
+struct TamLdsTabs {
+  TamLogEntry log[129];
+  TamDD exp[64];
+};
+__device__ __forceinline__ void tam_lds_tabs_fill(TamLdsTabs* t) {
+  for (uint32_t i = threadIdx.x; i < 129u; i += blockDim.x) t->log[i] = tam_log_tab_d[i];
+  for (uint32_t i = threadIdx.x; i < 64u; i += blockDim.x) t->exp[i] = tam_exp_tab_d[i];
+  __syncthreads();
+}
+__device__ __forceinline__ float tam_logf_lds(float x, const TamLdsTabs* t) {
+  return tam_logf_with(x, [t](int j) { return t->log[j]; });
+}
+__device__ __forceinline__ float tam_expf_lds(float x, const TamLdsTabs* t) {
+  return tam_expf_with(x, [t](int j) { return t->exp[j]; });
+}
+
 template <bool FULL>
 __device__ __forceinline__ void tam_vpath(const TamTensor& d, const TamWave& W, const TamVIn& vin, const float* g,
-                                          float* v, float* lutw, uint32_t seed_lo, uint32_t seed_hi) {
+                                          float* v, float* lutw, const TamLdsTabs* tabs, uint32_t seed_lo,
+                                          uint32_t seed_hi) {
   const uint32_t bits = d.v_bits;
   const uint32_t nbk = 1u << bits;
   const float fnb = (float)nbk;
@@ -387,7 +406,7 @@ __device__ __forceinline__ void tam_vpath(const TamTensor& d, const TamWave& W, 
   if (nbk <= 16u) {
     // every lane of the wave takes part in the permutes
     const uint32_t k = W.l16 & (nbk - 1u);
-    const float val = tam_expf(lmin0 + ((float)k + 0.5f) * inv_nbk * span0);
+    const float val = tam_expf_lds(lmin0 + ((float)k + 0.5f) * inv_nbk * span0, tabs);
     const uint32_t row = W.lane & 48u;
 #pragma unroll
     for (int i = 0; i < TAM_EPL; ++i) {
@@ -400,7 +419,7 @@ __device__ __forceinline__ void tam_vpath(const TamTensor& d, const TamWave& W, 
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const uint32_t k = W.l16 + 16u * (uint32_t)j;
-      tab[k] = tam_expf(lmin0 + ((float)k + 0.5f) * inv_nbk * span0);
+      tab[k] = tam_expf_lds(lmin0 + ((float)k + 0.5f) * inv_nbk * span0, tabs);
     }
     tam_wave_lds_sync();
 #pragma unroll
@@ -408,7 +427,7 @@ __device__ __forceinline__ void tam_vpath(const TamTensor& d, const TamWave& W, 
     tam_wave_lds_sync();  // the next tile rewrites the table
   } else {
 #pragma unroll
-    for (int i = 0; i < TAM_EPL; ++i) vo[i] = tam_expf(lmin0 + ((float)idx[i] + 0.5f) * inv_nbk * span0);
+    for (int i = 0; i < TAM_EPL; ++i) vo[i] = tam_expf_lds(lmin0 + ((float)idx[i] + 0.5f) * inv_nbk * span0, tabs);
   }
   // EMA (quantize.py:259-270) and the clamp of :275.  A clamped v is
   // positive or NaN: the block extremes are taken on bit patterns (NaN
@@ -432,7 +451,7 @@ __device__ __forceinline__ void tam_vpath(const TamTensor& d, const TamWave& W, 
   kmx = tam_block_umax(kmx);
   nan_seen = tam_block_or(nan_seen);
   // correctly rounded logs of the extremes: even lanes log(vmin), odd lanes log(vmax)
-  const float lx = tam_logf(tam_u2f((W.l16 & 1u) ? kmx : kmn));
+  const float lx = tam_logf_lds(tam_u2f((W.l16 & 1u) ? kmx : kmn), tabs);
   const float ly = tam_dppf<TAM_DPP_XOR1>(lx);
   float lmn = (W.l16 & 1u) ? ly : lx;
   float lmx = (W.l16 & 1u) ? lx : ly;
@@ -498,7 +517,7 @@ __device__ __forceinline__ void tam_vpath(const TamTensor& d, const TamWave& W, 
 #pragma unroll
     for (int i = 0; i < TAM_EPL; ++i) {
       if (amb & (1u << i)) {
-        const float l = tam_logf(vc[i]);
+        const float l = tam_logf_lds(vc[i], tabs);
         const float c = ((l - lmn) / sp) * fnb;  // quantize.py:284-285
         const float f = __builtin_floorf(c);
         const float fr = c - f;
@@ -615,7 +634,8 @@ __device__ __forceinline__ bool tam_quarter_full(const TamTensor& d, uint32_t wq
 // m.g over the quarter's 4 blocks (pairwise: blocks, then pairs of blocks).
 template <uint32_t DT, bool FULL>
 __device__ __forceinline__ void tam_k1_quarter(const TamTensor& d, uint32_t wq, uint32_t lane, float* lutw,
-                                               uint32_t seed_lo, uint32_t seed_hi, double2* __restrict__ part) {
+                                               const TamLdsTabs* tabs, uint32_t seed_lo, uint32_t seed_hi,
+                                               double2* __restrict__ part) {
   const TamWave W = tam_wave(d, wq, lane, FULL);
   const bool costate = (d.flags & TAM_FLAG_COSTATE) != 0;
   const bool compress_v = (d.flags & TAM_FLAG_COMPRESS_V) != 0;
@@ -664,7 +684,7 @@ __device__ __forceinline__ void tam_k1_quarter(const TamTensor& d, uint32_t wq, 
 
   // ---- second moment --------------------------------------------------
   if (compress_v) {
-    tam_vpath<FULL>(d, W, vin, g, v, lutw, seed_lo, seed_hi);
+    tam_vpath<FULL>(d, W, vin, g, v, lutw, tabs, seed_lo, seed_hi);
   } else if (FULL || W.bvalid) {
     // fp32 exp_avg_sq (optimizer.py:166): v = fma(fl((1-b2)*g), g, fl(v*b2))
     float es[TAM_EPL];
@@ -689,6 +709,8 @@ __global__ __launch_bounds__(TAM_WG) __attribute__((amdgpu_waves_per_eu(4, 4))) 
                                                       uint32_t total_tiles, uint32_t seed_lo,
                                                       uint32_t seed_hi, double2* __restrict__ partials) {
   __shared__ float lut[TAM_WG / 64][4 * 64];
+  __shared__ TamLdsTabs tabs;
+  tam_lds_tabs_fill(&tabs);
   const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
   float* lutw = lut[wave];
   int ti = tam_find_tensor(T, nT, blockIdx.x);
@@ -700,16 +722,16 @@ __global__ __launch_bounds__(TAM_WG) __attribute__((amdgpu_waves_per_eu(4, 4))) 
     const bool full = tam_quarter_full(d, wq);
     switch (d.dtype) {
       case TAM_DTYPE_BF16:
-        if (full) tam_k1_quarter<TAM_DTYPE_BF16, true>(d, wq, lane, lutw, seed_lo, seed_hi, part);
-        else tam_k1_quarter<TAM_DTYPE_BF16, false>(d, wq, lane, lutw, seed_lo, seed_hi, part);
+        if (full) tam_k1_quarter<TAM_DTYPE_BF16, true>(d, wq, lane, lutw, &tabs, seed_lo, seed_hi, part);
+        else tam_k1_quarter<TAM_DTYPE_BF16, false>(d, wq, lane, lutw, &tabs, seed_lo, seed_hi, part);
         break;
       case TAM_DTYPE_F16:
-        if (full) tam_k1_quarter<TAM_DTYPE_F16, true>(d, wq, lane, lutw, seed_lo, seed_hi, part);
-        else tam_k1_quarter<TAM_DTYPE_F16, false>(d, wq, lane, lutw, seed_lo, seed_hi, part);
+        if (full) tam_k1_quarter<TAM_DTYPE_F16, true>(d, wq, lane, lutw, &tabs, seed_lo, seed_hi, part);
+        else tam_k1_quarter<TAM_DTYPE_F16, false>(d, wq, lane, lutw, &tabs, seed_lo, seed_hi, part);
         break;
       default:
-        if (full) tam_k1_quarter<TAM_DTYPE_F32, true>(d, wq, lane, lutw, seed_lo, seed_hi, part);
-        else tam_k1_quarter<TAM_DTYPE_F32, false>(d, wq, lane, lutw, seed_lo, seed_hi, part);
+        if (full) tam_k1_quarter<TAM_DTYPE_F32, true>(d, wq, lane, lutw, &tabs, seed_lo, seed_hi, part);
+        else tam_k1_quarter<TAM_DTYPE_F32, false>(d, wq, lane, lutw, &tabs, seed_lo, seed_hi, part);
         break;
     }
   }
