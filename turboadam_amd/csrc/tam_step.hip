@@ -387,10 +387,19 @@ __device__ __forceinline__ float tam_expf_lds(float x, const TamLdsTabs* t) {
   return tam_expf_with(x, [t](int j) { return t->exp[j]; });
 }
 
+// Block extremes of the clamped v: bit patterns of the minimum and maximum
+// (valid elements only) and whether any is NaN.
+struct TamVExt {
+  uint32_t kmn, kmx, nan_seen;
+};
+
+// First half: decode, EMA, clamp, block extremes.  The parameter update runs
+// between the halves (it needs v, not the new indices), so that p, m and v are
+// no longer live during the re-quantisation.
 template <bool FULL>
-__device__ __forceinline__ void tam_vpath(const TamTensor& d, const TamWave& W, const TamVIn& vin, const float* g,
-                                          float* v, float* lutw, const TamLdsTabs* tabs, uint32_t seed_lo,
-                                          uint32_t seed_hi) {
+__device__ __forceinline__ TamVExt tam_vpath_a(const TamTensor& d, const TamWave& W, const TamVIn& vin,
+                                               const float* g, float* v, float* vc, float* lutw,
+                                               const TamLdsTabs* tabs) {
   const uint32_t bits = d.v_bits;
   const uint32_t nbk = 1u << bits;
   const float fnb = (float)nbk;
@@ -432,7 +441,6 @@ __device__ __forceinline__ void tam_vpath(const TamTensor& d, const TamWave& W, 
   // EMA (quantize.py:259-270) and the clamp of :275.  A clamped v is
   // positive or NaN: the block extremes are taken on bit patterns (NaN
   // patterns order above +inf and are handled by nan_seen).
-  float vc[TAM_EPL];
   uint32_t kmn = 0x7f800000u, kmx = 0u;
   uint32_t nan_seen = 0;
 #pragma unroll
@@ -447,9 +455,21 @@ __device__ __forceinline__ void tam_vpath(const TamTensor& d, const TamWave& W, 
       kmx = __builtin_elementwise_max(kmx, tam_f2u(vc[i]));
     }
   }
-  kmn = tam_block_umin(kmn);
-  kmx = tam_block_umax(kmx);
-  nan_seen = tam_block_or(nan_seen);
+  TamVExt x;
+  x.kmn = tam_block_umin(kmn);
+  x.kmx = tam_block_umax(kmx);
+  x.nan_seen = tam_block_or(nan_seen);
+  return x;
+}
+
+// Second half: logs of the extremes, scales, stochastic re-quantisation.
+template <bool FULL>
+__device__ __forceinline__ void tam_vpath_b(const TamTensor& d, const TamWave& W, const float* vc, TamVExt x,
+                                            const TamLdsTabs* tabs, uint32_t seed_lo, uint32_t seed_hi) {
+  const uint32_t nbk = 1u << d.v_bits;
+  const float fnb = (float)nbk;
+  const bool bvalid = FULL || W.bvalid;
+  const uint32_t kmn = x.kmn, kmx = x.kmx, nan_seen = x.nan_seen;
   // correctly rounded logs of the extremes: even lanes log(vmin), odd lanes log(vmax)
   const float lx = tam_logf_lds(tam_u2f((W.l16 & 1u) ? kmx : kmn), tabs);
   const float ly = tam_dppf<TAM_DPP_XOR1>(lx);
@@ -683,8 +703,10 @@ __device__ __forceinline__ void tam_k1_quarter(const TamTensor& d, uint32_t wq, 
   }
 
   // ---- second moment --------------------------------------------------
+  float vc[TAM_EPL];
+  TamVExt vx = {0u, 0u, 0u};
   if (compress_v) {
-    tam_vpath<FULL>(d, W, vin, g, v, lutw, tabs, seed_lo, seed_hi);
+    vx = tam_vpath_a<FULL>(d, W, vin, g, v, vc, lutw, tabs);
   } else if (FULL || W.bvalid) {
     // fp32 exp_avg_sq (optimizer.py:166): v = fma(fl((1-b2)*g), g, fl(v*b2))
     float es[TAM_EPL];
@@ -701,6 +723,9 @@ __device__ __forceinline__ void tam_k1_quarter(const TamTensor& d, uint32_t wq, 
     if (DT == TAM_DTYPE_F32) tam_st8_f32<FULL>((float*)d.param, W.e0, W.nv, p);
     else tam_st8_bits<FULL>(d.param, W.e0, W.nv, pb);
   }
+
+  // ---- re-quantisation of v -------------------------------------------
+  if (compress_v) tam_vpath_b<FULL>(d, W, vc, vx, tabs, seed_lo, seed_hi);
 }
 
 // Persistent workgroups stride over the tiles; the four waves of a workgroup
