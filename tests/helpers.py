@@ -106,8 +106,21 @@ def make_grads(rng, sizes, dts, sigmas, drifts=None, drift_scale=0.3):
     return out
 
 
-def run_side_by_side(sizes, dts, steps, seed=0, check_every=1, shapes=None, grad_none=None, **kw):
-    """Step the GPU optimizer and the oracle on identical inputs; return mismatch list."""
+def _at_offset(t: torch.Tensor, offset: int) -> torch.Tensor:
+    """A copy of t that starts `offset` elements into a larger allocation."""
+    if not offset:
+        return t
+    base = torch.zeros(t.numel() + offset, dtype=t.dtype, device=t.device)
+    view = base[offset:].view(t.shape)
+    view.copy_(t)
+    return view
+
+
+def run_side_by_side(sizes, dts, steps, seed=0, check_every=1, shapes=None, grad_none=None, offset=0, **kw):
+    """Step the GPU optimizer and the oracle on identical inputs; return mismatch list.
+
+    offset > 0 places every parameter and gradient that many elements into a
+    larger allocation (unaligned arrays)."""
     from turboadam_amd import TurboAdam
 
     dev = torch.device("cuda:0")
@@ -115,7 +128,8 @@ def run_side_by_side(sizes, dts, steps, seed=0, check_every=1, shapes=None, grad
     shapes = shapes or [(n,) for n in sizes]
     init = [to_bits((rng.standard_normal(n) * 0.02).astype(np.float32), dts[i]) for i, n in enumerate(sizes)]
     o_params = [a.copy() for a in init]
-    g_params = [torch.nn.Parameter(to_torch(a, dts[i], shapes[i], dev)) for i, a in enumerate(init)]
+    g_params = [torch.nn.Parameter(_at_offset(to_torch(a, dts[i], shapes[i], dev), offset))
+                for i, a in enumerate(init)]
     opt = TurboAdam(g_params, **kw)
     opt.philox_seed = 1234567 + seed
     orc = O.OracleTurboAdam(o_params, dtypes=dts, seed=1234567 + seed, **kw)
@@ -127,7 +141,7 @@ def run_side_by_side(sizes, dts, steps, seed=0, check_every=1, shapes=None, grad
         if grad_none is not None:
             grads = [None if grad_none(s, i) else g for i, g in enumerate(grads)]
         for i, p in enumerate(g_params):
-            p.grad = None if grads[i] is None else to_torch(grads[i], dts[i], shapes[i], dev)
+            p.grad = None if grads[i] is None else _at_offset(to_torch(grads[i], dts[i], shapes[i], dev), offset)
         opt.step()
         orc.step(grads)
         if (s + 1) % check_every == 0 or s == steps - 1:

@@ -175,3 +175,12 @@ def test_large_tensors_multi_workgroup_reductions():
     log("bf16 5.0M + 2.1M elements, 3 steps (multi-chunk alpha, multi-slice selection)")
     sizes = [5_000_000 + 333, 8192 * 128 * 2 + 777]
     _check(run_side_by_side(sizes, [BF16] * 2, steps=3, lr=1e-3, weight_decay=0.1))
+
+
+@pytest.mark.parametrize("dt", [F32, BF16])
+def test_unaligned_parameter_views(dt):
+    # parameters and gradients one element past a 16-byte boundary: every quarter
+    # takes the bounds-checked path
+    log(f"unaligned views dtype={dt}")
+    sizes = [70_000, 4096 + 5, 300]
+    _check(run_side_by_side(sizes, [dt] * 3, steps=4, offset=1, lr=1e-3, weight_decay=0.05))

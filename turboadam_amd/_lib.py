@@ -75,7 +75,7 @@ class TamStepInfo(ctypes.Structure):
         ("n_costate", ctypes.c_uint32),
         ("total_chunks", ctypes.c_uint32),
         ("total_slices", ctypes.c_uint32),
-        ("pad0", ctypes.c_uint32),
+        ("dtype_mask", ctypes.c_uint32),
         ("ratio_blocks", ctypes.c_uint64),
         ("off_partials", ctypes.c_uint64),
         ("off_alpha", ctypes.c_uint64),

@@ -728,11 +728,15 @@ __device__ __forceinline__ void tam_k1_quarter(const TamTensor& d, uint32_t wq, 
   if (compress_v) tam_vpath_b<FULL>(d, W, vc, vx, tabs, seed_lo, seed_hi);
 }
 
-// Persistent workgroups stride over the tiles; the four waves of a workgroup
+// Full quarters (inside the tensor, aligned arrays) of one parameter dtype:
+// persistent workgroups stride over the tiles; the four waves of a workgroup
 // take the four quarters of each tile and never synchronise with each other.
-__global__ __launch_bounds__(TAM_WG) __attribute__((amdgpu_waves_per_eu(4, 4))) void tam_k1_main(const TamTensor* __restrict__ T, int nT,
-                                                      uint32_t total_tiles, uint32_t seed_lo,
-                                                      uint32_t seed_hi, double2* __restrict__ partials) {
+// One kernel per dtype holds only that dtype's full-quarter code, so the
+// register budget admits five waves per SIMD for 16-bit parameters.
+template <uint32_t DT>
+__device__ __forceinline__ void tam_k1_full_body(const TamTensor* __restrict__ T, int nT, uint32_t total_tiles,
+                                                 uint32_t seed_lo, uint32_t seed_hi,
+                                                 double2* __restrict__ partials) {
   __shared__ float lut[TAM_WG / 64][4 * 64];
   __shared__ TamLdsTabs tabs;
   tam_lds_tabs_fill(&tabs);
@@ -742,21 +746,47 @@ __global__ __launch_bounds__(TAM_WG) __attribute__((amdgpu_waves_per_eu(4, 4))) 
   for (uint32_t tile = blockIdx.x; tile < total_tiles; tile += gridDim.x) {
     while (tile >= T[ti].tile0 + T[ti].ntiles) ++ti;
     const TamTensor& d = T[ti];
+    if (d.dtype != DT) continue;  // uniform over the workgroup
     const uint32_t wq = (tile - d.tile0) * 4u + wave;  // quarter tile within the tensor
-    double2* part = partials + (uint64_t)tile * 4u + wave;
-    const bool full = tam_quarter_full(d, wq);
+    if (!tam_quarter_full(d, wq)) continue;           // left to tam_k1_tail
+    tam_k1_quarter<DT, true>(d, wq, lane, lutw, &tabs, seed_lo, seed_hi, partials + (uint64_t)tile * 4u + wave);
+  }
+}
+
+#define TAM_K1_FULL_KERNEL(NAME, DT, WAVES)                                                                  \
+  __global__ __launch_bounds__(TAM_WG) __attribute__((amdgpu_waves_per_eu(WAVES, WAVES))) void NAME(       \
+      const TamTensor* __restrict__ T, int nT, uint32_t total_tiles, uint32_t seed_lo, uint32_t seed_hi,   \
+      double2* __restrict__ partials) {                                                                    \
+    tam_k1_full_body<DT>(T, nT, total_tiles, seed_lo, seed_hi, partials);                                  \
+  }
+TAM_K1_FULL_KERNEL(tam_k1_main_bf16, TAM_DTYPE_BF16, 5)
+TAM_K1_FULL_KERNEL(tam_k1_main_f16, TAM_DTYPE_F16, 5)
+TAM_K1_FULL_KERNEL(tam_k1_main_f32, TAM_DTYPE_F32, 4)
+
+// The quarters that are not full: the last (at most four) quarters of each
+// tensor, or every quarter of a tensor whose parameter or gradient is not
+// 16-byte aligned.  One workgroup per tensor; wave w takes every fourth quarter.
+__global__ __launch_bounds__(TAM_WG) void tam_k1_tail(const TamTensor* __restrict__ T, uint32_t seed_lo,
+                                                      uint32_t seed_hi, double2* __restrict__ partials) {
+  __shared__ float lut[TAM_WG / 64][4 * 64];
+  __shared__ TamLdsTabs tabs;
+  tam_lds_tabs_fill(&tabs);
+  const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+  const TamTensor& d = T[blockIdx.x];
+  const bool aligned = (((uintptr_t)d.param | (uintptr_t)d.grad) & 15u) == 0;
+  const uint32_t nq = d.ntiles * 4u;
+  const uint32_t first = aligned ? (uint32_t)(d.n / (4u * TAM_BLOCK_SIZE)) : 0u;  // full quarters precede
+  for (uint32_t wq = first + wave; wq < nq; wq += 4u) {
+    double2* part = partials + (uint64_t)d.tile0 * 4u + wq;
     switch (d.dtype) {
       case TAM_DTYPE_BF16:
-        if (full) tam_k1_quarter<TAM_DTYPE_BF16, true>(d, wq, lane, lutw, &tabs, seed_lo, seed_hi, part);
-        else tam_k1_quarter<TAM_DTYPE_BF16, false>(d, wq, lane, lutw, &tabs, seed_lo, seed_hi, part);
+        tam_k1_quarter<TAM_DTYPE_BF16, false>(d, wq, lane, lut[wave], &tabs, seed_lo, seed_hi, part);
         break;
       case TAM_DTYPE_F16:
-        if (full) tam_k1_quarter<TAM_DTYPE_F16, true>(d, wq, lane, lutw, &tabs, seed_lo, seed_hi, part);
-        else tam_k1_quarter<TAM_DTYPE_F16, false>(d, wq, lane, lutw, &tabs, seed_lo, seed_hi, part);
+        tam_k1_quarter<TAM_DTYPE_F16, false>(d, wq, lane, lut[wave], &tabs, seed_lo, seed_hi, part);
         break;
       default:
-        if (full) tam_k1_quarter<TAM_DTYPE_F32, true>(d, wq, lane, lutw, &tabs, seed_lo, seed_hi, part);
-        else tam_k1_quarter<TAM_DTYPE_F32, false>(d, wq, lane, lutw, &tabs, seed_lo, seed_hi, part);
+        tam_k1_quarter<TAM_DTYPE_F32, false>(d, wq, lane, lut[wave], &tabs, seed_lo, seed_hi, part);
         break;
     }
   }
@@ -1311,6 +1341,7 @@ int tam_prepare(TamTensor* tensors, int n_tensors, TamStepInfo* info) {
   tam_err_buf[0] = 0;
   if (!info || n_tensors < 0 || (n_tensors > 0 && !tensors)) return tam_fail(TAM_E_INVALID, "%snull argument", "");
   uint64_t tiles = 0, ratio_blocks = 0, chunks = 0, slices = 0;
+  uint32_t dtype_mask = 0;
   uint32_t ncs = 0;
   for (int i = 0; i < n_tensors; ++i) {
     TamTensor& t = tensors[i];
@@ -1343,6 +1374,7 @@ int tam_prepare(TamTensor* tensors, int n_tensors, TamStepInfo* info) {
     t.nb = (uint32_t)nb;
     t.ntiles = (uint32_t)nt;
     t.tile0 = (uint32_t)tiles;
+    dtype_mask |= 1u << t.dtype;
     t.chunk0 = (uint32_t)chunks;
     t.slice0 = (uint32_t)slices;
     t.sel_pad = 0;
@@ -1357,6 +1389,7 @@ int tam_prepare(TamTensor* tensors, int n_tensors, TamStepInfo* info) {
   info->n_costate = ncs;
   info->total_chunks = (uint32_t)chunks;
   info->total_slices = (uint32_t)slices;
+  info->dtype_mask = dtype_mask;
   info->ratio_blocks = ratio_blocks;
   uint64_t off = 0;
   info->off_partials = off;
@@ -1394,8 +1427,18 @@ static int tam_launch_pass(int pass, const TamTensor* d_tensors, const TamStepIn
   const uint32_t grid = info->total_tiles < (uint32_t)(cus * 8) ? info->total_tiles : (uint32_t)(cus * 8);
   switch (pass) {
     case 0:
-      hipLaunchKernelGGL(tam_k1_main, dim3(grid), dim3(TAM_WG), 0, s, d_tensors, info->n_tensors,
-                         info->total_tiles, (uint32_t)seed, (uint32_t)(seed >> 32), partials);
+      if (info->dtype_mask & (1u << TAM_DTYPE_BF16))
+        hipLaunchKernelGGL(tam_k1_main_bf16, dim3(grid), dim3(TAM_WG), 0, s, d_tensors, info->n_tensors,
+                           info->total_tiles, (uint32_t)seed, (uint32_t)(seed >> 32), partials);
+      if (info->dtype_mask & (1u << TAM_DTYPE_F16))
+        hipLaunchKernelGGL(tam_k1_main_f16, dim3(grid), dim3(TAM_WG), 0, s, d_tensors, info->n_tensors,
+                           info->total_tiles, (uint32_t)seed, (uint32_t)(seed >> 32), partials);
+      if (info->dtype_mask & (1u << TAM_DTYPE_F32))
+        hipLaunchKernelGGL(tam_k1_main_f32, dim3(grid), dim3(TAM_WG), 0, s, d_tensors, info->n_tensors,
+                           info->total_tiles, (uint32_t)seed, (uint32_t)(seed >> 32), partials);
+      TAM_HIP_CHECK(hipGetLastError());
+      hipLaunchKernelGGL(tam_k1_tail, dim3(info->n_tensors), dim3(TAM_WG), 0, s, d_tensors, (uint32_t)seed,
+                         (uint32_t)(seed >> 32), partials);
       break;
     case 1:
       hipLaunchKernelGGL(tam_k_alpha_chunks, dim3(info->total_chunks), dim3(TAM_WG), 0, s, d_tensors,
