@@ -156,6 +156,57 @@ int tam_v_dequantize(const uint8_t* v_idx, const uint16_t* v_scales, uint64_t n,
 int tam_philox_uniforms(uint32_t tensor_id, uint32_t step, uint64_t seed,
                         uint64_t count, float* out, void* stream);
 
+/* ---- standalone helpers: the reference's public functions, one tensor per
+ * call, with the step's arithmetic.  Device pointers, caller's stream. ---- */
+
+/* decode_blocks (reference costate.py:261-324): m_out[i] = fl(alpha*g[i]) +
+ * s_b*sign_i for n elements (g of g_dtype; alpha a device float).  With
+ * ema != 0 the EMA of CoStateManager.update (costate.py:416) follows:
+ * m_out = fl(beta1*m_hat) + fl(one_minus_beta1*g); has_state == 0 means
+ * m_hat = 0 and the CoState arrays are not read. */
+int tam_costate_decode(const uint8_t* labels, const uint8_t* signs, const float* norms, const uint16_t* amp,
+                       const float* alpha, const void* g, uint32_t g_dtype, uint64_t n, int has_state, int ema,
+                       float beta1, float one_minus_beta1, float* m_out, void* stream);
+
+/* decompose (reference costate.py:22-43): *alpha (device float) = fl(mg)/fl(gg)
+ * with the step's fp64 pairwise dot products (0 when gg == 0), delta =
+ * fl(m - fl(alpha*g)).  m, g fp32[n].  Workspace: tam_decompose_workspace(n)
+ * bytes of device memory. */
+size_t tam_decompose_workspace(uint64_t n);
+int tam_decompose(const float* m, const float* g, uint64_t n, float* alpha, float* delta, void* workspace,
+                  size_t ws_bytes, void* stream);
+
+/* compute_block_ratios (reference costate.py:51-86): ratios[b] =
+ * ||delta_b|| / ||m_b|| (fp64 pairwise block norms), 0 where ||m_b|| == 0. */
+int tam_block_ratios(const float* delta, const float* m, uint64_t n, float* ratios, void* stream);
+
+/* compute_thresholds (reference costate.py:94-118): taus[0], taus[1] (device
+ * floats) = the k_lo-th and k_hi-th smallest ratios (NaN last).  ratios is
+ * 16-byte aligned; workspace: tam_thresholds_workspace(nb) bytes. */
+size_t tam_thresholds_workspace(uint64_t nb);
+int tam_thresholds(const float* ratios, uint64_t nb, uint32_t k_lo, uint32_t k_hi, float* taus, void* workspace,
+                   size_t ws_bytes, void* stream);
+
+/* classify_blocks (reference costate.py:126-149) with taus[0], taus[1] on the device. */
+int tam_classify(const float* ratios, uint64_t nb, const float* taus, uint8_t* labels, void* stream);
+
+/* encode_blocks (reference costate.py:213-258, _pack_signs :157-182): block
+ * norms of delta, fp16 amplitudes norm/f32(sqrt(128)), sign bits (MSB first). */
+int tam_costate_encode(const float* delta, uint64_t n, uint8_t* signs, float* norms, uint16_t* amp, void* stream);
+
+/* fused_v_update (reference quantize.py:222-299) for one tensor: decode, EMA,
+ * re-quantisation with the step's Philox draws for (tensor_id, step, seed);
+ * v_out receives v (fp32, n values).  The outputs may be the inputs. */
+int tam_fused_v_update(const uint8_t* idx_in, const uint16_t* scales_in, const void* g, uint32_t g_dtype, uint64_t n,
+                       uint32_t v_bits, float beta2, float one_minus_beta2, uint32_t tensor_id, uint32_t step,
+                       uint64_t seed, uint8_t* idx_out, uint16_t* scales_out, float* v_out, void* stream);
+
+/* quantize_logscale_nbits (reference quantize.py:126-180) of v (n_padded, a
+ * multiple of 128): fp16 (log_min, log_max) per block and indices, rounded
+ * down (stochastic == 0) or stochastically with the Philox draws. */
+int tam_v_quantize(const float* v, uint64_t n_padded, uint32_t v_bits, int stochastic, uint32_t tensor_id,
+                   uint32_t step, uint64_t seed, uint8_t* idx, uint16_t* scales, void* stream);
+
 /* Self-check of the device arithmetic: out[i] = f(in[i]) with f selected by
  * `fn` (0 log, 1 exp, 2 f32->f16->f32, 3 f32->bf16->f32 in software, 4 sqrt,
  * 5 f32->bf16->f32 by the hardware conversion).  No counterpart in

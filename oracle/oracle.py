@@ -74,6 +74,10 @@ def lib():
         L.or_decode_blocks.argtypes = [_VP, _VP, _VP, _VP, ctypes.c_float, _VP, ctypes.c_uint64, ctypes.c_float, _VP]
         L.or_fused_v_update.argtypes = [_VP, _VP, _VP, ctypes.c_uint64, ctypes.c_int, ctypes.c_float,
                                         ctypes.c_float, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint64, _VP]
+        L.or_quantize_logscale.argtypes = [_VP, ctypes.c_uint64, ctypes.c_int, ctypes.c_int, ctypes.c_uint32,
+                                           ctypes.c_uint32, ctypes.c_uint64, _VP, _VP]
+        L.or_costate_update.argtypes = [_VP, ctypes.c_uint64, ctypes.c_float, ctypes.c_float, ctypes.c_float,
+                                        ctypes.c_uint64, ctypes.c_uint64, ctypes.c_int, _VP, _VP, _VP, _VP, _VP, _VP]
         L.or_struct_size.restype = ctypes.c_size_t
         if L.or_struct_size() != ctypes.sizeof(OrTensor):
             raise RuntimeError("oracle struct layout mismatch")

@@ -346,6 +346,52 @@ void or_fused_v_update(uint8_t* idx, uint16_t* scales, const float* g, uint64_t 
   }
 }
 
+/* quantize_logscale_nbits, reference quantize.py:126-180, on v already padded
+ * to whole blocks (npad a multiple of 128).  Min / max run over every value
+ * of the block (NaN propagates); stochastic != 0 draws u as the step does. */
+void or_quantize_logscale(const float* v, uint64_t npad, int bits, int stochastic, uint32_t tid, uint32_t step,
+                          uint64_t seed, uint8_t* idx, uint16_t* scales) {
+  uint64_t nb = npad / OR_BS;
+  float nbk = (float)(1u << bits);
+  float top = (float)((double)(1u << bits) - 0.001);  /* clamp(0, n_buckets - 0.001), :179 */
+  float lg[OR_BS];
+  for (uint64_t b = 0; b < nb; ++b) {
+    float lmin = INFINITY, lmax = -INFINITY;
+    int nan_seen = 0;
+    for (int j = 0; j < OR_BS; ++j) {
+      float x = v[b * OR_BS + j];
+      float c = x < 1e-38f ? 1e-38f : x;              /* clamp(min=1e-38), :155 */
+      lg[j] = or_logf(c);
+      if (lg[j] != lg[j]) nan_seen = 1;
+      else {
+        if (lg[j] < lmin) lmin = lg[j];
+        if (lg[j] > lmax) lmax = lg[j];
+      }
+    }
+    if (nan_seen) lmin = lmax = NAN;                   /* min / max propagate NaN, :157-158 */
+    scales[2 * b] = or_f32_to_f16(lmin);               /* :159 */
+    scales[2 * b + 1] = or_f32_to_f16(lmax);
+    float sp = lmax - lmin;
+    if (sp < 1e-10f) sp = 1e-10f;                      /* :161 */
+    for (int j = 0; j < OR_BS; ++j) {
+      uint64_t i = b * OR_BS + j;
+      float c = ((lg[j] - lmin) / sp) * nbk;           /* :162-163 */
+      float q;
+      if (stochastic) {                                /* :165-175 */
+        float f = floorf(c);
+        float u = or_uniform(i, tid, step, seed);
+        q = f + (u < c - f ? 1.0f : 0.0f);
+        if (q < 0.0f) q = 0.0f;
+        if (q > nbk - 1.0f) q = nbk - 1.0f;
+      } else {                                         /* :177-178 */
+        q = c < 0.0f ? 0.0f : c;
+        if (q > top) q = top;
+      }
+      idx[i] = (q != q) ? 0 : (uint8_t)q;
+    }
+  }
+}
+
 /* ------------------------------------------------------ one parameter's step */
 typedef struct OrTensor {
   void* param;

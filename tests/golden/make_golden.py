@@ -179,14 +179,70 @@ def run_reference(ref_mod, name, case):
     return out, meta
 
 
+# Function-level fixtures of the 1Q quantizer (quantize.py:126-180 and
+# oneq.py:13-48), which the step reaches only through its closed-form first
+# state.  Inputs are stored with the outputs.
+Q_CASES = {
+    "q_det_b4": dict(n=128 * 64, bits=4, stochastic=False, fn="quantize"),
+    "q_det_b2": dict(n=128 * 64, bits=2, stochastic=False, fn="quantize"),
+    "q_sto_b3": dict(n=128 * 64, bits=3, stochastic=True, fn="quantize", tid=3, step=4),
+    "q_sto_b8": dict(n=128 * 64, bits=8, stochastic=True, fn="quantize", tid=7, step=2),
+    "compress_b4": dict(n=5000, bits=4, stochastic=False, fn="compress"),
+}
+
+
+def q_case_input(name, case):
+    """Positive values spread over ~35 e-folds, some exact zeros (clamped to 1e-38)."""
+    z = I.normal(case["n"], 77 + sorted(Q_CASES).index(name), 0)
+    v = np.exp(-20.0 + 5.0 * z).astype(np.float32)
+    v[::97] = 0.0
+    return v
+
+
+def run_reference_quantize(ref_mod, name, case):
+    import importlib
+
+    quant = importlib.import_module(ref_mod.__name__ + ".quantize")
+    oneq = importlib.import_module(ref_mod.__name__ + ".oneq")
+    v = q_case_input(name, case)
+    rl = PhiloxRandLike(SR_SEED)
+    orig = torch.rand_like
+    try:
+        torch.rand_like = rl
+        if case["fn"] == "quantize":
+            if case["stochastic"]:
+                rl.queue = [(case["tid"], case["step"])]
+            idx, scales, _ = quant.quantize_logscale_nbits(torch.from_numpy(v), n_bits=case["bits"], block_size=128,
+                                                           stochastic_round=case["stochastic"])
+        else:
+            st = oneq.compress_v_logscale(torch.from_numpy(v), n_bits=case["bits"], block_size=128,
+                                          stochastic_round=False)
+            idx, scales = st["indices"], st["scales"]
+    finally:
+        torch.rand_like = orig
+    out = {"v": v, "indices": np_of(idx.to(torch.uint8)), "scales": np_of(scales.to(torch.float16))}
+    meta = {"name": name, **case, "sr_seed": SR_SEED, "torch": torch.__version__, "threads": torch.get_num_threads()}
+    return out, meta
+
+
 def main():
     ref_root = sys.argv[1] if len(sys.argv) > 1 else "/root/reference"
+    only = sys.argv[2:]  # optional case names
     sys.path.insert(0, os.path.join(ref_root, "src"))
     import turboadam as ref_mod  # the reference package
 
     torch.set_num_threads(1)
     for name, case in CASES.items():
+        if only and name not in only:
+            continue
         out, meta = run_reference(ref_mod, name, case)
+        path = os.path.join(HERE, f"golden_{name}.npz")
+        np.savez_compressed(path, meta=np.array(json.dumps(meta)), **out)
+        print(f"{name}: {os.path.getsize(path)} bytes", flush=True)
+    for name, case in Q_CASES.items():
+        if only and name not in only:
+            continue
+        out, meta = run_reference_quantize(ref_mod, name, case)
         path = os.path.join(HERE, f"golden_{name}.npz")
         np.savez_compressed(path, meta=np.array(json.dumps(meta)), **out)
         print(f"{name}: {os.path.getsize(path)} bytes", flush=True)

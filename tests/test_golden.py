@@ -176,3 +176,24 @@ def test_exact_and_faithful_differ_only_by_ties(name):
     print(name, json.dumps(total))
     # parameters move by at most a few ulps per step (sqrt and division inputs agree to the last bit or two)
     assert total["param_rel"] <= 1e-6
+
+
+@pytest.mark.parametrize("name", list(MG.Q_CASES))
+def test_oracle_quantizer_matches_reference(name):
+    """or_quantize_logscale (and the compress_v_logscale padding) against the
+    reference's quantize_logscale_nbits / compress_v_logscale outputs, including
+    the stochastic branch fed the same Philox draws."""
+    case = MG.Q_CASES[name]
+    z = np.load(os.path.join(HERE, "golden", f"golden_{name}.npz"))
+    v = z["v"]
+    if case["fn"] == "compress":  # oneq.py:31-34: pad with max(min(v), 1e-38)
+        n = v.size
+        npad = (n + 127) // 128 * 128
+        v = np.concatenate([v, np.full(npad - n, np.float32(max(float(v.min()), 1e-38)), np.float32)])
+    npad = v.size
+    idx = np.empty(npad, np.uint8)
+    sc = np.empty(2 * (npad // 128), np.uint16)
+    O.lib().or_quantize_logscale(O.ptr(v), npad, case["bits"], int(case["stochastic"]), case.get("tid", 0),
+                                 case.get("step", 1), MG.SR_SEED, O.ptr(idx), O.ptr(sc))
+    assert np.array_equal(idx, z["indices"])
+    assert np.array_equal(sc, z["scales"].reshape(-1))

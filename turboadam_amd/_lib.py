@@ -17,6 +17,9 @@ TAM_DTYPE_F32 = 0
 TAM_DTYPE_BF16 = 1
 TAM_DTYPE_F16 = 2
 
+# torch dtype of a parameter / gradient -> TAM_DTYPE_*
+DTYPES = {torch.float32: TAM_DTYPE_F32, torch.bfloat16: TAM_DTYPE_BF16, torch.float16: TAM_DTYPE_F16}
+
 TAM_FLAG_COSTATE = 0x1
 TAM_FLAG_COMPRESS_V = 0x2
 TAM_FLAG_HAS_STATE = 0x4
@@ -108,6 +111,31 @@ SIGNATURES = {
         [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_uint64, _VP, _VP],
     ),
     "tam_math_eval": (ctypes.c_int, [ctypes.c_int, _VP, _VP, ctypes.c_uint64, _VP]),
+    "tam_costate_decode": (
+        ctypes.c_int,
+        [_VP, _VP, _VP, _VP, _VP, _VP, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_int, ctypes.c_int, ctypes.c_float,
+         ctypes.c_float, _VP, _VP],
+    ),
+    "tam_decompose_workspace": (ctypes.c_size_t, [ctypes.c_uint64]),
+    "tam_decompose": (ctypes.c_int, [_VP, _VP, ctypes.c_uint64, _VP, _VP, _VP, ctypes.c_size_t, _VP]),
+    "tam_block_ratios": (ctypes.c_int, [_VP, _VP, ctypes.c_uint64, _VP, _VP]),
+    "tam_thresholds_workspace": (ctypes.c_size_t, [ctypes.c_uint64]),
+    "tam_thresholds": (
+        ctypes.c_int,
+        [_VP, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint32, _VP, _VP, ctypes.c_size_t, _VP],
+    ),
+    "tam_classify": (ctypes.c_int, [_VP, ctypes.c_uint64, _VP, _VP, _VP]),
+    "tam_costate_encode": (ctypes.c_int, [_VP, ctypes.c_uint64, _VP, _VP, _VP, _VP]),
+    "tam_fused_v_update": (
+        ctypes.c_int,
+        [_VP, _VP, _VP, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_float, ctypes.c_float,
+         ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint64, _VP, _VP, _VP, _VP],
+    ),
+    "tam_v_quantize": (
+        ctypes.c_int,
+        [_VP, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_int, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint64, _VP,
+         _VP, _VP],
+    ),
 }
 
 _lib = None

@@ -1267,6 +1267,288 @@ __global__ __launch_bounds__(TAM_WG) void tam_k_sel_labels(const TamTensor* __re
 }
 
 // ---------------------------------------------------------------------------
+// standalone helpers (the reference's public functions, one tensor per call)
+// ---------------------------------------------------------------------------
+// They reuse the step's per-quarter code on a TamTensor built in registers
+// (or, for the reductions, one built in the caller's workspace by
+// tam_k_make_desc), so their arithmetic is the step's arithmetic.
+
+// Quarter grid for n elements: a 256-thread workgroup covers one tile (four
+// quarters); wave w of workgroup t takes quarter 4t + w.
+__host__ __device__ __forceinline__ uint32_t tam_tiles_of(uint64_t n) {
+  const uint64_t nb = (n + TAM_BLOCK_SIZE - 1) / TAM_BLOCK_SIZE;
+  return (uint32_t)((nb + TAM_BPT - 1) / TAM_BPT);
+}
+
+__device__ __forceinline__ TamTensor tam_local_desc(uint64_t n) {
+  TamTensor d;
+  memset(&d, 0, sizeof(d));
+  d.n = n;
+  d.nb = (uint32_t)((n + TAM_BLOCK_SIZE - 1) / TAM_BLOCK_SIZE);
+  d.ntiles = tam_tiles_of(n);
+  d.sqrt_block = 0x1.6a09e6p+3f;  // f32(sqrt(128))
+  return d;
+}
+
+// decode_blocks (costate.py:261-324), optionally followed by the EMA of
+// CoStateManager.update (costate.py:416): m = fl(b1*m_hat) + fl(ob1*g).
+// has_state == 0 gives m_hat = 0 (costate.py:405-407).
+__global__ __launch_bounds__(TAM_WG) void tam_k_decode(const uint8_t* __restrict__ labels,
+                                                       const uint8_t* __restrict__ signs,
+                                                       const float* __restrict__ norms,
+                                                       const uint16_t* __restrict__ amp,
+                                                       const float* __restrict__ alpha, const void* __restrict__ g,
+                                                       uint32_t g_dtype, uint64_t n, int has_state, int ema,
+                                                       float beta1, float one_minus_beta1, float* __restrict__ out) {
+  TamTensor d = tam_local_desc(n);
+  d.labels = (uint8_t*)labels;
+  d.signs = (uint8_t*)signs;
+  d.norms = (float*)norms;
+  d.amp = (uint16_t*)amp;
+  d.flags = has_state ? TAM_FLAG_HAS_STATE : 0u;
+  d.beta1 = ema ? beta1 : 0.0f;
+  d.one_minus_beta1 = ema ? one_minus_beta1 : 0.0f;
+  const uint32_t wq = blockIdx.x * 4u + (threadIdx.x >> 6);
+  const TamWave W = tam_wave(d, wq, threadIdx.x & 63u, false);
+  if (!W.bvalid) return;
+  float gv[TAM_EPL], m[TAM_EPL];
+  switch (g_dtype) {
+    case TAM_DTYPE_BF16: tam_ld8<TAM_DTYPE_BF16, false>(g, W.e0, W.nv, gv); break;
+    case TAM_DTYPE_F16: tam_ld8<TAM_DTYPE_F16, false>(g, W.e0, W.nv, gv); break;
+    default: tam_ld8<TAM_DTYPE_F32, false>(g, W.e0, W.nv, gv); break;
+  }
+  const TamCsIn cs = tam_cs_load<false>(d, W);
+  const float a = has_state ? alpha[0] : 0.0f;
+  if (ema) {
+    tam_costate_m<false>(d, W, cs, a, gv, m);
+  } else {
+    // m_hat alone: fl(alpha*g) + s_b*sign (costate.py:317-323)
+    const float sph = cs.nrm / d.sqrt_block;
+    const float sb = cs.label == 1u ? sph : (cs.label == 2u ? tam_f16_to_f32((uint16_t)cs.amp) : 0.0f);
+#pragma unroll
+    for (int i = 0; i < TAM_EPL; ++i) {
+      const float sd = tam_u2f((tam_f2u(sb) & 0x7fffffffu) | ((cs.byte << (24 + i)) & 0x80000000u));
+      m[i] = has_state ? a * gv[i] + sd : 0.0f;
+    }
+  }
+  tam_st8_f32<false>(out, W.e0, W.nv, m);
+}
+
+// Quarter partials of g.g and m.g (fp32 inputs), as pass 1 forms them.
+__global__ __launch_bounds__(TAM_WG) void tam_k_dot_quarters(const float* __restrict__ m, const float* __restrict__ g,
+                                                             uint64_t n, double2* __restrict__ partials) {
+  const TamTensor d = tam_local_desc(n);
+  const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+  const uint32_t wq = blockIdx.x * 4u + wave;
+  const TamWave W = tam_wave(d, wq, lane, false);
+  float mv[TAM_EPL], gv[TAM_EPL];
+  tam_ld8<TAM_DTYPE_F32, false>(m, W.e0, W.nv, mv);
+  tam_ld8<TAM_DTYPE_F32, false>(g, W.e0, W.nv, gv);
+  double gg[TAM_EPL], mg[TAM_EPL];
+#pragma unroll
+  for (int i = 0; i < TAM_EPL; ++i) {
+    const bool ok = (uint32_t)i < W.nv;
+    gg[i] = ok ? (double)gv[i] * (double)gv[i] : 0.0;
+    mg[i] = ok ? (double)mv[i] * (double)gv[i] : 0.0;
+  }
+  const double sgg = tam_block_sum(tam_pair8(gg));
+  const double smg = tam_block_sum(tam_pair8(mg));
+  const double tgg = (tam_readlane_d(sgg, 0) + tam_readlane_d(sgg, 16)) +
+                     (tam_readlane_d(sgg, 32) + tam_readlane_d(sgg, 48));
+  const double tmg = (tam_readlane_d(smg, 0) + tam_readlane_d(smg, 16)) +
+                     (tam_readlane_d(smg, 32) + tam_readlane_d(smg, 48));
+  if (lane == 0) tam_g((TamD2*)(partials + wq))[0] = TamD2{tgg, tmg};
+}
+
+// One CoState descriptor for the alpha and selection kernels.
+__global__ void tam_k_make_desc(TamTensor* __restrict__ out, uint64_t n, uint32_t nb, uint32_t k_lo, uint32_t k_hi) {
+  TamTensor d = tam_local_desc(n);
+  d.nb = nb;
+  d.flags = TAM_FLAG_COSTATE;
+  d.k_lo = k_lo;
+  d.k_hi = k_hi;
+  *out = d;
+}
+
+// delta = fl(m - fl(alpha*g)) (costate.py:42)
+__global__ void tam_k_delta(const float* __restrict__ m, const float* __restrict__ g, uint64_t n,
+                            const float* __restrict__ alpha, float* __restrict__ delta) {
+  const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float a = alpha[0];
+  delta[i] = m[i] - a * g[i];
+}
+
+// Per-block fp64 norm of x (zero padded) in all 16 lanes of the block.
+__device__ __forceinline__ double tam_block_sq(const float* x, const TamWave& W) {
+  float v[TAM_EPL];
+  tam_ld8<TAM_DTYPE_F32, false>(x, W.e0, W.nv, v);
+  double q[TAM_EPL];
+#pragma unroll
+  for (int i = 0; i < TAM_EPL; ++i) q[i] = (double)v[i] * (double)v[i];
+  return tam_block_sum(tam_pair8(q));
+}
+
+// compute_block_ratios (costate.py:51-86): r = ||delta_b|| / ||m_b||, 0 where ||m_b|| = 0
+__global__ __launch_bounds__(TAM_WG) void tam_k_ratios(const float* __restrict__ delta, const float* __restrict__ m,
+                                                       uint64_t n, float* __restrict__ ratios) {
+  const TamTensor d = tam_local_desc(n);
+  const TamWave W = tam_wave(d, blockIdx.x * 4u + (threadIdx.x >> 6), threadIdx.x & 63u, false);
+  const double sd = tam_block_sq(delta, W), sm = tam_block_sq(m, W);
+  if (W.bvalid && W.l16 == 0) {
+    const float nd = (float)__builtin_sqrt(sd), nm = (float)__builtin_sqrt(sm);
+    ratios[W.b] = nm == 0.0f ? 0.0f : nd / nm;
+  }
+}
+
+// encode_blocks (costate.py:213-258): block norms, fp16 amplitudes, sign bits
+__global__ __launch_bounds__(TAM_WG) void tam_k_encode(const float* __restrict__ delta, uint64_t n,
+                                                       uint8_t* __restrict__ signs, float* __restrict__ norms,
+                                                       uint16_t* __restrict__ amp) {
+  const TamTensor d = tam_local_desc(n);
+  const TamWave W = tam_wave(d, blockIdx.x * 4u + (threadIdx.x >> 6), threadIdx.x & 63u, false);
+  float v[TAM_EPL];
+  tam_ld8<TAM_DTYPE_F32, false>(delta, W.e0, W.nv, v);
+  double q[TAM_EPL];
+  uint32_t sbyte = 0;
+#pragma unroll
+  for (int i = 0; i < TAM_EPL; ++i) {
+    q[i] = (double)v[i] * (double)v[i];
+    sbyte |= (((uint32_t)i < W.nv && v[i] < 0.0f) ? 1u : 0u) << (7 - i);  // costate.py:170-181
+  }
+  const double sd = tam_block_sum(tam_pair8(q));
+  if (!W.bvalid) return;
+  if (W.nv > 0) signs[W.e0 >> 3] = (uint8_t)sbyte;
+  if (W.l16 == 0) {
+    const float nd = (float)__builtin_sqrt(sd);
+    norms[W.b] = nd;
+    amp[W.b] = tam_f32_to_f16(nd / d.sqrt_block);
+  }
+}
+
+// classify_blocks (costate.py:126-149), thresholds read from taus[0], taus[1]
+__global__ void tam_k_classify(const float* __restrict__ ratios, uint64_t nb, const float* __restrict__ taus,
+                               uint8_t* __restrict__ labels) {
+  const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= nb) return;
+  const float x = ratios[i], tau0 = taus[0], tau1 = taus[1];
+  labels[i] = x >= tau1 ? (uint8_t)2 : (x >= tau0 ? (uint8_t)1 : (uint8_t)0);
+}
+
+// The two thresholds of a finished selection.
+__global__ void tam_k_sel_taus(const TamSel* __restrict__ sel, float* __restrict__ taus) {
+  taus[0] = tam_u2f(sel[0].prefix[0]);
+  taus[1] = tam_u2f(sel[0].prefix[1]);
+}
+
+// fused_v_update (quantize.py:222-299) for one tensor: the 1Q half of pass 1
+// without the first moment and the parameter update; v (fp32, n values) is
+// written out.  idx_out / scales_out may equal idx_in / scales_in.
+__global__ __launch_bounds__(TAM_WG) void tam_k_fused_v(const uint8_t* idx_in, const uint16_t* scales_in,
+                                                        const void* __restrict__ g, uint32_t g_dtype, uint64_t n,
+                                                        uint32_t bits, float beta2, float one_minus_beta2,
+                                                        uint32_t tensor_id, uint32_t step, uint32_t seed_lo,
+                                                        uint32_t seed_hi, uint8_t* idx_out, uint16_t* scales_out,
+                                                        float* __restrict__ v_out) {
+  __shared__ float lut[TAM_WG / 64][4 * 64];
+  __shared__ TamLdsTabs tabs;
+  tam_lds_tabs_fill(&tabs);
+  const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+  TamTensor d = tam_local_desc(n);
+  d.v_idx = (uint8_t*)idx_in;
+  d.v_scales = (uint16_t*)scales_in;
+  d.v_bits = bits;
+  d.beta2 = beta2;
+  d.one_minus_beta2 = one_minus_beta2;
+  d.tensor_id = tensor_id;
+  d.step = step;
+  const TamWave W = tam_wave(d, blockIdx.x * 4u + wave, lane, false);
+  float gv[TAM_EPL], v[TAM_EPL], vc[TAM_EPL];
+  switch (g_dtype) {
+    case TAM_DTYPE_BF16: tam_ld8<TAM_DTYPE_BF16, false>(g, W.e0, W.nv, gv); break;
+    case TAM_DTYPE_F16: tam_ld8<TAM_DTYPE_F16, false>(g, W.e0, W.nv, gv); break;
+    default: tam_ld8<TAM_DTYPE_F32, false>(g, W.e0, W.nv, gv); break;
+  }
+  const TamVIn vin = tam_v_load<false>(d, W);
+  const TamVExt x = tam_vpath_a<false>(d, W, vin, gv, v, vc, lut[wave], &tabs);
+  if (W.bvalid) tam_st8_f32<false>(v_out, W.e0, W.nv, v);
+  d.v_idx = idx_out;
+  d.v_scales = scales_out;
+  tam_vpath_b<false>(d, W, vc, x, &tabs, seed_lo, seed_hi);
+}
+
+// quantize_logscale_nbits (quantize.py:126-180) of a padded positive tensor:
+// per-block fp16 (log_min, log_max) over all of the block's values, and
+// indices trunc(clamp(c, 0, 2^bits - 0.001)) (deterministic) or
+// floor(c) + (u < frac(c)) clamped (stochastic, Philox draws as in the step),
+// c = fl(fl(log v - log_min) / max(span, 1e-10)) * 2^bits.
+__global__ __launch_bounds__(TAM_WG) void tam_k_quantize(const float* __restrict__ v, uint64_t npad, uint32_t bits,
+                                                         int stochastic, uint32_t tensor_id, uint32_t step,
+                                                         uint32_t seed_lo, uint32_t seed_hi,
+                                                         uint8_t* __restrict__ idx, uint16_t* __restrict__ scales) {
+  __shared__ TamLdsTabs tabs;
+  tam_lds_tabs_fill(&tabs);
+  const TamTensor d = tam_local_desc(npad);
+  const TamWave W = tam_wave(d, blockIdx.x * 4u + (threadIdx.x >> 6), threadIdx.x & 63u, false);
+  const float fnb = (float)(1u << bits);
+  float x[TAM_EPL], l[TAM_EPL];
+  tam_ld8<TAM_DTYPE_F32, false>(v, W.e0, W.nv, x);
+  float lmn = tam_inf(), lmx = -tam_inf();
+  uint32_t nan_seen = 0;
+#pragma unroll
+  for (int i = 0; i < TAM_EPL; ++i) {
+    const float c = x[i] < 1e-38f ? 1e-38f : x[i];  // clamp(min=1e-38), NaN stays
+    l[i] = tam_logf_lds(c, &tabs);
+    if ((uint32_t)i < W.nv) {
+      nan_seen |= tam_isnan(l[i]) ? 1u : 0u;
+      lmn = __builtin_fminf(lmn, l[i]);
+      lmx = __builtin_fmaxf(lmx, l[i]);
+    }
+  }
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {  // block min / max over the 16 lanes (minNum / maxNum; NaN tracked apart)
+    const float a = s == 0 ? tam_dppf<TAM_DPP_XOR1>(lmn) : s == 1 ? tam_dppf<TAM_DPP_XOR2>(lmn)
+                  : s == 2 ? tam_dppf<TAM_DPP_HALF_MIRROR>(lmn) : tam_dppf<TAM_DPP_MIRROR>(lmn);
+    const float b = s == 0 ? tam_dppf<TAM_DPP_XOR1>(lmx) : s == 1 ? tam_dppf<TAM_DPP_XOR2>(lmx)
+                  : s == 2 ? tam_dppf<TAM_DPP_HALF_MIRROR>(lmx) : tam_dppf<TAM_DPP_MIRROR>(lmx);
+    lmn = __builtin_fminf(lmn, a);
+    lmx = __builtin_fmaxf(lmx, b);
+  }
+  nan_seen = tam_block_or(nan_seen);
+  if (nan_seen) lmn = lmx = tam_qnan();
+  if (!W.bvalid) return;
+  if (W.l16 == 0)
+    tam_g((uint32_t*)scales)[W.b] = (uint32_t)tam_f32_to_f16(lmn) | ((uint32_t)tam_f32_to_f16(lmx) << 16);
+  float sp = lmx - lmn;
+  sp = sp < 1e-10f ? 1e-10f : sp;
+  uint32_t rw[TAM_EPL] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+  if (stochastic) {
+    const uint64_t quad0 = W.e0 >> 2;
+    const TamU4 r0 = tam_philox_quad(quad0, tensor_id, step, seed_lo, seed_hi);
+    const TamU4 r1 = tam_philox_quad(quad0 + 1, tensor_id, step, seed_lo, seed_hi);
+    rw[0] = r0.x; rw[1] = r0.y; rw[2] = r0.z; rw[3] = r0.w;
+    rw[4] = r1.x; rw[5] = r1.y; rw[6] = r1.z; rw[7] = r1.w;
+  }
+  const float top = fnb - 0.001f;  // f32(2^bits - 0.001)
+#pragma unroll
+  for (int i = 0; i < TAM_EPL; ++i) {
+    const float c = ((l[i] - lmn) / sp) * fnb;
+    float q;
+    if (stochastic) {
+      const float f = __builtin_floorf(c);
+      const float u = (float)(rw[i] >> 8) * 0x1p-24f;
+      q = f + (u < c - f ? 1.0f : 0.0f);
+      q = q < 0.0f ? 0.0f : q;
+      q = q > fnb - 1.0f ? fnb - 1.0f : q;
+    } else {
+      q = c < 0.0f ? 0.0f : c;
+      q = q > top ? top : q;
+    }
+    if ((uint32_t)i < W.nv) idx[W.e0 + i] = tam_isnan(q) ? (uint8_t)0 : (uint8_t)(uint32_t)q;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // utility kernels
 // ---------------------------------------------------------------------------
 __global__ void tam_k_v_dequantize(const uint8_t* __restrict__ idx, const uint16_t* __restrict__ scales,
@@ -1522,6 +1804,183 @@ int tam_math_eval(int fn, const float* in, float* out, uint64_t n, void* stream)
   if (n == 0) return TAM_OK;
   const uint64_t blocks = (n + 255) / 256;
   hipLaunchKernelGGL(tam_k_math_eval, dim3((uint32_t)blocks), dim3(256), 0, (hipStream_t)stream, fn, in, out, n);
+  TAM_HIP_CHECK(hipGetLastError());
+  return TAM_OK;
+}
+
+
+// ---------------------------------------------------------------------------
+// standalone helpers: host side
+// ---------------------------------------------------------------------------
+static int tam_check_dtype(uint32_t dt) {
+  return dt <= TAM_DTYPE_F16 ? TAM_OK : tam_fail(TAM_E_INVALID, "%sunknown dtype %ld", "", (long)dt);
+}
+
+int tam_costate_decode(const uint8_t* labels, const uint8_t* signs, const float* norms, const uint16_t* amp,
+                       const float* alpha, const void* g, uint32_t g_dtype, uint64_t n, int has_state, int ema,
+                       float beta1, float one_minus_beta1, float* m_out, void* stream) {
+  tam_err_buf[0] = 0;
+  if (!g || !m_out || (has_state && (!labels || !signs || !norms || !amp || !alpha)))
+    return tam_fail(TAM_E_INVALID, "%snull argument", "");
+  if (tam_check_dtype(g_dtype)) return TAM_E_INVALID;
+  if (n == 0) return TAM_OK;
+  hipLaunchKernelGGL(tam_k_decode, dim3(tam_tiles_of(n)), dim3(TAM_WG), 0, (hipStream_t)stream, labels, signs, norms,
+                     amp, alpha, g, g_dtype, n, has_state, ema, beta1, one_minus_beta1, m_out);
+  TAM_HIP_CHECK(hipGetLastError());
+  return TAM_OK;
+}
+
+static uint64_t tam_decompose_layout(uint64_t n, uint64_t* off_part, uint64_t* off_chunks, uint64_t* off_alpha) {
+  const uint64_t nt = tam_tiles_of(n);
+  const uint32_t nch = tam_alpha_chunks(TAM_FLAG_COSTATE, (uint32_t)nt);
+  uint64_t off = tam_align_up(sizeof(TamTensor), 256);
+  *off_part = off;
+  off = tam_align_up(off + nt * 4u * sizeof(double2), 256);
+  *off_chunks = off;
+  off = tam_align_up(off + (uint64_t)nch * sizeof(double2), 256);
+  *off_alpha = off;
+  return tam_align_up(off + sizeof(float), 256);
+}
+
+size_t tam_decompose_workspace(uint64_t n) {
+  uint64_t a, b, c;
+  return (size_t)tam_decompose_layout(n, &a, &b, &c);
+}
+
+int tam_decompose(const float* m, const float* g, uint64_t n, float* alpha, float* delta, void* workspace,
+                  size_t ws_bytes, void* stream) {
+  tam_err_buf[0] = 0;
+  if (!m || !g || !alpha || !delta || !workspace) return tam_fail(TAM_E_INVALID, "%snull argument", "");
+  if (n == 0 || (n + TAM_BLOCK_SIZE - 1) / TAM_BLOCK_SIZE > (1ull << 31))
+    return tam_fail(TAM_E_INVALID, "%selement count out of range", "");
+  uint64_t off_part, off_chunks, off_alpha;
+  const uint64_t need = tam_decompose_layout(n, &off_part, &off_chunks, &off_alpha);
+  if (ws_bytes < need) return tam_fail(TAM_E_WORKSPACE, "%sworkspace too small: need %ld bytes", "", (long)need);
+  hipStream_t s = (hipStream_t)stream;
+  char* ws = (char*)workspace;
+  TamTensor* desc = (TamTensor*)ws;
+  const uint32_t nt = tam_tiles_of(n);
+  const uint32_t nb = (uint32_t)((n + TAM_BLOCK_SIZE - 1) / TAM_BLOCK_SIZE);
+  hipLaunchKernelGGL(tam_k_make_desc, dim3(1), dim3(1), 0, s, desc, n, nb, 0u, 0u);
+  TAM_HIP_CHECK(hipGetLastError());
+  hipLaunchKernelGGL(tam_k_dot_quarters, dim3(nt), dim3(TAM_WG), 0, s, m, g, n, (double2*)(ws + off_part));
+  TAM_HIP_CHECK(hipGetLastError());
+  hipLaunchKernelGGL(tam_k_alpha_chunks, dim3(tam_alpha_chunks(TAM_FLAG_COSTATE, nt)), dim3(TAM_WG), 0, s, desc, 1,
+                     (const double2*)(ws + off_part), (double2*)(ws + off_chunks));
+  TAM_HIP_CHECK(hipGetLastError());
+  hipLaunchKernelGGL(tam_k_alpha, dim3(1), dim3(TAM_WG), 0, s, desc, (const double2*)(ws + off_chunks), alpha);
+  TAM_HIP_CHECK(hipGetLastError());
+  hipLaunchKernelGGL(tam_k_delta, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, s, m, g, n, alpha, delta);
+  TAM_HIP_CHECK(hipGetLastError());
+  return TAM_OK;
+}
+
+int tam_block_ratios(const float* delta, const float* m, uint64_t n, float* ratios, void* stream) {
+  tam_err_buf[0] = 0;
+  if (!delta || !m || !ratios) return tam_fail(TAM_E_INVALID, "%snull argument", "");
+  if (n == 0) return TAM_OK;
+  hipLaunchKernelGGL(tam_k_ratios, dim3(tam_tiles_of(n)), dim3(TAM_WG), 0, (hipStream_t)stream, delta, m, n, ratios);
+  TAM_HIP_CHECK(hipGetLastError());
+  return TAM_OK;
+}
+
+static uint64_t tam_thresholds_layout(uint64_t* off_sel, uint64_t* off_hist) {
+  uint64_t off = tam_align_up(sizeof(TamTensor), 256);
+  *off_sel = off;
+  off = tam_align_up(off + sizeof(TamSel), 256);
+  *off_hist = off;
+  return tam_align_up(off + 4096u * sizeof(uint32_t), 256);
+}
+
+size_t tam_thresholds_workspace(uint64_t nb) {
+  (void)nb;
+  uint64_t a, b;
+  return (size_t)tam_thresholds_layout(&a, &b);
+}
+
+int tam_thresholds(const float* ratios, uint64_t nb, uint32_t k_lo, uint32_t k_hi, float* taus, void* workspace,
+                   size_t ws_bytes, void* stream) {
+  tam_err_buf[0] = 0;
+  if (!ratios || !taus || !workspace) return tam_fail(TAM_E_INVALID, "%snull argument", "");
+  if (nb == 0 || nb > (1ull << 31)) return tam_fail(TAM_E_INVALID, "%sblock count out of range", "");
+  if (k_lo >= nb || k_hi >= nb) return tam_fail(TAM_E_INVALID, "%srank out of range", "");
+  if ((uintptr_t)ratios & 15u) return tam_fail(TAM_E_INVALID, "%sratios must be 16-byte aligned", "");
+  uint64_t off_sel, off_hist;
+  const uint64_t need = tam_thresholds_layout(&off_sel, &off_hist);
+  if (ws_bytes < need) return tam_fail(TAM_E_WORKSPACE, "%sworkspace too small: need %ld bytes", "", (long)need);
+  hipStream_t s = (hipStream_t)stream;
+  char* ws = (char*)workspace;
+  TamTensor* desc = (TamTensor*)ws;
+  TamSel* sel = (TamSel*)(ws + off_sel);
+  uint32_t* hist = (uint32_t*)(ws + off_hist);
+  const uint32_t slices = tam_sel_slices(TAM_FLAG_COSTATE, (uint32_t)nb);
+  hipLaunchKernelGGL(tam_k_make_desc, dim3(1), dim3(1), 0, s, desc, nb * TAM_BLOCK_SIZE, (uint32_t)nb, k_lo, k_hi);
+  TAM_HIP_CHECK(hipGetLastError());
+  hipLaunchKernelGGL(tam_k_sel_reset, dim3(1), dim3(TAM_WG), 0, s, desc, sel, hist);
+  TAM_HIP_CHECK(hipGetLastError());
+  hipLaunchKernelGGL(tam_k_sel_minmax, dim3(slices), dim3(TAM_WG), 0, s, desc, 1, ratios, sel);
+  TAM_HIP_CHECK(hipGetLastError());
+  for (int r = 0; r < 3; ++r) {
+    hipLaunchKernelGGL(tam_k_sel_hist, dim3(slices), dim3(TAM_WG), 0, s, desc, 1, ratios, sel, hist);
+    TAM_HIP_CHECK(hipGetLastError());
+    hipLaunchKernelGGL(tam_k_sel_pick, dim3(1), dim3(TAM_SEL_WG), 0, s, desc, sel, hist);
+    TAM_HIP_CHECK(hipGetLastError());
+  }
+  hipLaunchKernelGGL(tam_k_sel_taus, dim3(1), dim3(1), 0, s, sel, taus);
+  TAM_HIP_CHECK(hipGetLastError());
+  return TAM_OK;
+}
+
+int tam_classify(const float* ratios, uint64_t nb, const float* taus, uint8_t* labels, void* stream) {
+  tam_err_buf[0] = 0;
+  if (!ratios || !taus || !labels) return tam_fail(TAM_E_INVALID, "%snull argument", "");
+  if (nb == 0) return TAM_OK;
+  hipLaunchKernelGGL(tam_k_classify, dim3((uint32_t)((nb + 255) / 256)), dim3(256), 0, (hipStream_t)stream, ratios,
+                     nb, taus, labels);
+  TAM_HIP_CHECK(hipGetLastError());
+  return TAM_OK;
+}
+
+int tam_costate_encode(const float* delta, uint64_t n, uint8_t* signs, float* norms, uint16_t* amp, void* stream) {
+  tam_err_buf[0] = 0;
+  if (!delta || !signs || !norms || !amp) return tam_fail(TAM_E_INVALID, "%snull argument", "");
+  if (n == 0) return TAM_OK;
+  hipLaunchKernelGGL(tam_k_encode, dim3(tam_tiles_of(n)), dim3(TAM_WG), 0, (hipStream_t)stream, delta, n, signs,
+                     norms, amp);
+  TAM_HIP_CHECK(hipGetLastError());
+  return TAM_OK;
+}
+
+int tam_fused_v_update(const uint8_t* idx_in, const uint16_t* scales_in, const void* g, uint32_t g_dtype, uint64_t n,
+                       uint32_t v_bits, float beta2, float one_minus_beta2, uint32_t tensor_id, uint32_t step,
+                       uint64_t seed, uint8_t* idx_out, uint16_t* scales_out, float* v_out, void* stream) {
+  tam_err_buf[0] = 0;
+  if (!idx_in || !scales_in || !g || !idx_out || !scales_out || !v_out)
+    return tam_fail(TAM_E_INVALID, "%snull argument", "");
+  if (tam_check_dtype(g_dtype)) return TAM_E_INVALID;
+  if (!(v_bits == 2 || v_bits == 3 || v_bits == 4 || v_bits == 6 || v_bits == 8))
+    return tam_fail(TAM_E_INVALID, "%sv_bits must be 2, 3, 4, 6 or 8", "");
+  if (((uintptr_t)idx_in | (uintptr_t)idx_out) & 7u || ((uintptr_t)scales_in | (uintptr_t)scales_out) & 3u)
+    return tam_fail(TAM_E_INVALID, "%smisaligned v state", "");
+  if (n == 0) return TAM_OK;
+  hipLaunchKernelGGL(tam_k_fused_v, dim3(tam_tiles_of(n)), dim3(TAM_WG), 0, (hipStream_t)stream, idx_in, scales_in, g,
+                     g_dtype, n, v_bits, beta2, one_minus_beta2, tensor_id, step, (uint32_t)seed,
+                     (uint32_t)(seed >> 32), idx_out, scales_out, v_out);
+  TAM_HIP_CHECK(hipGetLastError());
+  return TAM_OK;
+}
+
+int tam_v_quantize(const float* v, uint64_t n_padded, uint32_t v_bits, int stochastic, uint32_t tensor_id,
+                   uint32_t step, uint64_t seed, uint8_t* idx, uint16_t* scales, void* stream) {
+  tam_err_buf[0] = 0;
+  if (!v || !idx || !scales) return tam_fail(TAM_E_INVALID, "%snull argument", "");
+  if (n_padded % TAM_BLOCK_SIZE) return tam_fail(TAM_E_INVALID, "%slength must be a multiple of 128", "");
+  if (!(v_bits == 2 || v_bits == 3 || v_bits == 4 || v_bits == 6 || v_bits == 8))
+    return tam_fail(TAM_E_INVALID, "%sv_bits must be 2, 3, 4, 6 or 8", "");
+  if ((uintptr_t)scales & 3u) return tam_fail(TAM_E_INVALID, "%smisaligned scales", "");
+  if (n_padded == 0) return TAM_OK;
+  hipLaunchKernelGGL(tam_k_quantize, dim3(tam_tiles_of(n_padded)), dim3(TAM_WG), 0, (hipStream_t)stream, v, n_padded,
+                     v_bits, stochastic, tensor_id, step, (uint32_t)seed, (uint32_t)(seed >> 32), idx, scales);
   TAM_HIP_CHECK(hipGetLastError());
   return TAM_OK;
 }

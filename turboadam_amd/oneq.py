@@ -1,4 +1,4 @@
-"""1Q second-moment state: initial state and inspection decode.
+"""1Q second-moment state: initial state, compression and decode.
 
 State dict layout (reference src/turboadam/oneq.py:41-48):
     {"indices": u8[nb*128], "scales": f16[nb, 2] (log_min, log_max),
@@ -9,7 +9,8 @@ State dict layout (reference src/turboadam/oneq.py:41-48):
 import torch
 
 from . import _lib
-from .utils import BLOCK_SIZE, num_blocks
+from .quantize import DEFAULT_SEED, quantize_logscale_nbits
+from .utils import BLOCK_SIZE, num_blocks, pad_to_blocks
 
 # TurboAdam starts v from full(1e-30) quantised deterministically
 # (reference optimizer.py:273-280 -> oneq.py:13-48 -> quantize.py:177-178):
@@ -30,6 +31,29 @@ def init_v_state(param: torch.Tensor, n_bits: int, block_size: int = BLOCK_SIZE)
         "n_bits": n_bits,
         "original_shape": param.shape,
         "original_length": n,
+        "block_size": block_size,
+    }
+
+
+def compress_v_logscale(v: torch.Tensor, n_bits: int = 3, block_size: int = BLOCK_SIZE,
+                        stochastic_round: bool = False, *, tensor_id: int = 0, step: int = 1,
+                        seed: int = DEFAULT_SEED) -> dict:
+    """Compress v (reference oneq.py:13-48): pad to whole blocks with
+    max(min(v), 1e-38), then quantize_logscale_nbits."""
+    original_shape = v.shape
+    v_flat = v.reshape(-1).float()
+    v_min = v_flat.min().item()
+    pad_value = max(v_min, 1e-38)
+    v_padded, original_length = pad_to_blocks(v_flat, block_size, pad_value=pad_value)
+    indices, scales, _ = quantize_logscale_nbits(v_padded, n_bits=n_bits, block_size=block_size,
+                                                 stochastic_round=stochastic_round, tensor_id=tensor_id,
+                                                 step=step, seed=seed)
+    return {
+        "indices": indices,
+        "scales": scales,
+        "n_bits": n_bits,
+        "original_shape": original_shape,
+        "original_length": original_length,
         "block_size": block_size,
     }
 

@@ -24,7 +24,7 @@ from .utils import BLOCK_SIZE, num_blocks
 # Key of the Philox4x32-10 stream that drives stochastic rounding.  The
 # counter is (element/4, tensor_id, step, 0), so a step is reproducible from
 # (seed, parameter order, step number) alone.
-DEFAULT_SEED = 0x7A3D_5EED_0BAD_C0DE
+from .quantize import DEFAULT_SEED  # noqa: E402  (the Philox key of the stochastic rounding)
 
 _DTYPES = {
     torch.float32: _lib.TAM_DTYPE_F32,
