@@ -184,3 +184,50 @@ def test_unaligned_parameter_views(dt):
     log(f"unaligned views dtype={dt}")
     sizes = [70_000, 4096 + 5, 300]
     _check(run_side_by_side(sizes, [dt] * 3, steps=4, offset=1, lr=1e-3, weight_decay=0.05))
+
+
+@pytest.mark.parametrize("bits,pct", [(2, (0.10, 0.90)), (3, (0.05, 0.95)), (6, (0.10, 0.90)), (8, (0.05, 0.95))])
+def test_ragged_multi_tensor_sweep(bits, pct):
+    # the ragged-config pattern at a size the oracle finishes in seconds: 120 fp32
+    # tensors log-uniform in [1, 2^14], mostly with tail blocks
+    rng = np.random.default_rng(bits)
+    sizes = [int(max(1, round(2 ** (14 * u)))) for u in rng.random(120)]
+    log(f"ragged sweep: 120 tensors, {sum(sizes)} params, v_bits={bits}, pct={pct}")
+    _check(run_side_by_side(sizes, [F32] * len(sizes), steps=3, v_bits=bits, null_pct=pct[0], amp_pct=pct[1],
+                            lr=1e-3))
+
+
+def test_sparse_heavy_tailed_gradients():
+    # exact-zero gradient rows (a sparse embedding pattern) and Student-t(3) tails
+    log("sparse rows of zeros + heavy tails, fp32, 4 steps")
+    from turboadam_amd import TurboAdam
+    from tests.helpers import from_torch, gpu_state, compare_states, to_torch
+
+    dev = torch.device("cuda:0")
+    rng = np.random.default_rng(11)
+    rows, cols = 400, 96
+    sizes = [rows * cols, 5000]
+    init = [(rng.standard_normal(n) * 0.02).astype(np.float32) for n in sizes]
+    o_params = [a.copy() for a in init]
+    g_params = [torch.nn.Parameter(to_torch(a, F32, (n,), dev)) for a, n in zip(init, sizes)]
+    opt = TurboAdam(g_params, lr=6e-4, weight_decay=0.01)
+    opt.philox_seed = 4242
+    orc = O.OracleTurboAdam(o_params, dtypes=[F32, F32], seed=4242, lr=6e-4, weight_decay=0.01)
+    bad = []
+    for s in range(4):
+        t = rng.standard_t(3, size=sizes[0]).astype(np.float32) * np.float32(1e-3)
+        keep = rng.random(rows) < 0.05
+        t = (t.reshape(rows, cols) * keep[:, None]).reshape(-1).astype(np.float32)
+        g2 = (rng.standard_t(3, size=sizes[1]) * 1e-3).astype(np.float32)
+        grads = [t, g2]
+        for p, g, n in zip(g_params, grads, sizes):
+            p.grad = to_torch(g, F32, (n,), dev)
+        opt.step()
+        orc.step(grads)
+        torch.cuda.synchronize()
+        for i, p in enumerate(g_params):
+            where = f"step {s + 1} tensor {i}"
+            if not np.array_equal(from_torch(p.data).view(np.uint32), o_params[i].view(np.uint32)):
+                bad.append(f"{where}: param differs")
+            bad += compare_states(gpu_state(opt, p), orc.state[i], where)
+    _check(bad)
