@@ -297,7 +297,7 @@ def main():
             "step_hbm_frac": step_gbps / HBM_PEAK_GBPS,
         },
         "roofline": {
-            "kernel": "tam_k1_main (pass 1)",
+            "kernel": "pass 1 (tam_k1_main_<dtype> + tam_k1_tail)",
             "bound": "hbm",
             "achieved": k1_gbps,
             "peak": HBM_PEAK_GBPS,
