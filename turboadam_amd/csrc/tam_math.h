@@ -45,6 +45,15 @@ struct TamU4 {
   uint32_t x, y, z, w;
 };
 
+// a ^ b ^ c in one gfx950 three-input bitwise instruction (truth table 0x96).
+TAM_HD uint32_t tam_xor3(uint32_t a, uint32_t b, uint32_t c) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __builtin_amdgcn_bitop3_b32(a, b, c, 0x96);
+#else
+  return a ^ b ^ c;
+#endif
+}
+
 TAM_HD TamU4 tam_philox4x32_10(TamU4 c, uint32_t k0, uint32_t k1) {
 #pragma unroll
   for (int r = 0; r < 10; ++r) {
@@ -57,9 +66,9 @@ TAM_HD TamU4 tam_philox4x32_10(TamU4 c, uint32_t k0, uint32_t k1) {
     const uint32_t hi0 = (uint32_t)(p0 >> 32), lo0 = (uint32_t)p0;
     const uint32_t hi1 = (uint32_t)(p1 >> 32), lo1 = (uint32_t)p1;
     TamU4 n;
-    n.x = hi1 ^ c.y ^ k0;
+    n.x = tam_xor3(hi1, c.y, k0);
     n.y = lo1;
-    n.z = hi0 ^ c.w ^ k1;
+    n.z = tam_xor3(hi0, c.w, k1);
     n.w = lo0;
     c = n;
   }

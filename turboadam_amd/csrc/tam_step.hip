@@ -88,6 +88,22 @@ __device__ __forceinline__ uint16_t tam_round16_hw(float x) {
   return DT == TAM_DTYPE_BF16 ? tam_f32_to_bf16_rne(x) : tam_f32_to_f16(x);
 }
 
+// Rounds lo and hi to the parameter dtype; returns whether both round to the
+// same value, which is stored in r (bf16: both in one packed conversion).
+template <uint32_t DT>
+__device__ __forceinline__ bool tam_same16(float lo, float hi, uint16_t* r) {
+  if (DT == TAM_DTYPE_BF16) {
+    typedef float tam_f2 __attribute__((ext_vector_type(2)));
+    typedef __bf16 tam_bf2 __attribute__((ext_vector_type(2)));
+    const uint32_t u = __builtin_bit_cast(uint32_t, __builtin_convertvector((tam_f2){lo, hi}, tam_bf2));
+    *r = (uint16_t)u;
+    return (uint16_t)u == (uint16_t)(u >> 16);
+  }
+  const uint16_t a = tam_round16_hw<DT>(lo), b = tam_round16_hw<DT>(hi);
+  *r = a;
+  return a == b;
+}
+
 // Elements [e0, e0+8) of a parameter or gradient.  FULL: all 8 exist and the
 // array is 16-byte aligned; otherwise only the first nv exist (the rest read 0).
 template <uint32_t DT, bool FULL>
@@ -163,11 +179,14 @@ __device__ __forceinline__ uint16_t tam_round16(float x, uint32_t dtype) {
 // reductions over the 16 lanes of a block (one DPP row)
 // ---------------------------------------------------------------------------
 // gfx9 DPP controls: quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror
-// (lane i <-> 7-i within each half row), row_mirror (lane i <-> 15-i).
+// (lane i <-> 7-i within each half row), row_mirror (lane i <-> 15-i),
+// row_ror:4 and row_ror:8 (lane i reads lane (i - 4) mod 16, (i - 8) mod 16).
 #define TAM_DPP_XOR1 0xB1
 #define TAM_DPP_XOR2 0x4E
 #define TAM_DPP_HALF_MIRROR 0x141
 #define TAM_DPP_MIRROR 0x140
+#define TAM_DPP_ROR4 0x124
+#define TAM_DPP_ROR8 0x128
 
 // Every control used here reads a lane of the same row, so no lane is out of
 // range and bound_ctrl (read 0 from an invalid lane) never applies; with it
@@ -211,6 +230,38 @@ __device__ __forceinline__ double tam_block_sum(double v) {
   v = v + tam_dppd<TAM_DPP_MIRROR>(v);
   return v;
 }
+// x plus its value in the paired row (rows 0/1 and 2/3: v_permlane16_swap) or
+// half wave (v_permlane32_swap).  Both operands of the swap are x, so every lane
+// receives its partner's x in one of the two results and the sum is the same in
+// both partners.  Requires every lane of the wave active.
+template <int ROWS>
+__device__ __forceinline__ double tam_swap_add(double x) {
+  const uint64_t u = tam_d2u(x);
+  const uint32_t lo = (uint32_t)u, hi = (uint32_t)(u >> 32);
+  const auto l = ROWS == 1 ? __builtin_amdgcn_permlane16_swap(lo, lo, true, false)
+                           : __builtin_amdgcn_permlane32_swap(lo, lo, true, false);
+  const auto h = ROWS == 1 ? __builtin_amdgcn_permlane16_swap(hi, hi, true, false)
+                           : __builtin_amdgcn_permlane32_swap(hi, hi, true, false);
+  return tam_u2d(((uint64_t)h[0] << 32) | l[0]) + tam_u2d(((uint64_t)h[1] << 32) | l[1]);
+}
+
+// Sums of a and b over a wave's 4 blocks, each with the tree of tam_block_sum
+// per block and then (b0 + b1) + (b2 + b3), in one reduction: after the first
+// step even lanes carry partial sums of a and odd lanes of b (quad steps pair
+// lanes of equal parity).  row_ror:4 then pairs lanes 0-3 with 4-7 (valid in
+// lanes 4-7 and 12-15) and row_ror:8 pairs 0-7 with 8-15 (valid in lanes
+// 12-15); the swaps pair blocks 0/1, 2/3 and then the two halves.  Returns the
+// sum of a in lane 12 and the sum of b in lane 13.  Requires every lane active.
+__device__ __forceinline__ double tam_quarter_sum2(double a, double b, uint32_t lane) {
+  const bool odd = (lane & 1u) != 0;
+  double x = (odd ? b : a) + tam_dppd<TAM_DPP_XOR1>(odd ? a : b);
+  x = x + tam_dppd<TAM_DPP_XOR2>(x);
+  x = x + tam_dppd<TAM_DPP_ROR4>(x);
+  x = x + tam_dppd<TAM_DPP_ROR8>(x);
+  x = tam_swap_add<1>(x);
+  return tam_swap_add<2>(x);
+}
+
 // Minimum / maximum over the block of unsigned keys (bit patterns of
 // positive floats order like the floats).
 __device__ __forceinline__ uint32_t tam_block_umin(uint32_t v) {
@@ -494,8 +545,11 @@ __device__ __forceinline__ void tam_vpath_b(const TamTensor& d, const TamWave& W
   const TamU4 r0 = tam_philox_quad(quad0, d.tensor_id, d.step, seed_lo, seed_hi);
   const TamU4 r1 = tam_philox_quad(quad0 + 1, d.tensor_id, d.step, seed_lo, seed_hi);
   const uint32_t rw[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
-  uint32_t qb[TAM_EPL];
-  uint32_t amb = 0;
+  // indices go straight into their bytes (v_cvt_pk_u8_f32 of an integral
+  // value in [0, 255]); acceptance per element as lane masks
+  uint32_t ow[2] = {0u, 0u};
+  bool okv[TAM_EPL];
+  bool all_ok = true;
   if (FULL) {
     // Every element of a full block lies in [vmin, vmax] (normal, no NaN
     // checked once here), so |log2 v| <= L and, when B < 1/4, |c~| <= 2^bits + 1
@@ -514,9 +568,10 @@ __device__ __forceinline__ void tam_vpath_b(const TamTensor& d, const TamWave& W
       const float dd = __builtin_fmaf(-(float)(rw[i] >> 8), 0x1p-24f, ct);  // fl(ct - u), u exact
       const float q = __builtin_ceilf(dd);
       const float t = (q - 0.5f) - dd;
-      const bool ok = __builtin_fabsf(t) < H;
-      amb |= ok ? 0u : (1u << i);
-      qb[i] = (uint32_t)__builtin_amdgcn_fmed3f(q, 0.0f, fnb - 1.0f);  // the exact path overwrites !ok
+      okv[i] = __builtin_fabsf(t) < H;
+      all_ok &= okv[i];
+      // the exact path overwrites !ok
+      ow[i >> 2] = __builtin_amdgcn_cvt_pk_u8_f32(__builtin_amdgcn_fmed3f(q, 0.0f, fnb - 1.0f), i & 3, ow[i >> 2]);
     }
   } else {
 #pragma unroll
@@ -527,16 +582,16 @@ __device__ __forceinline__ void tam_vpath_b(const TamTensor& d, const TamWave& W
       const float B = __builtin_fmaf(__builtin_fabsf(l2), KB, __builtin_fmaf(__builtin_fabsf(ct), 0x1p-21f, CB));
       const float q = __builtin_ceilf(dd);
       const float r = q - dd;
-      const bool ok = (vc[i] >= 0x1p-126f) && (r >= B) && (1.0f - r > B);  // false for NaN
-      amb |= ok ? 0u : (1u << i);
-      qb[i] = (uint32_t)__builtin_amdgcn_fmed3f(q, 0.0f, fnb - 1.0f);  // the exact path overwrites !ok
+      okv[i] = (vc[i] >= 0x1p-126f) && (r >= B) && (1.0f - r > B);  // false for NaN
+      all_ok &= okv[i];
+      ow[i >> 2] = __builtin_amdgcn_cvt_pk_u8_f32(__builtin_amdgcn_fmed3f(q, 0.0f, fnb - 1.0f), i & 3, ow[i >> 2]);
     }
   }
-  if (amb) {
+  if (!all_ok) {
     // exact path: the reference's own sequence with correctly rounded log and division
 #pragma unroll
     for (int i = 0; i < TAM_EPL; ++i) {
-      if (amb & (1u << i)) {
+      if (!okv[i]) {
         const float l = tam_logf_lds(vc[i], tabs);
         const float c = ((l - lmn) / sp) * fnb;  // quantize.py:284-285
         const float f = __builtin_floorf(c);
@@ -545,13 +600,13 @@ __device__ __forceinline__ void tam_vpath_b(const TamTensor& d, const TamWave& W
         float q = f + (u < fr ? 1.0f : 0.0f);  // quantize.py:288-294
         q = q < 0.0f ? 0.0f : q;
         q = q > fnb - 1.0f ? fnb - 1.0f : q;
-        qb[i] = tam_isnan(q) ? 0u : (uint32_t)q;
+        const uint32_t qi = tam_isnan(q) ? 0u : (uint32_t)q;
+        const uint32_t sh = 8u * (uint32_t)(i & 3);
+        ow[i >> 2] = (ow[i >> 2] & ~(0xffu << sh)) | (qi << sh);
       }
     }
   }
-  const uint32_t ow0 = qb[0] | (qb[1] << 8) | (qb[2] << 16) | (qb[3] << 24);
-  const uint32_t ow1 = qb[4] | (qb[5] << 8) | (qb[6] << 16) | (qb[7] << 24);
-  tam_g((TamW2*)(d.v_idx + W.e0))[0] = TamW2{ow0, ow1};
+  tam_g((TamW2*)(d.v_idx + W.e0))[0] = TamW2{ow[0], ow[1]};
 }
 
 // ---------------------------------------------------------------------------
@@ -571,6 +626,9 @@ __device__ __forceinline__ void tam_vpath_b(const TamTensor& d, const TamWave& W
 // R_p(fl(p + upd)) is accepted when R_p(fl(s~ - E)) == R_p(fl(s~ + E)) (R_p and
 // fl are monotone); otherwise the exact sequence runs.  The result of a
 // 16-bit parameter is returned as its bit pattern in pb.
+// v_cmp_class_f32 masks: +normal; +-normal or +-zero
+#define TAM_CLASS_POS_NORMAL 0x100
+#define TAM_CLASS_NORMAL_OR_ZERO 0x168
 template <uint32_t DT>
 __device__ __forceinline__ void tam_update(const TamTensor& d, float* p, const float* m, const float* v,
                                            uint16_t* pb) {
@@ -588,7 +646,6 @@ __device__ __forceinline__ void tam_update(const TamTensor& d, float* p, const f
     }
     return;
   }
-  uint32_t amb = 0;
   float pw[TAM_EPL];
   // weight decay rounds to the parameter dtype (p.mul_ on a 16-bit tensor)
   if (wd) {
@@ -600,6 +657,9 @@ __device__ __forceinline__ void tam_update(const TamTensor& d, float* p, const f
   }
   // -lr / bc1 (one more rounding in the fast sequence, inside the 2^-19 bound)
   const float c_lr = d.neg_lr / d.bias_correction1;
+  // per-element acceptance as lane masks (no per-element VALU to combine them)
+  bool okv[TAM_EPL];
+  bool all_ok = true;
 #pragma unroll
   for (int i = 0; i < TAM_EPL; ++i) {
     const float q = v[i] * d.inv_bc2_f32;
@@ -609,20 +669,25 @@ __device__ __forceinline__ void tam_update(const TamTensor& d, float* p, const f
     const float u = cm * __builtin_amdgcn_rcpf(den);
     const float st = pw[i] + u;
     const float E = __builtin_fmaf(__builtin_fabsf(u), 0x1p-19f, __builtin_fmaf(__builtin_fabsf(st), 0x1p-22f, 0x1p-148f));
-    // finite, normal hardware inputs and outputs, and c*m exact zero or normal
-    // (its relative error bound); NaN fails every comparison
-    const bool ok0 = (q >= 0x1p-126f) && (den < 0x1p125f) && (__builtin_fabsf(st) < 0x1p126f) &&
-                     ((__builtin_fabsf(cm) >= 0x1p-126f) || (cm == 0.0f));
-    const uint16_t rl = tam_round16_hw<DT>(st - E);
-    const uint16_t rh = tam_round16_hw<DT>(st + E);
-    const bool ok = ok0 && rl == rh;
-    pb[i] = rl;
-    amb |= ok ? 0u : (1u << i);
+    // finite, normal hardware inputs and outputs (q a positive normal; then
+    // den < 2^125), and c*m exact zero or normal (its relative error bound);
+    // NaN fails every test
+    const bool ok0 = __builtin_amdgcn_classf(q, TAM_CLASS_POS_NORMAL) & (__builtin_fabsf(st) < 0x1p126f) &
+                     __builtin_amdgcn_classf(cm, TAM_CLASS_NORMAL_OR_ZERO);
+    okv[i] = tam_same16<DT>(st - E, st + E, &pb[i]) & ok0;
+    all_ok &= okv[i];
   }
-  if (amb) {
+  // with q finite, s < 2^64, so den = s + eps < 2^125 when eps < 2^124
+  // (a uniform condition: otherwise every element takes the exact sequence)
+  if (!(d.eps < 0x1p124f)) {
+#pragma unroll
+    for (int i = 0; i < TAM_EPL; ++i) okv[i] = false;
+    all_ok = false;
+  }
+  if (!all_ok) {
 #pragma unroll
     for (int i = 0; i < TAM_EPL; ++i) {
-      if (amb & (1u << i)) {
+      if (!okv[i]) {
         const float den = __builtin_sqrtf(v[i] / d.bias_correction2) + d.eps;
         pb[i] = tam_round16(pw[i] + (d.neg_lr * m[i]) / (den * d.bias_correction1), DT);
       }
@@ -685,14 +750,10 @@ __device__ __forceinline__ void tam_k1_quarter(const TamTensor& d, uint32_t wq, 
       gg[i] = ok ? (double)g[i] * (double)g[i] : 0.0;
       mg[i] = ok ? (double)m[i] * (double)g[i] : 0.0;
     }
-    const double sgg = tam_block_sum(tam_pair8(gg));
-    const double smg = tam_block_sum(tam_pair8(mg));
-    // the wave's 4 blocks (block k in lanes 16k..16k+15): adjacent pairs, then the two pairs
-    const double tgg = (tam_readlane_d(sgg, 0) + tam_readlane_d(sgg, 16)) +
-                       (tam_readlane_d(sgg, 32) + tam_readlane_d(sgg, 48));
-    const double tmg = (tam_readlane_d(smg, 0) + tam_readlane_d(smg, 16)) +
-                       (tam_readlane_d(smg, 32) + tam_readlane_d(smg, 48));
-    if (lane == 0) tam_g((TamD2*)part)[0] = TamD2{tgg, tmg};
+    // per block, then the wave's 4 blocks (block k in lanes 16k..16k+15):
+    // adjacent pairs, then the two pairs; lane 12 stores g.g, lane 13 m.g
+    const double t = tam_quarter_sum2(tam_pair8(gg), tam_pair8(mg), lane);
+    if (lane - 12u < 2u) tam_g((double*)part)[lane - 12u] = t;
   } else if (FULL || W.bvalid) {
     // fp32 exp_avg (optimizer.py:113): m = fma(1-b1, g, fl(m*b1))
     float ea[TAM_EPL];
