@@ -245,19 +245,24 @@ __device__ __forceinline__ double tam_swap_add(double x) {
   return tam_u2d(((uint64_t)h[0] << 32) | l[0]) + tam_u2d(((uint64_t)h[1] << 32) | l[1]);
 }
 
-// Sums of a and b over a wave's 4 blocks, each with the tree of tam_block_sum
-// per block and then (b0 + b1) + (b2 + b3), in one reduction: after the first
-// step even lanes carry partial sums of a and odd lanes of b (quad steps pair
-// lanes of equal parity).  row_ror:4 then pairs lanes 0-3 with 4-7 (valid in
-// lanes 4-7 and 12-15) and row_ror:8 pairs 0-7 with 8-15 (valid in lanes
-// 12-15); the swaps pair blocks 0/1, 2/3 and then the two halves.  Returns the
-// sum of a in lane 12 and the sum of b in lane 13.  Requires every lane active.
-__device__ __forceinline__ double tam_quarter_sum2(double a, double b, uint32_t lane) {
-  const bool odd = (lane & 1u) != 0;
+// Per-block sums of a and b with the tree of tam_block_sum, in one reduction:
+// after the first step even lanes carry partial sums of a and odd lanes of b
+// (quad steps pair lanes of equal parity); row_ror:4 then pairs lanes 0-3
+// with 4-7 and row_ror:8 pairs 0-7 with 8-15.  The sum of a is valid in lanes
+// 12 and 14 of each row, the sum of b in lanes 13 and 15.
+__device__ __forceinline__ double tam_row_sum2(double a, double b, bool odd) {
   double x = (odd ? b : a) + tam_dppd<TAM_DPP_XOR1>(odd ? a : b);
   x = x + tam_dppd<TAM_DPP_XOR2>(x);
   x = x + tam_dppd<TAM_DPP_ROR4>(x);
-  x = x + tam_dppd<TAM_DPP_ROR8>(x);
+  return x + tam_dppd<TAM_DPP_ROR8>(x);
+}
+
+// Sums of a and b over a wave's 4 blocks: tam_row_sum2 per block, then
+// (b0 + b1) + (b2 + b3) through the swaps (blocks 0/1 and 2/3, then the two
+// halves).  Returns the sum of a in lane 12 and the sum of b in lane 13.
+// Requires every lane active.
+__device__ __forceinline__ double tam_quarter_sum2(double a, double b, uint32_t lane) {
+  double x = tam_row_sum2(a, b, (lane & 1u) != 0);
   x = tam_swap_add<1>(x);
   return tam_swap_add<2>(x);
 }
@@ -995,29 +1000,28 @@ __device__ __forceinline__ void tam_k2_quarter(const TamTensor& d, uint32_t wq, 
       const float delta = ok ? m[i] - a * g[i] : 0.0f;  // costate.py:42
       dd[i] = (double)delta * (double)delta;
       mm[i] = ok ? (double)m[i] * (double)m[i] : 0.0;
-      sbyte |= (delta < 0.0f ? 1u : 0u) << (7 - i);  // costate.py:170-181
+      sbyte = 2u * sbyte + (delta < 0.0f ? 1u : 0u);  // element 8j+i is bit 7-i, costate.py:170-181
     }
   } else {
 #pragma unroll
     for (int i = 0; i < TAM_EPL; ++i) dd[i] = mm[i] = 0.0;
   }
-  const double sd = tam_block_sum(tam_pair8(dd));
-  const double sm = tam_block_sum(tam_pair8(mm));
-  // Per-block results, shared between lane pairs so that each lane evaluates
-  // one square root and one division: even lanes the residual norm and the
-  // amplitude, odd lanes the norm of m and the ratio.
+  // Block sums with the tree of tam_block_sum: the sum of dd in lane 12 of the
+  // block's row, of mm in lane 13.  Each lane of a pair evaluates one square
+  // root and one division: lane 12 the residual norm and the amplitude, lane 13
+  // the norm of m and the ratio.
   const bool odd = (W.l16 & 1u) != 0;
-  const float nx = (float)__builtin_sqrt(odd ? sm : sd);
+  const float nx = (float)__builtin_sqrt(tam_row_sum2(tam_pair8(dd), tam_pair8(mm), odd));
   const float ny = tam_dppf<TAM_DPP_XOR1>(nx);
   const float nd = odd ? ny : nx;  // costate.py:241
   const float nm = odd ? nx : ny;
   const float qv = nd / (odd ? nm : d.sqrt_block);  // costate.py:248 / :81-84
   if (FULL || W.bvalid) {
     if (FULL || W.nv > 0) tam_g(d.signs)[W.e0 >> 3] = (uint8_t)sbyte;
-    if (W.l16 == 0) {
+    if (W.l16 == 12u) {
       tam_g(d.norms)[W.b] = nd;
       tam_g(d.amp)[W.b] = tam_f32_to_f16(qv);
-    } else if (W.l16 == 1) {
+    } else if (W.l16 == 13u) {
       tam_g(ratios)[d.ratio_off + W.b] = nm == 0.0f ? 0.0f : qv;
     }
   }
