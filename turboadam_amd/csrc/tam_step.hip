@@ -12,17 +12,19 @@
 // [tile0_i, tile0_i + ntiles_i)) and persistent workgroups stride over them,
 // so one launch covers the whole parameter list.
 //
-// Per step (tam_multi_tensor_step):
-//   K1 tam_k1_main    every tile: CoState decode + EMA (or fp32 exp_avg EMA),
-//                     1Q decode + EMA + stochastic re-quantisation (or fp32
-//                     exp_avg_sq), denominator, decoupled weight decay,
-//                     parameter update; per-quarter-tile fp64 partials of
-//                     g.g, m.g.
-//   K2 tam_k_alpha    one workgroup per CoState tensor: alpha = m.g / g.g.
-//   K3 tam_k2_encode  CoState tiles: recompute m, delta = m - alpha*g, sign
-//                     bits, block norms, fp16 amplitudes, block ratios.
-//   K4 tam_k3_select  one workgroup per CoState tensor: radix selection of the
-//                     two order statistics, labels, alpha write-back.
+// Per step (tam_multi_tensor_step), four passes:
+//   pass 0  tam_k1_main_<dtype> (full quarters; one kernel per parameter dtype
+//           present) and tam_k1_tail (the other quarters): CoState decode + EMA
+//           (or fp32 exp_avg EMA), 1Q decode + EMA + stochastic
+//           re-quantisation (or fp32 exp_avg_sq), denominator, decoupled
+//           weight decay, parameter update; per-quarter-tile fp64 partials of
+//           g.g and m.g.
+//   pass 1  tam_k_alpha_chunks, tam_k_alpha: alpha = m.g / g.g per CoState
+//           tensor (pairwise trees over the partials).
+//   pass 2  tam_k2_encode: CoState tiles: recompute m, delta = m - alpha*g,
+//           sign bits, block norms, fp16 amplitudes, block ratios.
+//   pass 3  tam_k_sel_*: radix selection of the two order statistics over
+//           slices of the ratios, labels, alpha write-back.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -717,7 +719,7 @@ __device__ __forceinline__ bool tam_quarter_full(const TamTensor& d, uint32_t wq
 }
 
 // ---------------------------------------------------------------------------
-// K1: the fused pass
+// Pass 0: the fused update
 // ---------------------------------------------------------------------------
 // Per quarter tile: loads, first moment (CoState or fp32), second moment (1Q or
 // fp32), update, store; for CoState tensors the fp64 partial sums of g.g and
@@ -859,16 +861,16 @@ __global__ __launch_bounds__(TAM_WG) void tam_k1_tail(const TamTensor* __restric
 }
 
 // ---------------------------------------------------------------------------
-// K2: alpha of every CoState tensor (costate.py:37-41)
+// Pass 1: alpha of every CoState tensor (costate.py:37-41)
 // ---------------------------------------------------------------------------
 // The dot products are balanced pairwise sums over the tensor's quarter-tile
 // partials zero-padded to a power of two P.  The padded array is cut into
 // aligned chunks of 8192 (one chunk of P when P <= 8192); chunk sums are
-// subtrees of the same tree.  K2a sums every chunk of every tensor (one
-// workgroup per chunk: 32 consecutive values per thread, then a tree in LDS);
-// K2b sums each tensor's chunk sums (at most 2048, a power of two) and forms
-// alpha.  Zero padding does not change the sum: x + 0 == x, and +0.0 added
-// to the result settles the sign of an exact zero.
+// subtrees of the same tree.  tam_k_alpha_chunks sums every chunk of every
+// tensor (one workgroup per chunk: 32 consecutive values per thread, then a
+// tree in LDS); tam_k_alpha sums each tensor's chunk sums (at most 2048, a
+// power of two) and forms alpha.  Zero padding does not change the sum:
+// x + 0 == x, and +0.0 added to the result settles the sign of an exact zero.
 #define TAM_PAIR_PER_THREAD 32
 #define TAM_CHUNK (TAM_WG * TAM_PAIR_PER_THREAD)
 
@@ -979,7 +981,7 @@ __global__ __launch_bounds__(TAM_WG) void tam_k_alpha(const TamTensor* __restric
 }
 
 // ---------------------------------------------------------------------------
-// K3: CoState encode (costate.py:419-425, :213-258) and block ratios (:51-86)
+// Pass 2: CoState encode (costate.py:419-425, :213-258) and block ratios (:51-86)
 // ---------------------------------------------------------------------------
 template <uint32_t DT, bool FULL>
 __device__ __forceinline__ void tam_k2_quarter(const TamTensor& d, uint32_t wq, uint32_t lane, float a,
@@ -1058,28 +1060,30 @@ __global__ __launch_bounds__(TAM_WG) void tam_k2_encode(const TamTensor* __restr
 }
 
 // ---------------------------------------------------------------------------
-// K4: order statistics of the ratios (costate.py:114-118), labels
+// Pass 3: order statistics of the ratios (costate.py:114-118), labels
 // (costate.py:146-148), alpha write-back (costate.py:443-454)
 // ---------------------------------------------------------------------------
 // Ratios are >= +0 or NaN, so their fp32 bit patterns order like torch.sort
 // (NaN last).  The selection is an MSD radix select on those patterns, spread
 // over slices of 8192 keys so that large tensors use many workgroups:
-//   K4a  per tensor: reset the selection state and histograms;
-//   K4b  per slice: min / max of the keys (atomic min / max per tensor) -- the
-//        bits all keys share need no pass;
-//   K4c  per slice, three times: LDS histogram of the next 11-bit digit below
-//        the bits already fixed, for the keys that match the prefix of each of
-//        the two ranks (keys of similar magnitude spread over the bins), added
-//        into the tensor's histogram;
-//   K4d  per tensor, after each K4c: prefix sums of the histogram pick the
-//        digit holding each rank;
-//   K4e  per slice: labels from the two thresholds; alpha write-back.
+//   tam_k_sel_reset   per tensor: reset the selection state and histograms;
+//   tam_k_sel_minmax  per slice: min / max of the keys (atomic min / max per
+//                     tensor) -- the bits all keys share need no pass;
+//   tam_k_sel_hist    per slice, three times: LDS histogram of the next 11-bit
+//                     digit below the bits already fixed, for the keys that
+//                     match the prefix of each of the two ranks (keys of
+//                     similar magnitude spread over the bins), added into the
+//                     tensor's histogram;
+//   tam_k_sel_pick    per tensor, after each histogram: prefix sums of the
+//                     histogram pick the digit holding each rank;
+//   tam_k_sel_labels  per slice: labels from the two thresholds; alpha
+//                     write-back.
 #define TAM_SLICE 8192u
 #define TAM_SEL_WG 1024
 
 // Selection state of one tensor (workspace).
 struct TamSel {
-  uint32_t kmin, kmax;  // key range (K4b)
+  uint32_t kmin, kmax;  // key range (tam_k_sel_minmax)
   uint32_t prefix[2];   // bits fixed so far of the k_lo-th and k_hi-th key
   uint32_t k[2];        // rank within the keys sharing the prefix
   uint32_t mask;        // bits fixed so far
