@@ -35,7 +35,7 @@ class OrTensor(ctypes.Structure):
         ("n", ctypes.c_uint64),
         ("dtype", ctypes.c_uint32), ("flags", ctypes.c_uint32), ("v_bits", ctypes.c_uint32),
         ("tensor_id", ctypes.c_uint32), ("step", ctypes.c_uint32), ("k_lo", ctypes.c_uint32),
-        ("k_hi", ctypes.c_uint32), ("pad1", ctypes.c_uint32),
+        ("k_hi", ctypes.c_uint32), ("block0", ctypes.c_uint32),
         ("c_wd", ctypes.c_float), ("beta1", ctypes.c_float), ("one_minus_beta1", ctypes.c_float),
         ("beta2", ctypes.c_float), ("one_minus_beta2", ctypes.c_float), ("bias_correction1", ctypes.c_float),
         ("bias_correction2", ctypes.c_float), ("eps", ctypes.c_float), ("neg_lr", ctypes.c_float),
@@ -114,10 +114,14 @@ class OracleTurboAdam:
 
     params: list of numpy arrays (float32, or uint16 bit patterns with the
     matching entry of `dtypes` = DT_BF16 / DT_F16), or a list of groups
-    {"params": [...], **hyperparameters}.
+    {"params": [...], **hyperparameters}.  tensor_ids: the Philox tensor id of
+    each parameter (default: its position, as TurboAdam numbers them);
+    block0: for a parameter that is a block-aligned slice of a larger one
+    without CoState, the slice's first block (its draws are then that
+    parameter's).
     """
 
-    def __init__(self, params, dtypes=None, seed=0, **kw):
+    def __init__(self, params, dtypes=None, seed=0, tensor_ids=None, block0=None, **kw):
         if params and isinstance(params[0], dict):
             groups = params
         else:
@@ -132,6 +136,8 @@ class OracleTurboAdam:
             flat.extend(grp["params"])
             self.param_groups.append(grp)
         self.dtypes = list(dtypes) if dtypes is not None else [DT_F32] * len(flat)
+        self.tensor_ids = list(tensor_ids) if tensor_ids is not None else list(range(len(flat)))
+        self.block0 = list(block0) if block0 is not None else [0] * len(flat)
         self.seed = seed
         self.state = {}
 
@@ -214,7 +220,8 @@ class OracleTurboAdam:
             if wd != 0.0:
                 flags |= FLAG_WD
             t.flags = flags
-            t.tensor_id = pid
+            t.tensor_id = self.tensor_ids[pid]
+            t.block0 = self.block0[pid]
             t.step = st["step"]
             c1, c2 = bc[gi]
             t.c_wd = f32(1.0 - lr * wd)

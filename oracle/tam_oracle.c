@@ -295,9 +295,12 @@ void or_costate_update(const float* g, uint64_t n, float beta1, float one_minus_
 }
 
 /* fused_v_update, reference quantize.py:222-299.  idx (N_pad) and scales
- * (2*nb f16) updated in place; v_out receives v (n). */
-void or_fused_v_update(uint8_t* idx, uint16_t* scales, const float* g, uint64_t n, int bits, float beta2,
-                       float one_minus_beta2, uint32_t tid, uint32_t step, uint64_t seed, float* v_out) {
+ * (2*nb f16) updated in place; v_out receives v (n).  The draw of element i is
+ * the one of element e_base + i (a block-aligned slice of a larger parameter
+ * draws as that parameter does). */
+static void or_fused_v_update_at(uint8_t* idx, uint16_t* scales, const float* g, uint64_t n, int bits,
+                                 float beta2, float one_minus_beta2, uint32_t tid, uint32_t step, uint64_t seed,
+                                 uint64_t e_base, float* v_out) {
   uint64_t nb = (n + OR_BS - 1) / OR_BS;
   float nbk = (float)(1u << bits);
   float vb[OR_BS], lg[OR_BS];
@@ -336,7 +339,7 @@ void or_fused_v_update(uint8_t* idx, uint16_t* scales, const float* g, uint64_t 
       float c = ((lg[j] - nmin) / sp) * nbk;       /* :284-285 */
       float f = floorf(c);
       float fr = c - f;
-      float u = or_uniform(i, tid, step, seed);
+      float u = or_uniform(e_base + i, tid, step, seed);
       float r = f + (u < fr ? 1.0f : 0.0f);        /* :288-294 */
       if (r < 0.0f) r = 0.0f;
       if (r > nbk - 1.0f) r = nbk - 1.0f;
@@ -344,6 +347,11 @@ void or_fused_v_update(uint8_t* idx, uint16_t* scales, const float* g, uint64_t 
       if (i < n) v_out[i] = vb[j];
     }
   }
+}
+
+void or_fused_v_update(uint8_t* idx, uint16_t* scales, const float* g, uint64_t n, int bits, float beta2,
+                       float one_minus_beta2, uint32_t tid, uint32_t step, uint64_t seed, float* v_out) {
+  or_fused_v_update_at(idx, scales, g, n, bits, beta2, one_minus_beta2, tid, step, seed, 0, v_out);
 }
 
 /* quantize_logscale_nbits, reference quantize.py:126-180, on v already padded
@@ -406,7 +414,10 @@ typedef struct OrTensor {
   uint16_t* amp;
   float* alpha;
   uint64_t n;
-  uint32_t dtype, flags, v_bits, tensor_id, step, k_lo, k_hi, pad1;
+  /* block0: first block of this tensor within the parameter it is a
+   * block-aligned slice of (0 for a whole parameter); only the stochastic
+   * rounding draws depend on it */
+  uint32_t dtype, flags, v_bits, tensor_id, step, k_lo, k_hi, block0;
   float c_wd, beta1, one_minus_beta1, beta2, one_minus_beta2, bias_correction1, bias_correction2, eps,
       neg_lr, sqrt_block;
 } OrTensor;
@@ -442,8 +453,8 @@ void or_step_tensor(OrTensor* t, uint64_t seed) {
     }
   }
   if (t->flags & OR_FLAG_COMPRESS_V) {              /* :121-163 */
-    or_fused_v_update(t->v_idx, t->v_scales, g, n, (int)t->v_bits, t->beta2, t->one_minus_beta2, t->tensor_id,
-                      t->step, seed, v);
+    or_fused_v_update_at(t->v_idx, t->v_scales, g, n, (int)t->v_bits, t->beta2, t->one_minus_beta2, t->tensor_id,
+                         t->step, seed, (uint64_t)t->block0 * OR_BS, v);
   } else {                                          /* :165-167 */
     for (uint64_t i = 0; i < n; ++i) {
       float a = t->exp_avg_sq[i] * t->beta2;

@@ -1,0 +1,202 @@
+"""Parity at the benchmark configurations' full sizes (GPU, through the C ABI).
+
+A parameter's update depends on that parameter alone: alpha and the two
+thresholds are per tensor, and the Philox counter carries the parameter's index.
+A full-size step is therefore checked against the oracle tensor by tensor, at
+the tensors' real sizes, while the GPU steps the whole configuration in its
+fused passes.  Without CoState the blocks of a parameter are independent as
+well, so block-aligned slices of a 2^28-element parameter check against the
+oracle with their block offset.
+
+Every tensor is also checked for properties that hold at any size:
+* the 1Q indices lie below 2^bits;
+* each block's fp16 scales are ordered;
+* the CoState labels agree with the threshold ranks: at most k_lo blocks fall
+  below the k_lo-th smallest ratio, and at least nb - k_hi reach the k_hi-th.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import bench
+from oracle import oracle as O
+from tests.helpers import compare_states, f16_bits, from_torch, gpu_state, log
+
+pytestmark = pytest.mark.gpu
+
+SEED = 20251
+
+
+def _param_bits(t: torch.Tensor) -> np.ndarray:
+    a = from_torch(t)
+    return a.view(np.uint32) if a.dtype == np.float32 else a
+
+
+def _invariants(opt, params, v_bits, null_pct=0.10, amp_pct=0.90):
+    bad = []
+    for i, p in enumerate(params):
+        st = opt.state[p]
+        nb = (p.numel() + 127) // 128
+        cv = st["compressed_v"]
+        top = int(cv["indices"].max())
+        if top >= (1 << v_bits):
+            bad.append(f"tensor {i}: index {top} >= 2^{v_bits}")
+        sc = cv["scales"].float().reshape(nb, 2)
+        if not bool((sc[:, 0] <= sc[:, 1]).all()):
+            bad.append(f"tensor {i}: unordered 1Q scales")
+        if st["_compress_m"]:
+            k_lo, k_hi = O.ranks(nb, null_pct, amp_pct)
+            cnt = torch.bincount(st["m_mgr"]._encoded["labels"].long(), minlength=3).cpu().tolist()
+            if len(cnt) != 3 or sum(cnt) != nb or cnt[0] > k_lo or cnt[2] < nb - k_hi:
+                bad.append(f"tensor {i}: label counts {cnt} against ranks ({k_lo}, {k_hi}) of {nb} blocks")
+    return bad
+
+
+def _compare_spot(opt, params, orc, spot, where):
+    bad = []
+    for j, i in enumerate(spot):
+        gp = _param_bits(params[i])
+        op = orc.param_groups[0]["params"][j]
+        op = op.view(np.uint32) if op.dtype == np.float32 else op
+        nd = int(np.count_nonzero(gp != op))
+        if nd:
+            bad.append(f"{where} tensor {i}: params differ in {nd}/{gp.size}")
+        bad += compare_states(gpu_state(opt, params[i]), orc.state[j], f"{where} tensor {i}")
+    return bad
+
+
+def test_llama3_8b_shaped_full_steps():
+    """Config C3: all 291 bf16 tensors (8.03e9 params) stepped on the GPU;
+    four of them (both norm shapes, a k and a q projection) against the oracle."""
+    from turboadam_amd import TurboAdam
+
+    shapes = bench.llama3_8b_shapes()
+    names = [s[0] for s in shapes]
+    spot = [names.index(k) for k in ("l0.norm1", "l0.k", "l31.q", "norm")]
+    log(f"C3 full size: {len(shapes)} tensors, spot checks {[names[i] for i in spot]}")
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(5)
+    params = []
+    for name, shp in shapes:
+        p = torch.empty(shp, dtype=torch.bfloat16, device=dev)
+        if "norm" in name:
+            p.fill_(1.0)
+        else:
+            p.normal_(0.0, 0.02, generator=gen)
+        params.append(torch.nn.Parameter(p))
+    kw = dict(lr=3e-4, weight_decay=0.1, v_bits=4)
+    opt = TurboAdam(params, philox_seed=SEED, **kw)
+    orc = O.OracleTurboAdam([from_torch(params[i]) for i in spot], dtypes=[O.DT_BF16] * len(spot), seed=SEED,
+                            tensor_ids=spot, **kw)
+    sig = np.exp(math.log(1e-4) + np.random.default_rng(1).standard_normal(len(shapes)))
+    bad = []
+    for step in range(3):
+        for i, p in enumerate(params):
+            g = torch.randn(p.shape, device=dev, generator=gen, dtype=torch.float32)
+            p.grad = g.mul_(float(sig[i])).to(torch.bfloat16)
+            del g
+        spot_g = [from_torch(params[i].grad) for i in spot]
+        opt.step()
+        torch.cuda.synchronize()
+        orc.step(spot_g)
+        bad += _compare_spot(opt, params, orc, spot, f"step {step + 1}")
+        log(f"  step {step + 1}: GPU step done, oracle spot checks {'ok' if not bad else 'FAILED'}")
+    bad += _invariants(opt, params, 4)
+    assert not bad, "\n".join(bad[:20])
+
+
+def test_v_only_2_28_full_steps_sliced():
+    """Config C1: one fp32 parameter of 2^28 elements, fp32 m, 4-bit v; three
+    block-aligned slices (start, middle, end) against the oracle."""
+    from turboadam_amd import TurboAdam
+
+    n = 1 << 28
+    nb = n // 128
+    slices = [(0, 64), (nb // 2 + 7, nb // 2 + 71), (nb - 64, nb)]
+    log(f"C1 full size: {n} elements, slices {slices}")
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(9)
+    p = torch.nn.Parameter(torch.empty(n, dtype=torch.float32, device=dev).normal_(0.0, 0.02, generator=gen))
+    kw = dict(lr=1e-3, compress_m=False, v_bits=4)
+    opt = TurboAdam([p], philox_seed=SEED, **kw)
+    p0 = from_torch(p)
+    orc = O.OracleTurboAdam([p0[a * 128:b * 128].copy() for a, b in slices], seed=SEED,
+                            tensor_ids=[0] * len(slices), block0=[a for a, _ in slices], **kw)
+    del p0
+    bad = []
+    for step in range(3):
+        p.grad = torch.randn(n, device=dev, generator=gen, dtype=torch.float32).mul_(1e-3)
+        g = from_torch(p.grad)
+        opt.step()
+        torch.cuda.synchronize()
+        orc.step([g[a * 128:b * 128].copy() for a, b in slices])
+        gp = _param_bits(p)
+        st = opt.state[p]
+        idx = from_torch(st["compressed_v"]["indices"])
+        sc = f16_bits(st["compressed_v"]["scales"])
+        ea = from_torch(st["exp_avg"]).view(np.uint32)
+        for j, (a, b) in enumerate(slices):
+            ost = orc.state[j]
+            where = f"step {step + 1} blocks [{a}, {b})"
+            if not np.array_equal(gp[a * 128:b * 128], orc.param_groups[0]["params"][j].view(np.uint32)):
+                bad.append(f"{where}: params differ")
+            if not np.array_equal(idx[a * 128:b * 128], ost["indices"]):
+                bad.append(f"{where}: indices differ")
+            if not np.array_equal(sc[2 * a:2 * b], ost["scales"]):
+                bad.append(f"{where}: scales differ")
+            if not np.array_equal(ea[a * 128:b * 128], ost["exp_avg"].view(np.uint32)):
+                bad.append(f"{where}: exp_avg differs")
+        log(f"  step {step + 1}: {'ok' if not bad else 'FAILED'}")
+        del g
+    bad += _invariants(opt, [p], 4)
+    assert not bad, "\n".join(bad[:20])
+
+
+def test_gpt2_124m_sparse_embedding_full_steps():
+    """Config C2: GPT-2 124M fp32 (148 tensors), Student-t(3) gradients, the
+    token embedding with all but 5% of its rows exactly zero each step; the
+    embedding, an MLP projection and a LayerNorm bias against the oracle."""
+    from turboadam_amd import TurboAdam
+
+    shapes = bench.gpt2_124m_shapes()
+    names = [s[0] for s in shapes]
+    spot = [names.index(k) for k in ("wte", "h11.mlp.c_proj.w", "ln_f.b")]
+    log(f"C2 full size: {len(shapes)} tensors, spot checks {[names[i] for i in spot]}")
+    dev = torch.device("cuda:0")
+    cpu = torch.Generator().manual_seed(13)
+    params = []
+    for name, shp in shapes:
+        if name.startswith("ln") or ".ln_" in name:
+            t = torch.ones(shp) if name.endswith(".w") else torch.zeros(shp)
+        else:
+            t = torch.randn(shp, generator=cpu) * 0.02
+        params.append(torch.nn.Parameter(t.to(dev)))
+    kw = dict(lr=6e-4, weight_decay=0.1, v_bits=4)
+    opt = TurboAdam(params, philox_seed=SEED, **kw)
+    orc = O.OracleTurboAdam([from_torch(params[i]) for i in spot], seed=SEED, tensor_ids=spot, **kw)
+    sig = np.exp(math.log(1e-3) + np.random.default_rng(2).standard_normal(len(shapes)))
+    wte_rows = shapes[0][1][0]
+    bad = []
+    for step in range(2):
+        for i, (p, (name, shp)) in enumerate(zip(params, shapes)):
+            z = torch.randn(shp, generator=cpu)
+            chi = torch.distributions.Chi2(torch.tensor(3.0)).sample(shp)
+            g = z / torch.sqrt(chi / 3.0) * float(sig[i])
+            if name == "wte":
+                keep = torch.zeros(wte_rows, dtype=torch.bool)
+                keep[torch.randperm(wte_rows, generator=cpu)[: wte_rows // 20]] = True
+                g[~keep] = 0.0
+            p.grad = g.to(torch.float32).to(dev)
+        spot_g = [from_torch(params[i].grad) for i in spot]
+        opt.step()
+        torch.cuda.synchronize()
+        orc.step(spot_g)
+        bad += _compare_spot(opt, params, orc, spot, f"step {step + 1}")
+        log(f"  step {step + 1}: {'ok' if not bad else 'FAILED'}")
+    bad += _invariants(opt, params, 4)
+    assert not bad, "\n".join(bad[:20])

@@ -124,3 +124,16 @@ def test_constructor_validation_matches_reference():
         (1e-3, (0.9, 0.999), 1e-8, 0.0, 128, 4)
     assert d["compress_m"] is True and d["compress_v"] is True
     assert (d["null_pct"], d["amp_pct"], d["min_m_compress_elements"]) == (0.10, 0.90, 4096)
+
+
+def test_philox_seed_keyword():
+    from turboadam_amd import TurboAdam
+    from turboadam_amd.quantize import DEFAULT_SEED
+
+    ps = [torch.nn.Parameter(torch.randn(4))]
+    assert TurboAdam(ps).philox_seed == DEFAULT_SEED
+    assert TurboAdam(ps, philox_seed=(1 << 64) - 1).philox_seed == (1 << 64) - 1
+    with pytest.raises(ValueError, match="philox_seed"):
+        TurboAdam(ps, philox_seed=-1)
+    with pytest.raises(TypeError):
+        TurboAdam(ps, 1e-3, (0.9, 0.999), 1e-8, 0.0, 128, 4, True, True, 0.1, 0.9, False, False, 4096, 7)

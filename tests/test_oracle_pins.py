@@ -328,3 +328,31 @@ def test_v_update_invariants_and_unbiased_rounding():
     lo = np.min(lv); hi = np.max(lv)
     cont = np.minimum((lv - lo) / (hi - lo) * 16, 15)
     assert abs((acc / T - cont).mean()) < 0.05
+
+
+def test_block_slice_draws_as_the_whole_parameter():
+    # Without CoState every block of a parameter updates independently; a
+    # block-aligned slice stepped with its block offset (and the parameter's
+    # tensor id) must reproduce those blocks of the whole parameter exactly.
+    rng = np.random.default_rng(3)
+    nb, b0, b1 = 40, 13, 29
+    n = nb * O.BS
+    p0 = (rng.standard_normal(n) * 0.02).astype(np.float32)
+    kw = dict(lr=1e-3, compress_m=False, v_bits=4)
+    whole = O.OracleTurboAdam([p0.copy()], seed=77, tensor_ids=[5], **kw)
+    part = O.OracleTurboAdam([p0[b0 * O.BS:b1 * O.BS].copy()], seed=77, tensor_ids=[5], block0=[b0], **kw)
+    shifted = O.OracleTurboAdam([p0[b0 * O.BS:b1 * O.BS].copy()], seed=77, tensor_ids=[5], **kw)
+    for _ in range(3):
+        g = (rng.standard_normal(n) * 1e-3).astype(np.float32)
+        whole.step([g])
+        part.step([g[b0 * O.BS:b1 * O.BS].copy()])
+        shifted.step([g[b0 * O.BS:b1 * O.BS].copy()])
+    sl = slice(b0 * O.BS, b1 * O.BS)
+    w, s = whole.state[0], part.state[0]
+    assert np.array_equal(whole.param_groups[0]["params"][0][sl].view(np.uint32),
+                          part.param_groups[0]["params"][0].view(np.uint32))
+    assert np.array_equal(w["indices"][sl], s["indices"])
+    assert np.array_equal(w["scales"][2 * b0:2 * b1], s["scales"])
+    assert np.array_equal(w["exp_avg"][sl].view(np.uint32), s["exp_avg"].view(np.uint32))
+    # the offset matters: without it the slice draws other uniforms
+    assert not np.array_equal(w["indices"][sl], shifted.state[0]["indices"])

@@ -67,6 +67,9 @@ class TurboAdam(Optimizer):
         block_size=128, v_bits in {2,3,4,6,8} (default 4), compress_m=True,
         compress_v=True, null_pct=0.10, amp_pct=0.90, error_feedback=False,
         capturable=False, min_m_compress_elements=4096.
+
+    philox_seed (keyword only, an addition): the 64-bit key of the Philox
+    stream that drives stochastic rounding (attribute of the same name).
     """
 
     def __init__(
@@ -85,6 +88,8 @@ class TurboAdam(Optimizer):
         error_feedback: bool = False,
         capturable: bool = False,
         min_m_compress_elements: int = 4096,
+        *,
+        philox_seed: int = DEFAULT_SEED,
     ):
         if v_bits not in (2, 3, 4, 6, 8):
             raise ValueError(f"v_bits must be one of {{2, 3, 4, 6, 8}}, got {v_bits}")
@@ -106,7 +111,9 @@ class TurboAdam(Optimizer):
         )
         super().__init__(params, defaults)
         self._group_step_tensors = {}
-        self.philox_seed = DEFAULT_SEED
+        if not 0 <= int(philox_seed) < (1 << 64):
+            raise ValueError(f"philox_seed must be a 64-bit unsigned integer, got {philox_seed}")
+        self.philox_seed = int(philox_seed)
         self._buffers = {}
         self._bc_values = {}
         # Optional callable(pass_index, "begin"|"end") run around each of the four
