@@ -200,3 +200,45 @@ def test_gpt2_124m_sparse_embedding_full_steps():
         log(f"  step {step + 1}: {'ok' if not bad else 'FAILED'}")
     bad += _invariants(opt, params, 4)
     assert not bad, "\n".join(bad[:20])
+
+
+@pytest.mark.parametrize("bits", [2, 3, 6, 8])
+@pytest.mark.parametrize("pct", [(0.10, 0.90), (0.05, 0.95)])
+def test_ragged_1000_tensors_full_steps(bits, pct):
+    """Config C4: 1000 fp32 tensors of sizes round(2^(20U)) (CoState from 4096
+    elements, tail blocks almost everywhere), each v_bits x percentile run;
+    twelve tensors of every size class against the oracle."""
+    from turboadam_amd import TurboAdam
+
+    shapes = bench.ragged_shapes()
+    sizes = np.array([s[1][0] for s in shapes])
+    order = np.argsort(sizes, kind="stable")
+    picks = [order[0], order[-1]]
+    picks.append(int(np.flatnonzero(sizes < 128)[0]))
+    picks.append(int(np.flatnonzero((sizes > 128) & (sizes < 4096) & (sizes % 128 != 0))[0]))
+    picks.append(int(np.flatnonzero((sizes >= 4096) & (sizes % 128 != 0))[0]))
+    picks.append(int(np.flatnonzero(sizes % 128 == 0)[0]))
+    rng = np.random.default_rng(bits * 10 + int(pct[0] * 100))
+    picks += [int(i) for i in rng.choice(len(shapes), 6, replace=False)]
+    spot = sorted(set(int(i) for i in picks))
+    log(f"C4 full size: {len(shapes)} tensors ({int(sizes.sum())} params), v_bits={bits}, pct={pct}, "
+        f"spot sizes {[int(sizes[i]) for i in spot]}")
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(bits)
+    params = [torch.nn.Parameter(torch.empty(s[1], device=dev).normal_(0.0, 0.02, generator=gen)) for s in shapes]
+    kw = dict(lr=1e-3, v_bits=bits, null_pct=pct[0], amp_pct=pct[1])
+    opt = TurboAdam(params, philox_seed=SEED + bits, **kw)
+    orc = O.OracleTurboAdam([from_torch(params[i]) for i in spot], seed=SEED + bits, tensor_ids=spot, **kw)
+    bad = []
+    for step in range(4):
+        for p in params:
+            p.grad = torch.randn(p.shape, device=dev, generator=gen).mul_(1e-3)
+        spot_g = [from_torch(params[i].grad) for i in spot]
+        opt.step()
+        torch.cuda.synchronize()
+        orc.step(spot_g)
+        bad += _compare_spot(opt, params, orc, spot, f"step {step + 1}")
+    log(f"  4 steps: {'ok' if not bad else 'FAILED'}")
+    bad += _invariants(opt, params, bits, *pct)
+    assert not bad, "\n".join(bad[:20])
