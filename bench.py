@@ -3,11 +3,11 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c3]
 
 A step is one TurboAdam.step() over the whole synthetic parameter set with
-its gradients already resident in HBM.  Default workload (the headline of
-BASELINE.json): the Llama-3-8B-shaped parameter set (291 tensors,
+its gradients already resident in HBM.  Default workload (the headline
+configuration): the Llama-3-8B-shaped parameter set (291 tensors,
 8,030,261,248 parameters) in bf16, m+v compression, v_bits=4.  Prints one
 JSON line with throughput (parameters updated per second), the roofline of
-the dominant kernel (pass 1) timed live with HIP events on the launch stream,
+the dominant pass (pass 0) timed live with HIP events on the launch stream,
 and a CPU baseline: the reference's CPU step (restated op for op in torch,
 oracle/torch_mirror.py) timed on a bounded sample on this host.
 """
@@ -81,9 +81,9 @@ WORKLOADS = {
 
 
 def bytes_per_param(dtype_bytes: int, costate: bool, compress_v: bool = True):
-    """Algorithmic HBM bytes per parameter per step (whole step and pass 1 alone).
+    """Algorithmic HBM bytes per parameter per step (whole step and pass 0 alone).
 
-    pass 1 reads p, g, the 1Q indices and scales and (CoState) the previous
+    pass 0 reads p, g, the 1Q indices and scales and (CoState) the previous
     signs/labels/norms/amplitudes and writes p, indices and scales; an fp32-m
     tensor reads and writes exp_avg instead.  CoState adds pass 2 (g, the
     previous encoding, new encoding, ratios) and the selection (ratios, labels).
@@ -238,7 +238,7 @@ def main():
         opt.step()
     torch.cuda.synchronize()
 
-    # timed region: K steps; pass 1 bracketed by events on the launch stream
+    # timed region: K steps; pass 0 bracketed by events on the launch stream
     ev = []
 
     def hook(k, when):
@@ -297,7 +297,7 @@ def main():
             "step_hbm_frac": step_gbps / HBM_PEAK_GBPS,
         },
         "roofline": {
-            "kernel": "pass 1 (tam_k1_main_<dtype> + tam_k1_tail)",
+            "kernel": "pass 0 (tam_k1_main_<dtype> + tam_k1_tail)",
             "bound": "hbm",
             "achieved": k1_gbps,
             "peak": HBM_PEAK_GBPS,

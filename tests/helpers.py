@@ -1,6 +1,8 @@
 """Shared helpers: run the GPU TurboAdam and the CPU oracle side by side."""
 
+import contextlib
 import sys
+import types
 
 import numpy as np
 import torch
@@ -160,3 +162,83 @@ def run_side_by_side(sizes, dts, steps, seed=0, check_every=1, shapes=None, grad
             if bad:
                 return bad
     return bad
+
+
+REFERENCE_MANAGER_ATTRS = ("block_size", "_null_pct", "_amp_pct", "_has_state", "_alpha", "_encoded",
+                           "_original_numel", "_error_feedback", "_ef_residual")
+
+
+@contextlib.contextmanager
+def reference_manager_class():
+    """A class that pickles under the reference's name
+    turboadam.costate.CoStateManager, for writing checkpoints in the reference's
+    format (its state dict pickles the manager's attribute dict,
+    costate.py:357-365) without the reference package."""
+    pkg, mod = types.ModuleType("turboadam"), types.ModuleType("turboadam.costate")
+
+    class CoStateManager:
+        pass
+
+    CoStateManager.__module__ = "turboadam.costate"
+    CoStateManager.__qualname__ = "CoStateManager"
+    mod.CoStateManager = CoStateManager
+    pkg.costate = mod
+    saved = {k: sys.modules.get(k) for k in ("turboadam", "turboadam.costate")}
+    sys.modules["turboadam"], sys.modules["turboadam.costate"] = pkg, mod
+    try:
+        yield CoStateManager
+    finally:
+        for k, v in saved.items():
+            if v is None:
+                sys.modules.pop(k, None)
+            else:
+                sys.modules[k] = v
+
+
+def reference_state_dict(orc, shapes, ref_cls, device="cpu"):
+    """The reference optimizer's state_dict (optimizer.py:238-286 layout) for
+    the oracle's current state: CoState managers as ref_cls objects, the 1Q
+    dict with a rand_buf, shared bias-correction tensors."""
+    state, pid = {}, 0
+    bc = (torch.zeros(1), torch.zeros(1))
+    groups = []
+    for grp in orc.param_groups:
+        ids = []
+        for p in grp["params"]:
+            if pid in orc.state:
+                st = orc.state[pid]
+                n = p.size
+                nb = (n + O.BS - 1) // O.BS
+                out = {"step": st["step"], "_compress_m": st["_compress_m"], "_bc1": bc[0], "_bc2": bc[1]}
+                if st["_compress_m"]:
+                    m = ref_cls()
+                    m.block_size, m._null_pct, m._amp_pct = O.BS, grp["null_pct"], grp["amp_pct"]
+                    m._has_state, m._original_numel = bool(st["has_state"]), n
+                    m._error_feedback, m._ef_residual = False, None
+                    m._alpha = torch.tensor(float(st["alpha"][0]), dtype=torch.float32)
+                    m._encoded = {
+                        "labels": torch.from_numpy(st["labels"].copy()),
+                        "sign_packed": torch.from_numpy(st["sign_packed"].copy()),
+                        "block_norms": torch.from_numpy(st["block_norms"].copy()),
+                        "scales": torch.from_numpy(st["amp"].view(np.int16).copy()).view(torch.float16),
+                    }
+                    out["m_mgr"] = m
+                else:
+                    out["exp_avg"] = torch.from_numpy(st["exp_avg"].copy()).reshape(shapes[pid])
+                if "exp_avg_sq" in st:
+                    out["exp_avg_sq"] = torch.from_numpy(st["exp_avg_sq"].copy()).reshape(shapes[pid])
+                if "indices" in st:
+                    out["compressed_v"] = {
+                        "indices": torch.from_numpy(st["indices"].copy()),
+                        "scales": torch.from_numpy(st["scales"].view(np.int16).copy()).view(torch.float16)
+                                       .reshape(nb, 2),
+                        "n_bits": grp["v_bits"], "original_shape": torch.Size(shapes[pid]), "original_length": n,
+                        "block_size": O.BS, "rand_buf": torch.zeros(nb * O.BS),
+                    }
+                state[pid] = out
+            ids.append(pid)
+            pid += 1
+        g = {k: v for k, v in grp.items() if k != "params"}
+        g["params"] = ids
+        groups.append(g)
+    return {"state": state, "param_groups": groups}

@@ -10,6 +10,7 @@ try:
 except PackageNotFoundError:
     __version__ = "0.1.0"
 
+from .checkpoint import load_reference_checkpoint  # noqa: E402
 from .optimizer import TurboAdam  # noqa: E402
 
-__all__ = ["TurboAdam"]
+__all__ = ["TurboAdam", "load_reference_checkpoint"]

@@ -191,6 +191,27 @@ class TurboAdam(Optimizer):
     # ------------------------------------------------------------------
     _PACKED_V = {"indices": torch.uint8, "scales": torch.float16}
 
+    def state_dict(self):
+        """torch's optimizer state dict plus the Philox key ("philox_seed"), so
+        that a resumed run draws the same stochastic rounding."""
+        sd = super().state_dict()
+        sd["philox_seed"] = self.philox_seed
+        return sd
+
+    @staticmethod
+    def _adopt_manager(mgr, group) -> CoStateManager:
+        """A CoStateManager of this package holding mgr's state.  mgr may be one
+        loaded from a reference checkpoint (only the attributes the reference
+        pickles, costate.py:357-365); settings it lacks come from the group."""
+        new = CoStateManager(block_size=getattr(mgr, "block_size", group["block_size"]),
+                             error_feedback=getattr(mgr, "_error_feedback", group["error_feedback"]),
+                             null_pct=getattr(mgr, "_null_pct", group["null_pct"]),
+                             amp_pct=getattr(mgr, "_amp_pct", group["amp_pct"]))
+        for key in ("_has_state", "_alpha", "_encoded", "_original_numel", "_ef_residual"):
+            if hasattr(mgr, key):
+                setattr(new, key, getattr(mgr, key))
+        return new
+
     def load_state_dict(self, state_dict):
         """Load optimizer state.
 
@@ -199,8 +220,13 @@ class TurboAdam(Optimizer):
         tensors are kept aside and restored unchanged, so a resumed run
         continues bit for bit; CoStateManager tensors are moved to the
         parameter's device as in the reference; a reference checkpoint's
-        `rand_buf` is dropped (this implementation draws from Philox).
+        `rand_buf` is dropped (this implementation draws from Philox), and its
+        CoStateManager objects are adopted into this package's class.  A
+        "philox_seed" entry (written by state_dict) restores the Philox key.
         """
+        if "philox_seed" in state_dict:
+            state_dict = dict(state_dict)
+            self.philox_seed = int(state_dict.pop("philox_seed"))
         saved_v = {}
         for pid, st in state_dict.get("state", {}).items():
             cv = st.get("compressed_v") if isinstance(st, dict) else None
@@ -229,6 +255,7 @@ class TurboAdam(Optimizer):
                             cv[k] = src.to(device=device, dtype=dt).clone().contiguous()
                 mgr = state.get("m_mgr")
                 if mgr is not None:
+                    mgr = state["m_mgr"] = self._adopt_manager(mgr, group)
                     if isinstance(mgr._alpha, torch.Tensor):
                         mgr._alpha = mgr._alpha.to(device=device, dtype=torch.float32).clone()
                     else:
