@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define TAM_ABI_VERSION 2
+#define TAM_ABI_VERSION 3
 #define TAM_BLOCK_SIZE 128 /* elements per quantisation / CoState block */
 
 /* error codes */
@@ -78,7 +78,7 @@ typedef struct TamTensor {
   float beta1, one_minus_beta1, beta2, one_minus_beta2; /* [in] f32 of the doubles */
   float bias_correction1, bias_correction2;             /* [in] f32(1-beta^step)   */
   float eps, neg_lr;    /* [in] f32(eps), f32(-lr)                           */
-  float sqrt_block;     /* [in] f32(sqrt(128))                               */
+  float sqrt_block;     /* [in] f32(sqrt(128)) (the only block size)         */
   uint32_t nb;          /* [derived] ceil(n/128)                             */
   uint32_t tile0;       /* [derived] first tile (16 blocks) of this tensor   */
   uint32_t ntiles;      /* [derived] ceil(nb/16)                             */
@@ -86,7 +86,7 @@ typedef struct TamTensor {
   uint64_t ratio_off;   /* [derived] COSTATE: offset of its ratios (blocks)  */
   double inv_bc2;       /* [in] 1 / (double)bias_correction2 (correctly rounded) */
   uint32_t slice0;      /* [derived] COSTATE: first selection slice (8192 blocks each) */
-  uint32_t sel_pad;
+  float c_lr;           /* [derived] f32(neg_lr / bias_correction1)          */
 } TamTensor;
 
 /* Launch summary and workspace layout, filled by tam_prepare(). */

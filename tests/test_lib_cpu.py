@@ -7,6 +7,7 @@ import ctypes
 import os
 import re
 
+import numpy as np
 import pytest
 import torch
 
@@ -49,6 +50,8 @@ def _tensor(n, costate=True, compress_v=True, bits=4):
     t.signs = t.labels = t.norms = t.amp = t.alpha = 0x60000
     nb = (n + 127) // 128
     t.k_lo, t.k_hi = max(0, int(0.1 * nb) - 1), min(nb - 1, int(0.9 * nb))
+    t.sqrt_block = np.float32(np.sqrt(128.0))
+    t.neg_lr, t.bias_correction1 = np.float32(-3e-4), np.float32(1.0 - 0.9 ** 3)
     return t
 
 
@@ -75,6 +78,8 @@ def test_prepare_layout():
     assert info.total_chunks == 2 and [a.chunk0 for a in arr] == [0, 1, 1]
     assert info.off_chunks >= info.off_ratios + 300 * 4 and info.ws_bytes >= info.off_chunks + 2 * 16
     assert info.off_alpha % 256 == 0 and info.off_ratios % 256 == 0
+    # derived: fl(-lr / bc1) as an fp32 division
+    assert np.float32(arr[0].c_lr) == np.float32(-3e-4) / np.float32(1.0 - 0.9 ** 3)
 
 
 @pytest.mark.parametrize("mutate,msg", [
@@ -84,6 +89,7 @@ def test_prepare_layout():
     (lambda t: setattr(t, "alpha", 0), "CoState"),
     (lambda t: setattr(t, "v_idx", 0x30001), "misaligned"),
     (lambda t: setattr(t, "k_hi", 10_000), "rank"),
+    (lambda t: setattr(t, "sqrt_block", 11.0), "sqrt_block"),
 ])
 def test_prepare_rejects_bad_input(mutate, msg):
     t = _tensor(5000)

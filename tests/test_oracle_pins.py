@@ -356,3 +356,26 @@ def test_block_slice_draws_as_the_whole_parameter():
     assert np.array_equal(w["exp_avg"][sl].view(np.uint32), s["exp_avg"].view(np.uint32))
     # the offset matters: without it the slice draws other uniforms
     assert not np.array_equal(w["indices"][sl], shifted.state[0]["indices"])
+
+
+def test_division_by_sqrt_block_as_fp64_product():
+    # The kernels form fl(x / fl(sqrt(128))) (costate.py:306) as the fp32
+    # rounding of x times the fp64 reciprocal; equal to the fp32 division for
+    # every non-negative fp32 x (norms), checked exhaustively (negative x
+    # follows by symmetry).
+    c = np.float32(math.sqrt(128.0))
+    r = 1.0 / float(c)
+    step = 1 << 22  # 0x7F800000 is a multiple
+    base = np.arange(step, dtype=np.uint32)
+    xu = np.empty(step, np.uint32)
+    prod = np.empty(step, np.float64)
+    a = np.empty(step, np.float32)
+    q = np.empty(step, np.float32)
+    x = xu.view(np.float32)
+    for start in range(0, 0x7F800000, step):
+        np.add(base, np.uint32(start), out=xu)
+        np.copyto(prod, x)  # exact widening, then one fp64 product
+        np.multiply(prod, r, out=prod)
+        np.copyto(a, prod, casting="unsafe")
+        np.divide(x, c, out=q)
+        assert np.array_equal(a.view(np.uint32), q.view(np.uint32)), hex(start)

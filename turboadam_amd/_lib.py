@@ -25,7 +25,7 @@ TAM_FLAG_COMPRESS_V = 0x2
 TAM_FLAG_HAS_STATE = 0x4
 TAM_FLAG_WD = 0x8
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 
 class TamTensor(ctypes.Structure):
@@ -67,7 +67,7 @@ class TamTensor(ctypes.Structure):
         ("ratio_off", ctypes.c_uint64),
         ("inv_bc2", ctypes.c_double),
         ("slice0", ctypes.c_uint32),
-        ("sel_pad", ctypes.c_uint32),
+        ("c_lr", ctypes.c_float),
     ]
 
 

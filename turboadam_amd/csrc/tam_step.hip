@@ -362,6 +362,17 @@ __device__ __forceinline__ TamCsIn tam_cs_load(const TamTensor& d, const TamWave
   return c;
 }
 
+// fl(x / fl(sqrt(128))) (costate.py:306, true division) as the fp64 product of
+// x and the correctly rounded fp64 reciprocal of fl(sqrt(128)): its error is
+// below 2^-52 relative, while a quotient of two 24-bit significands never lies
+// within 2^-49 of an fp32 rounding boundary, so the fp32 rounding of the
+// product is the correctly rounded quotient for every fp32 x (also checked
+// exhaustively on the host).
+#define TAM_SQRT_BLOCK_F 0x1.6a09e6p+3f
+__device__ __forceinline__ float tam_div_sqrt_block(float x) {
+  return (float)((double)x * (1.0 / (double)TAM_SQRT_BLOCK_F));
+}
+
 template <bool FULL>
 __device__ __forceinline__ void tam_costate_m(const TamTensor& d, const TamWave& W, const TamCsIn& cs,
                                               float alpha_prev, const float* g, float* m) {
@@ -370,7 +381,7 @@ __device__ __forceinline__ void tam_costate_m(const TamTensor& d, const TamWave&
     float s = 0.0f;
     const uint32_t byte = cs.byte;
     if (FULL || W.bvalid) {
-      const float sph = cs.nrm / d.sqrt_block;
+      const float sph = tam_div_sqrt_block(cs.nrm);
       s = cs.label == 1u ? sph : (cs.label == 2u ? tam_f16_to_f32((uint16_t)cs.amp) : 0.0f);
     }
 #pragma unroll
@@ -662,8 +673,9 @@ __device__ __forceinline__ void tam_update(const TamTensor& d, float* p, const f
 #pragma unroll
     for (int i = 0; i < TAM_EPL; ++i) pw[i] = p[i];
   }
-  // -lr / bc1 (one more rounding in the fast sequence, inside the 2^-19 bound)
-  const float c_lr = d.neg_lr / d.bias_correction1;
+  // c_lr = fl(-lr / bc1), from tam_prepare (one more rounding in the fast
+  // sequence, inside the 2^-19 bound)
+  const float c_lr = d.c_lr;
   // per-element acceptance as lane masks (no per-element VALU to combine them)
   bool okv[TAM_EPL];
   bool all_ok = true;
@@ -1355,7 +1367,7 @@ __device__ __forceinline__ TamTensor tam_local_desc(uint64_t n) {
   d.n = n;
   d.nb = (uint32_t)((n + TAM_BLOCK_SIZE - 1) / TAM_BLOCK_SIZE);
   d.ntiles = tam_tiles_of(n);
-  d.sqrt_block = 0x1.6a09e6p+3f;  // f32(sqrt(128))
+  d.sqrt_block = TAM_SQRT_BLOCK_F;
   return d;
 }
 
@@ -1392,7 +1404,7 @@ __global__ __launch_bounds__(TAM_WG) void tam_k_decode(const uint8_t* __restrict
     tam_costate_m<false>(d, W, cs, a, gv, m);
   } else {
     // m_hat alone: fl(alpha*g) + s_b*sign (costate.py:317-323)
-    const float sph = cs.nrm / d.sqrt_block;
+    const float sph = tam_div_sqrt_block(cs.nrm);
     const float sb = cs.label == 1u ? sph : (cs.label == 2u ? tam_f16_to_f32((uint16_t)cs.amp) : 0.0f);
 #pragma unroll
     for (int i = 0; i < TAM_EPL; ++i) {
@@ -1491,7 +1503,7 @@ __global__ __launch_bounds__(TAM_WG) void tam_k_encode(const float* __restrict__
   if (W.l16 == 0) {
     const float nd = (float)__builtin_sqrt(sd);
     norms[W.b] = nd;
-    amp[W.b] = tam_f32_to_f16(nd / d.sqrt_block);
+    amp[W.b] = tam_f32_to_f16(tam_div_sqrt_block(nd));
   }
 }
 
@@ -1721,6 +1733,8 @@ int tam_prepare(TamTensor* tensors, int n_tensors, TamStepInfo* info) {
     TamTensor& t = tensors[i];
     if (t.n == 0) return tam_fail(TAM_E_INVALID, "%stensor %ld has no elements", "", i);
     if (t.dtype > TAM_DTYPE_F16) return tam_fail(TAM_E_INVALID, "%stensor %ld: unknown dtype", "", i);
+    if (t.sqrt_block != TAM_SQRT_BLOCK_F)
+      return tam_fail(TAM_E_INVALID, "%stensor %ld: sqrt_block must be f32(sqrt(128))", "", i);
     if (!t.param || !t.grad) return tam_fail(TAM_E_INVALID, "%stensor %ld: null param/grad", "", i);
     const uint64_t nb = (t.n + TAM_BLOCK_SIZE - 1) / TAM_BLOCK_SIZE;
     if (nb > (1ull << 31)) return tam_fail(TAM_E_INVALID, "%stensor %ld too large", "", i);
@@ -1751,7 +1765,7 @@ int tam_prepare(TamTensor* tensors, int n_tensors, TamStepInfo* info) {
     dtype_mask |= 1u << t.dtype;
     t.chunk0 = (uint32_t)chunks;
     t.slice0 = (uint32_t)slices;
-    t.sel_pad = 0;
+    t.c_lr = t.neg_lr / t.bias_correction1;  // fp32 division, correctly rounded
     tiles += nt;
     chunks += tam_alpha_chunks(t.flags, t.ntiles);
     slices += tam_sel_slices(t.flags, t.nb);
