@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define TAM_ABI_VERSION 3
+#define TAM_ABI_VERSION 4
 #define TAM_BLOCK_SIZE 128 /* elements per quantisation / CoState block */
 
 /* error codes */
@@ -46,6 +46,8 @@ extern "C" {
 #define TAM_FLAG_COMPRESS_V 0x2u /* v kept as 1Q indices (else fp32 exp_avg_sq) */
 #define TAM_FLAG_HAS_STATE 0x4u  /* CoState holds a previous encoding          */
 #define TAM_FLAG_WD 0x8u         /* apply decoupled weight decay p *= c_wd     */
+#define TAM_FLAG_EF 0x10u        /* COSTATE with error feedback (ef_residual)  */
+#define TAM_FLAG_HAS_EF 0x20u    /* EF: ef_residual holds a residual           */
 
 /* One parameter tensor of one optimizer step.  The caller fills the fields
  * marked [in]; tam_prepare() fills the fields marked [derived].  The array is
@@ -87,6 +89,9 @@ typedef struct TamTensor {
   double inv_bc2;       /* [in] 1 / (double)bias_correction2 (correctly rounded) */
   uint32_t slice0;      /* [derived] COSTATE: first selection slice (8192 blocks each) */
   float c_lr;           /* [derived] f32(neg_lr / bias_correction1)          */
+  float* ef_residual;   /* [in] EF: f32[n] error-feedback residual (in/out;  */
+                        /*      written, not read, without HAS_EF)           */
+  uint64_t ef_off;      /* [derived] EF: workspace offset of the staged encoding */
 } TamTensor;
 
 /* Launch summary and workspace layout, filled by tam_prepare(). */
@@ -105,6 +110,9 @@ typedef struct TamStepInfo {
   uint64_t off_chunks;
   uint64_t off_sel;
   uint64_t off_hist;
+  uint32_t n_ef;           /* tensors with error feedback (a fifth pass runs) */
+  uint32_t info_pad;
+  uint64_t off_ef_alpha;   /* EF: previous alpha of each tensor (f32 per tensor) */
 } TamStepInfo;
 
 /* Version of this ABI (TAM_ABI_VERSION). */
@@ -136,11 +144,12 @@ int tam_multi_tensor_step(const TamTensor* d_tensors, const TamTensor* h_tensors
                           const TamStepInfo* info, uint64_t seed, void* workspace,
                           size_t ws_bytes, void* stream);
 
-/* One of the four launches of tam_multi_tensor_step (same arguments):
- * pass 0 = fused pass 1, 1 = alpha, 2 = CoState encode, 3 = selection and
- * labels.  Issuing passes 0..3 in order on one stream equals one
- * tam_multi_tensor_step call; callers use it to time the launches one by one.
- * No counterpart in the reference (its step is not split into passes). */
+/* One of the passes of tam_multi_tensor_step (same arguments): 0 = the fused
+ * update, 1 = alpha, 2 = CoState encode, 3 = selection and labels, 4 = the
+ * error-feedback residual and commit of the staged encoding (nothing to do
+ * without TAM_FLAG_EF tensors).  Issuing passes 0..4 in order on one stream
+ * equals one tam_multi_tensor_step call; callers use it to time the passes one
+ * by one.  No counterpart in the reference (its step is not split into passes). */
 int tam_step_pass(int pass, const TamTensor* d_tensors, const TamStepInfo* info, uint64_t seed,
                   void* workspace, size_t ws_bytes, void* stream);
 

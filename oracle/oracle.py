@@ -20,7 +20,7 @@ import numpy as np
 from .build import LIB_PATH, build_oracle
 
 DT_F32, DT_BF16, DT_F16 = 0, 1, 2
-FLAG_COSTATE, FLAG_COMPRESS_V, FLAG_HAS_STATE, FLAG_WD = 1, 2, 4, 8
+FLAG_COSTATE, FLAG_COMPRESS_V, FLAG_HAS_STATE, FLAG_WD, FLAG_EF, FLAG_HAS_EF = 1, 2, 4, 8, 16, 32
 BS = 128
 # f16(log(f32(1e-30))): the initial 1Q scale (reference oneq.py:13-48 on full(1e-30)).
 V_INIT_SCALE_BITS = np.float16(-69.0625).view(np.uint16)
@@ -32,7 +32,7 @@ class OrTensor(ctypes.Structure):
     _fields_ = [
         ("param", _VP), ("grad", _VP), ("v_idx", _VP), ("v_scales", _VP), ("exp_avg_sq", _VP),
         ("exp_avg", _VP), ("signs", _VP), ("labels", _VP), ("norms", _VP), ("amp", _VP), ("alpha", _VP),
-        ("n", ctypes.c_uint64),
+        ("ef_residual", _VP), ("n", ctypes.c_uint64),
         ("dtype", ctypes.c_uint32), ("flags", ctypes.c_uint32), ("v_bits", ctypes.c_uint32),
         ("tensor_id", ctypes.c_uint32), ("step", ctypes.c_uint32), ("k_lo", ctypes.c_uint32),
         ("k_hi", ctypes.c_uint32), ("block0", ctypes.c_uint32),
@@ -78,6 +78,9 @@ def lib():
                                            ctypes.c_uint32, ctypes.c_uint64, _VP, _VP]
         L.or_costate_update.argtypes = [_VP, ctypes.c_uint64, ctypes.c_float, ctypes.c_float, ctypes.c_float,
                                         ctypes.c_uint64, ctypes.c_uint64, ctypes.c_int, _VP, _VP, _VP, _VP, _VP, _VP]
+        L.or_costate_update_ef.argtypes = [_VP, ctypes.c_uint64, ctypes.c_float, ctypes.c_float, ctypes.c_float,
+                                           ctypes.c_uint64, ctypes.c_uint64, ctypes.c_int, _VP, _VP, _VP, _VP, _VP,
+                                           ctypes.c_int, ctypes.c_int, _VP, _VP]
         L.or_struct_size.restype = ctypes.c_size_t
         if L.or_struct_size() != ctypes.sizeof(OrTensor):
             raise RuntimeError("oracle struct layout mismatch")
@@ -153,6 +156,9 @@ class OracleTurboAdam:
             st["amp"] = np.zeros(nb, np.uint16)
             st["alpha"] = np.zeros(1, np.float32)
             st["has_state"] = False
+            if grp["error_feedback"]:  # costate.py:409-437: the residual appears after the first update
+                st["ef_residual"] = np.zeros(n, np.float32)
+                st["has_ef"] = False
         else:
             st["exp_avg"] = np.zeros(n, np.float32)
         if not grp["compress_v"]:
@@ -212,6 +218,9 @@ class OracleTurboAdam:
                 t.norms = ptr(st["block_norms"])
                 t.amp = ptr(st["amp"])
                 t.alpha = ptr(st["alpha"])
+                if "ef_residual" in st:
+                    flags |= FLAG_EF | (FLAG_HAS_EF if st["has_ef"] else 0)
+                    t.ef_residual = ptr(st["ef_residual"])
                 t.k_lo, t.k_hi = ranks(nb, grp["null_pct"], grp["amp_pct"])
             else:
                 t.exp_avg = ptr(st["exp_avg"])
@@ -234,3 +243,5 @@ class OracleTurboAdam:
             L.or_step_tensor(ctypes.byref(t), self.seed)
             if st["_compress_m"]:
                 st["has_state"] = True
+                if "ef_residual" in st:
+                    st["has_ef"] = True

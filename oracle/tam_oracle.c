@@ -269,15 +269,21 @@ void or_encode(const float* delta, uint64_t n, float q, uint8_t* signs, float* n
 /* CoStateManager.update, reference costate.py:367-464 (no error feedback).
  * State arrays are updated in place; *alpha is alpha_{t-1} on entry and
  * alpha_t on exit.  m_out receives m_t. */
-void or_costate_update(const float* g, uint64_t n, float beta1, float one_minus_beta1, float q,
-                       uint64_t k_lo, uint64_t k_hi, int has_state, uint8_t* labels, uint8_t* signs,
-                       float* norms, uint16_t* amp, float* alpha, float* m_out) {
+/* With error feedback (ef, costate.py:409-437) the residual is added to g in
+ * the EMA (decompose keeps g); after encoding, ef_error = delta - decode(new
+ * encoding, alpha = 0) becomes the residual (has_ef == 0, its first step) or
+ * enters its EMA: r = fl(beta1*r) + fl((1-beta1)*ef_error). */
+void or_costate_update_ef(const float* g, uint64_t n, float beta1, float one_minus_beta1, float q,
+                          uint64_t k_lo, uint64_t k_hi, int has_state, uint8_t* labels, uint8_t* signs,
+                          float* norms, uint16_t* amp, float* alpha, int ef, int has_ef, float* ef_residual,
+                          float* m_out) {
   uint64_t nb = (n + OR_BS - 1) / OR_BS;
   float* m_hat = (float*)calloc(n, sizeof(float));
   if (has_state) or_decode_blocks(labels, signs, norms, amp, *alpha, g, n, q, m_hat);
   for (uint64_t i = 0; i < n; ++i) {
+    float gc = (ef && has_ef) ? g[i] + ef_residual[i] : g[i];  /* :410-413 */
     float a = beta1 * m_hat[i];
-    float b = one_minus_beta1 * g[i];
+    float b = one_minus_beta1 * gc;
     m_out[i] = a + b;                              /* :416 */
   }
   float* delta = (float*)malloc(n * sizeof(float));
@@ -289,9 +295,29 @@ void or_costate_update(const float* g, uint64_t n, float beta1, float one_minus_
   or_classify(ratios, nb, t0, t1, labels);
   or_encode(delta, n, q, signs, norms, amp);
   *alpha = al;
+  if (ef) {                                        /* :428-437 */
+    or_decode_blocks(labels, signs, norms, amp, 0.0f, g, n, q, m_hat);
+    for (uint64_t i = 0; i < n; ++i) {
+      float e = delta[i] - m_hat[i];
+      if (has_ef) {
+        float a = beta1 * ef_residual[i];
+        float b = one_minus_beta1 * e;
+        ef_residual[i] = a + b;
+      } else {
+        ef_residual[i] = e;
+      }
+    }
+  }
   free(m_hat);
   free(delta);
   free(ratios);
+}
+
+void or_costate_update(const float* g, uint64_t n, float beta1, float one_minus_beta1, float q,
+                       uint64_t k_lo, uint64_t k_hi, int has_state, uint8_t* labels, uint8_t* signs,
+                       float* norms, uint16_t* amp, float* alpha, float* m_out) {
+  or_costate_update_ef(g, n, beta1, one_minus_beta1, q, k_lo, k_hi, has_state, labels, signs, norms, amp, alpha,
+                       0, 0, NULL, m_out);
 }
 
 /* fused_v_update, reference quantize.py:222-299.  idx (N_pad) and scales
@@ -413,6 +439,7 @@ typedef struct OrTensor {
   float* norms;
   uint16_t* amp;
   float* alpha;
+  float* ef_residual; /* EF: f32[n] error-feedback residual (in/out) */
   uint64_t n;
   /* block0: first block of this tensor within the parameter it is a
    * block-aligned slice of (0 for a whole parameter); only the stochastic
@@ -426,6 +453,8 @@ typedef struct OrTensor {
 #define OR_FLAG_COMPRESS_V 2u
 #define OR_FLAG_HAS_STATE 4u
 #define OR_FLAG_WD 8u
+#define OR_FLAG_EF 16u
+#define OR_FLAG_HAS_EF 32u
 
 /* TurboAdam._full_step_kernel body for one parameter, reference
  * optimizer.py:97-170 (the caller increments the step counter and supplies
@@ -443,8 +472,9 @@ void or_step_tensor(OrTensor* t, uint64_t seed) {
   if (t->flags & OR_FLAG_WD)                        /* :106-107 */
     for (uint64_t i = 0; i < n; ++i) p[i] = round_p(p[i] * t->c_wd, (int)t->dtype);
   if (t->flags & OR_FLAG_COSTATE) {                 /* :110-111 */
-    or_costate_update(g, n, t->beta1, t->one_minus_beta1, t->sqrt_block, t->k_lo, t->k_hi,
-                      (t->flags & OR_FLAG_HAS_STATE) != 0, t->labels, t->signs, t->norms, t->amp, t->alpha, m);
+    or_costate_update_ef(g, n, t->beta1, t->one_minus_beta1, t->sqrt_block, t->k_lo, t->k_hi,
+                         (t->flags & OR_FLAG_HAS_STATE) != 0, t->labels, t->signs, t->norms, t->amp, t->alpha,
+                         (t->flags & OR_FLAG_EF) != 0, (t->flags & OR_FLAG_HAS_EF) != 0, t->ef_residual, m);
   } else {                                          /* :113-114 */
     for (uint64_t i = 0; i < n; ++i) {
       float a = t->exp_avg[i] * t->beta1;

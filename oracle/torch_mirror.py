@@ -149,13 +149,17 @@ def costate_decode(enc, alpha, g, n):
     return alpha * g + dh
 
 
-def costate_update(st, g, beta1, null_pct, amp_pct, ops, trace=None):
-    """CoStateManager.update without error feedback (costate.py:367-464); st is updated."""
+def costate_update(st, g, beta1, null_pct, amp_pct, ops, trace=None, ef=False):
+    """CoStateManager.update (costate.py:367-464); st is updated.  With error
+    feedback (ef, :409-437) the residual st["ef"] is added to g in the EMA
+    (decompose keeps g) and, after encoding, updated with the encoding loss
+    delta - decode(new encoding, alpha=0) (its EMA from the second step on)."""
     g = g.reshape(-1).float()
     n = g.numel()
     nb = (n + BS - 1) // BS
     m_hat = costate_decode(st, st["alpha"], g, n) if st["has_state"] else torch.zeros_like(g)
-    m = beta1 * m_hat + (1.0 - beta1) * g
+    g_corrected = g + st["ef"] if ef and st.get("ef") is not None else g
+    m = beta1 * m_hat + (1.0 - beta1) * g_corrected
     gg = ops.dot(g, g)
     mg = ops.dot(m, g)
     alpha = torch.where(gg > 0, mg / gg, gg.new_zeros(()))
@@ -179,6 +183,10 @@ def costate_update(st, g, beta1, null_pct, amp_pct, ops, trace=None):
     st["scales"] = (dn / math.sqrt(BS)).to(torch.float16)
     st["alpha"] = alpha.clone()
     st["has_state"] = True
+    if ef:
+        delta_hat = costate_decode(st, g.new_zeros(1), g, n)
+        ef_error = delta - delta_hat
+        st["ef"] = ef_error if st.get("ef") is None else beta1 * st["ef"] + (1.0 - beta1) * ef_error
     if trace is not None:
         trace.update(m=m, delta=delta, alpha=alpha, ratios=r, tau=(t0, t1), dn=dn, mn=mn)
     return m
@@ -274,7 +282,8 @@ class MirrorTurboAdam:
             if wd != 0.0:
                 p.mul_(1.0 - lr * wd)
             if st["_compress_m"]:
-                m = costate_update(st["cs"], g, b1, grp["null_pct"], grp["amp_pct"], ops, tr).reshape(p.shape)
+                m = costate_update(st["cs"], g, b1, grp["null_pct"], grp["amp_pct"], ops, tr,
+                                   ef=grp["error_feedback"]).reshape(p.shape)
             else:
                 st["exp_avg"].mul_(b1).add_(g.reshape(-1), alpha=1.0 - b1)
                 m = st["exp_avg"].reshape(p.shape)
@@ -307,6 +316,8 @@ class MirrorTurboAdam:
             out["block_norms"] = cs["block_norms"].numpy().copy()
             out["amp"] = cs["scales"].view(torch.int16).numpy().view(np.uint16).copy()
             out["alpha"] = cs["alpha"].reshape(1).float().numpy().copy()
+            if cs.get("ef") is not None:
+                out["ef_residual"] = cs["ef"].numpy().copy()
         if "exp_avg" in st:
             out["exp_avg"] = st["exp_avg"].numpy().copy()
         if "exp_avg_sq" in st:

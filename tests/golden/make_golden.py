@@ -55,6 +55,11 @@ CASES = {
                      keep_params=[25, 50, 100, 150, 200]),
     "gpt2_block": dict(sizes=[int(np.prod(s)) for s in GPT2_BLOCK], shapes=GPT2_BLOCK, dt=O.DT_F32, steps=3,
                        kw=dict(lr=6e-4, weight_decay=0.01), digests_only=True),
+    # CoState error feedback (costate.py:409-437): the residual EMA is part of the state
+    "ef_f32": dict(sizes=[5000, 4608, 300, 18509], dt=O.DT_F32, steps=8,
+                   kw=dict(lr=1e-3, weight_decay=0.01, error_feedback=True)),
+    "ef_bf16": dict(sizes=[8320, 4100], dt=O.DT_BF16, steps=6,
+                    kw=dict(lr=1e-3, weight_decay=0.1, error_feedback=True, null_pct=0.05, amp_pct=0.95)),
 }
 
 
@@ -115,6 +120,8 @@ def state_arrays(opt, p) -> dict:
         out["block_norms"] = np_of(enc["block_norms"])
         out["amp"] = np_of(enc["scales"])
         out["alpha"] = np_of(mgr._alpha.reshape(1).float())
+        if getattr(mgr, "_ef_residual", None) is not None:
+            out["ef_residual"] = np_of(mgr._ef_residual.float())
     if "exp_avg" in st:
         out["exp_avg"] = np_of(st["exp_avg"])
     if "exp_avg_sq" in st:

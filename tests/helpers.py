@@ -62,6 +62,8 @@ def gpu_state(opt, p) -> dict:
         out["amp"] = f16_bits(enc["scales"])
         out["alpha"] = from_torch(mgr._alpha.reshape(1))
         out["has_state"] = mgr._has_state
+        if getattr(mgr, "_ef_residual", None) is not None:
+            out["ef_residual"] = from_torch(mgr._ef_residual.float())
     else:
         out["exp_avg"] = from_torch(st["exp_avg"])
     if "exp_avg_sq" in st:
@@ -72,7 +74,8 @@ def gpu_state(opt, p) -> dict:
     return out
 
 
-STATE_KEYS = ["labels", "sign_packed", "block_norms", "amp", "alpha", "exp_avg", "exp_avg_sq", "indices", "scales"]
+STATE_KEYS = ["labels", "sign_packed", "block_norms", "amp", "alpha", "exp_avg", "exp_avg_sq", "indices", "scales",
+              "ef_residual"]
 
 
 def compare_states(gst: dict, ost: dict, where: str) -> list:

@@ -146,6 +146,38 @@ def test_costate_manager_update_steps(null_pct, amp_pct):
         assert _same(np.float32(mgr._alpha.item()), alpha[0]), f"step {s}: alpha"
 
 
+def test_costate_manager_update_error_feedback():
+    from turboadam_amd import costate as C
+
+    n = 70_001
+    log(f"CoStateManager.update with error feedback n={n}, 5 steps")
+    rng = np.random.default_rng(8)
+    nb = (n + 127) // 128
+    labels = np.zeros(nb, np.uint8)
+    signs = np.zeros((n + 7) // 8, np.uint8)
+    norms = np.zeros(nb, np.float32)
+    amp = np.zeros(nb, np.uint16)
+    alpha = np.zeros(1, np.float32)
+    res = np.zeros(n, np.float32)
+    mgr = C.CoStateManager(error_feedback=True)
+    k_lo, k_hi = O.ranks(nb, 0.10, 0.90)
+    for s in range(5):
+        g = (rng.standard_normal(n).astype(np.float32) * 1e-3).astype(np.float32)
+        m_o = np.empty(n, np.float32)
+        O.lib().or_costate_update_ef(O.ptr(g), n, O.f32(0.9), O.f32(1.0 - 0.9), SQRT128, k_lo, k_hi, int(s > 0),
+                                     O.ptr(labels), O.ptr(signs), O.ptr(norms), O.ptr(amp), O.ptr(alpha), 1,
+                                     int(s > 0), O.ptr(res), O.ptr(m_o))
+        m = mgr.update(_t(g), 0.9)
+        enc = mgr._encoded
+        assert _same(_np(m), m_o), f"step {s}: m"
+        assert _same(_np(enc["labels"]), labels), f"step {s}: labels"
+        assert _same(_np(enc["sign_packed"]), signs), f"step {s}: signs"
+        assert _same(_np(enc["block_norms"]), norms), f"step {s}: norms"
+        assert _same(_np(enc["scales"]), amp), f"step {s}: amp"
+        assert _same(np.float32(mgr._alpha.item()), alpha[0]), f"step {s}: alpha"
+        assert _same(_np(mgr._ef_residual), res), f"step {s}: residual"
+
+
 @pytest.mark.parametrize("bits,dt", [(4, torch.float32), (2, torch.bfloat16), (8, torch.float32), (6, torch.float16)])
 def test_fused_v_update_standalone(bits, dt):
     from turboadam_amd import quantize as Q

@@ -231,3 +231,22 @@ def test_sparse_heavy_tailed_gradients():
                 bad.append(f"{where}: param differs")
             bad += compare_states(gpu_state(opt, p), orc.state[i], where)
     _check(bad)
+
+
+@pytest.mark.parametrize("dt", [F32, BF16, F16])
+def test_error_feedback(dt):
+    # CoState error feedback (fifth pass): tensors with tail blocks and one small
+    # fp32-m tensor, residual compared bit for bit every step
+    log(f"error feedback dtype={dt}, 5 steps")
+    sizes = [5000, 4608 + 77, 300, 18509]
+    _check(run_side_by_side(sizes, [dt] * len(sizes), steps=5, error_feedback=True, lr=1e-3, weight_decay=0.01))
+
+
+def test_error_feedback_grad_none_unaligned_and_large():
+    # a tensor without a gradient in some steps, unaligned views (bounds-checked
+    # quarters), and a 2.1M-element tensor (many tiles, chunks and slices)
+    log("error feedback: grad=None steps, unaligned views, 2.1M elements")
+    _check(run_side_by_side([9000, 70_001], [BF16, F32], steps=4, error_feedback=True, offset=1,
+                            grad_none=lambda s, i: i == 1 and s == 1, lr=1e-3, null_pct=0.05, amp_pct=0.95))
+    _check(run_side_by_side([8192 * 128 * 2 + 777], [BF16], steps=3, error_feedback=True, lr=1e-3,
+                            weight_decay=0.1))

@@ -71,9 +71,15 @@ def test_gpu_matches_reference_fixtures(name):
     case, opt, params = _run(name)
     dt = case["dt"]
     frac_bad = []
+    # With error feedback a sign bit that flips at a tie (|delta| within the
+    # alpha difference) moves that element's residual by a whole block scale,
+    # which the following steps' m carry: the CPU restatement in exact mode
+    # (which the GPU equals bit for bit) ends 4.7e-5 from the reference on
+    # ef_f32 (tests/test_golden.py::test_error_feedback_end_to_end_ties).
+    tol = 1e-4 if case["kw"].get("error_feedback") else 1e-6
     for i, p in enumerate(params):
         pr = _rel(_as_f32(from_torch(p.data), dt), _as_f32(z[f"param_{i}"], dt))
-        assert pr <= 1e-6, f"{name} tensor {i}: param rel {pr:.3g}"
+        assert pr <= tol, f"{name} tensor {i}: param rel {pr:.3g}"
         st = gpu_state(opt, p)
         for k in ("indices",):
             if f"{k}_{i}" in z.files:

@@ -24,8 +24,10 @@ TAM_FLAG_COSTATE = 0x1
 TAM_FLAG_COMPRESS_V = 0x2
 TAM_FLAG_HAS_STATE = 0x4
 TAM_FLAG_WD = 0x8
+TAM_FLAG_EF = 0x10
+TAM_FLAG_HAS_EF = 0x20
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 
 class TamTensor(ctypes.Structure):
@@ -68,6 +70,8 @@ class TamTensor(ctypes.Structure):
         ("inv_bc2", ctypes.c_double),
         ("slice0", ctypes.c_uint32),
         ("c_lr", ctypes.c_float),
+        ("ef_residual", ctypes.c_void_p),
+        ("ef_off", ctypes.c_uint64),
     ]
 
 
@@ -87,6 +91,9 @@ class TamStepInfo(ctypes.Structure):
         ("off_chunks", ctypes.c_uint64),
         ("off_sel", ctypes.c_uint64),
         ("off_hist", ctypes.c_uint64),
+        ("n_ef", ctypes.c_uint32),
+        ("info_pad", ctypes.c_uint32),
+        ("off_ef_alpha", ctypes.c_uint64),
     ]
 
 

@@ -201,21 +201,36 @@ class CoStateManager:
         """One CoState step for gradient g (reference costate.py:367-464): decode
         the previous state (or zeros), m = beta1*m_hat + (1-beta1)*g, then
         decompose, ratios, thresholds, labels and encode into the persistent
-        buffers.  Returns m (fp32, shape of g)."""
+        buffers.  With error feedback (:409-437) the EMA takes g + residual and
+        the residual then takes the encoding loss delta - decode(new, alpha=0)
+        (its EMA after the first step), in fp32 elementwise ops in the
+        reference's order.  Returns m (fp32, shape of g)."""
         _require_gpu(g, "CoStateManager.update")
         _require_block_size(self.block_size)
-        if self._error_feedback:
-            raise NotImplementedError("turboadam_amd: CoState error feedback is not implemented")
         n = g.numel()
         if self._encoded is None or self._encoded["labels"].device != g.device:
             self.allocate(n, g.device)
-        m = _decode(self._encoded, self._alpha, g, n, self._has_state, True, beta1)
         g32 = _f32_flat(g)
+        if self._error_feedback and self._ef_residual is not None:
+            m_hat = (_decode(self._encoded, self._alpha, g, n, True, False) if self._has_state
+                     else torch.zeros(n, dtype=torch.float32, device=g.device))
+            g_corrected = g32 + self._ef_residual.reshape(-1).float()
+            m = beta1 * m_hat + (1.0 - beta1) * g_corrected
+        else:
+            m = _decode(self._encoded, self._alpha, g, n, self._has_state, True, beta1)
         alpha_new, delta = decompose(m, g32)
         ratios = compute_block_ratios(delta, m)
         tau0, tau1 = compute_thresholds(ratios, self._null_pct, self._amp_pct)
         labels = classify_blocks(ratios, tau0, tau1)
         enc = encode_blocks(delta, labels)
+        if self._error_feedback:
+            zero = torch.zeros(1, dtype=torch.float32, device=g.device)
+            ef_error = delta.reshape(-1) - _decode(enc, zero, g, n, True, False)
+            if self._ef_residual is None:
+                self._ef_residual = ef_error.reshape(g.shape)
+            else:
+                self._ef_residual = (beta1 * self._ef_residual.reshape(-1).float()
+                                     + (1.0 - beta1) * ef_error).reshape(g.shape)
         for k in ("labels", "sign_packed", "block_norms", "scales"):
             self._encoded[k].copy_(enc[k])
         if isinstance(self._alpha, torch.Tensor):

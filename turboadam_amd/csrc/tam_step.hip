@@ -350,6 +350,41 @@ struct TamCsIn {
   uint32_t label, amp, byte;
   float nrm;
 };
+// Error feedback: the new encoding of a tensor is staged in the workspace
+// (passes 2 and 3) until pass 4 has used the previous one.  Layout as
+// tam_ef_stage_bytes: norms f32[nb], amplitudes f16[nb], labels u8[nb], sign
+// bytes u8[ceil(n/8)].
+struct TamStage {
+  float* norms;
+  uint16_t* amp;
+  uint8_t* labels;
+  uint8_t* signs;
+};
+__device__ __forceinline__ TamStage tam_stage(const TamTensor& d, char* ws) {
+  char* b = ws + d.ef_off;
+  TamStage st;
+  st.norms = (float*)b;
+  st.amp = (uint16_t*)(b + 4ull * d.nb);
+  st.labels = (uint8_t*)(b + 6ull * d.nb);
+  st.signs = (uint8_t*)(b + 7ull * d.nb);
+  return st;
+}
+
+// The gradient of the EMA term of an error-feedback tensor: g + residual once
+// a residual exists (costate.py:410-413), else g.
+template <bool FULL>
+__device__ __forceinline__ void tam_ef_grad(const TamTensor& d, const TamWave& W, const float* g, float* ge) {
+  if (d.flags & TAM_FLAG_HAS_EF) {
+    float r[TAM_EPL];
+    tam_ld8_f32<FULL>(d.ef_residual, W.e0, W.nv, r);
+#pragma unroll
+    for (int i = 0; i < TAM_EPL; ++i) ge[i] = g[i] + r[i];
+  } else {
+#pragma unroll
+    for (int i = 0; i < TAM_EPL; ++i) ge[i] = g[i];
+  }
+}
+
 template <bool FULL>
 __device__ __forceinline__ TamCsIn tam_cs_load(const TamTensor& d, const TamWave& W) {
   TamCsIn c = {0u, 0u, 0u, 0.0f};
@@ -373,9 +408,11 @@ __device__ __forceinline__ float tam_div_sqrt_block(float x) {
   return (float)((double)x * (1.0 / (double)TAM_SQRT_BLOCK_F));
 }
 
+// ge is the gradient of the EMA term: g, or g + the error-feedback residual
+// (costate.py:410-416; the decode keeps g).
 template <bool FULL>
 __device__ __forceinline__ void tam_costate_m(const TamTensor& d, const TamWave& W, const TamCsIn& cs,
-                                              float alpha_prev, const float* g, float* m) {
+                                              float alpha_prev, const float* g, const float* ge, float* m) {
   const bool has = (d.flags & TAM_FLAG_HAS_STATE) != 0;  // uniform over the launch
   if (has) {
     float s = 0.0f;
@@ -390,11 +427,11 @@ __device__ __forceinline__ void tam_costate_m(const TamTensor& d, const TamWave&
       // (a norm or an fp16 amplitude), so the bit becomes the sign of s
       const float sd = tam_u2f((tam_f2u(s) & 0x7fffffffu) | ((byte << (24 + i)) & 0x80000000u));
       const float mh = alpha_prev * g[i] + sd;
-      m[i] = d.beta1 * mh + d.one_minus_beta1 * g[i];
+      m[i] = d.beta1 * mh + d.one_minus_beta1 * ge[i];
     }
   } else {
 #pragma unroll
-    for (int i = 0; i < TAM_EPL; ++i) m[i] = d.beta1 * 0.0f + d.one_minus_beta1 * g[i];
+    for (int i = 0; i < TAM_EPL; ++i) m[i] = d.beta1 * 0.0f + d.one_minus_beta1 * ge[i];
   }
 }
 
@@ -736,7 +773,7 @@ __device__ __forceinline__ bool tam_quarter_full(const TamTensor& d, uint32_t wq
 // Per quarter tile: loads, first moment (CoState or fp32), second moment (1Q or
 // fp32), update, store; for CoState tensors the fp64 partial sums of g.g and
 // m.g over the quarter's 4 blocks (pairwise: blocks, then pairs of blocks).
-template <uint32_t DT, bool FULL>
+template <uint32_t DT, bool FULL, bool EF = false>
 __device__ __forceinline__ void tam_k1_quarter(const TamTensor& d, uint32_t wq, uint32_t lane, float* lutw,
                                                const TamLdsTabs* tabs, uint32_t seed_lo, uint32_t seed_hi,
                                                double2* __restrict__ part) {
@@ -761,7 +798,13 @@ __device__ __forceinline__ void tam_k1_quarter(const TamTensor& d, uint32_t wq, 
 
   // ---- first moment ---------------------------------------------------
   if (costate) {
-    if (FULL || W.bvalid) tam_costate_m<FULL>(d, W, cs, alpha_prev, g, m);
+    if (EF) {  // error feedback: the EMA takes g + residual (costate.py:410-416)
+      float ge[TAM_EPL];
+      tam_ef_grad<FULL>(d, W, g, ge);
+      if (FULL || W.bvalid) tam_costate_m<FULL>(d, W, cs, alpha_prev, g, ge, m);
+    } else if (FULL || W.bvalid) {
+      tam_costate_m<FULL>(d, W, cs, alpha_prev, g, g, m);
+    }
     double gg[TAM_EPL], mg[TAM_EPL];
 #pragma unroll
     for (int i = 0; i < TAM_EPL; ++i) {
@@ -826,9 +869,9 @@ __device__ __forceinline__ void tam_k1_full_body(const TamTensor* __restrict__ T
   for (uint32_t tile = blockIdx.x; tile < total_tiles; tile += gridDim.x) {
     while (tile >= T[ti].tile0 + T[ti].ntiles) ++ti;
     const TamTensor& d = T[ti];
-    if (d.dtype != DT) continue;  // uniform over the workgroup
-    const uint32_t wq = (tile - d.tile0) * 4u + wave;  // quarter tile within the tensor
-    if (!tam_quarter_full(d, wq)) continue;           // left to tam_k1_tail
+    if (d.dtype != DT || (d.flags & TAM_FLAG_EF)) continue;  // uniform; EF: tam_k1_ef
+    const uint32_t wq = (tile - d.tile0) * 4u + wave;        // quarter tile within the tensor
+    if (!tam_quarter_full(d, wq)) continue;                 // left to tam_k1_tail
     tam_k1_quarter<DT, true>(d, wq, lane, lutw, &tabs, seed_lo, seed_hi, partials + (uint64_t)tile * 4u + wave);
   }
 }
@@ -848,6 +891,7 @@ TAM_K1_FULL_KERNEL(tam_k1_main_f32, TAM_DTYPE_F32, 4)
 // 16-byte aligned.  One workgroup per tensor; wave w takes every fourth quarter.
 __global__ __launch_bounds__(TAM_WG) void tam_k1_tail(const TamTensor* __restrict__ T, uint32_t seed_lo,
                                                       uint32_t seed_hi, double2* __restrict__ partials) {
+  if (T[blockIdx.x].flags & TAM_FLAG_EF) return;  // the whole workgroup: tam_k1_ef covers the tensor
   __shared__ float lut[TAM_WG / 64][4 * 64];
   __shared__ TamLdsTabs tabs;
   tam_lds_tabs_fill(&tabs);
@@ -867,6 +911,40 @@ __global__ __launch_bounds__(TAM_WG) void tam_k1_tail(const TamTensor* __restric
         break;
       default:
         tam_k1_quarter<TAM_DTYPE_F32, false>(d, wq, lane, lut[wave], &tabs, seed_lo, seed_hi, part);
+        break;
+    }
+  }
+}
+
+// Every quarter of the tensors with error feedback (full or not, any dtype):
+// persistent workgroups stride over the tiles as the main kernels do.
+__global__ __launch_bounds__(TAM_WG) void tam_k1_ef(const TamTensor* __restrict__ T, int nT, uint32_t total_tiles,
+                                                    uint32_t seed_lo, uint32_t seed_hi,
+                                                    double2* __restrict__ partials) {
+  __shared__ float lut[TAM_WG / 64][4 * 64];
+  __shared__ TamLdsTabs tabs;
+  tam_lds_tabs_fill(&tabs);
+  const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+  int ti = tam_find_tensor(T, nT, blockIdx.x);
+  for (uint32_t tile = blockIdx.x; tile < total_tiles; tile += gridDim.x) {
+    while (tile >= T[ti].tile0 + T[ti].ntiles) ++ti;
+    const TamTensor& d = T[ti];
+    if (!(d.flags & TAM_FLAG_EF)) continue;  // uniform over the workgroup
+    const uint32_t wq = (tile - d.tile0) * 4u + wave;
+    double2* part = partials + (uint64_t)tile * 4u + wave;
+    const bool full = tam_quarter_full(d, wq);
+    switch (d.dtype) {
+      case TAM_DTYPE_BF16:
+        if (full) tam_k1_quarter<TAM_DTYPE_BF16, true, true>(d, wq, lane, lut[wave], &tabs, seed_lo, seed_hi, part);
+        else tam_k1_quarter<TAM_DTYPE_BF16, false, true>(d, wq, lane, lut[wave], &tabs, seed_lo, seed_hi, part);
+        break;
+      case TAM_DTYPE_F16:
+        if (full) tam_k1_quarter<TAM_DTYPE_F16, true, true>(d, wq, lane, lut[wave], &tabs, seed_lo, seed_hi, part);
+        else tam_k1_quarter<TAM_DTYPE_F16, false, true>(d, wq, lane, lut[wave], &tabs, seed_lo, seed_hi, part);
+        break;
+      default:
+        if (full) tam_k1_quarter<TAM_DTYPE_F32, true, true>(d, wq, lane, lut[wave], &tabs, seed_lo, seed_hi, part);
+        else tam_k1_quarter<TAM_DTYPE_F32, false, true>(d, wq, lane, lut[wave], &tabs, seed_lo, seed_hi, part);
         break;
     }
   }
@@ -995,19 +1073,28 @@ __global__ __launch_bounds__(TAM_WG) void tam_k_alpha(const TamTensor* __restric
 // ---------------------------------------------------------------------------
 // Pass 2: CoState encode (costate.py:419-425, :213-258) and block ratios (:51-86)
 // ---------------------------------------------------------------------------
+// With error feedback the EMA takes g + residual and the encoding goes to the
+// tensor's staging area (pass 4 still needs the previous one).
 template <uint32_t DT, bool FULL>
 __device__ __forceinline__ void tam_k2_quarter(const TamTensor& d, uint32_t wq, uint32_t lane, float a,
-                                               float* __restrict__ ratios) {
+                                               float* __restrict__ ratios, char* __restrict__ ws) {
   const TamWave W = tam_wave(d, wq, lane, FULL);
+  const bool ef = (d.flags & TAM_FLAG_EF) != 0;  // uniform
   double dd[TAM_EPL], mm[TAM_EPL];
   uint32_t sbyte = 0;
   if (FULL || W.bvalid) {
-    float g[TAM_EPL], m[TAM_EPL];
+    float g[TAM_EPL], ge[TAM_EPL], m[TAM_EPL];
     tam_ld8<DT, FULL>(d.grad, W.e0, W.nv, g);
     const TamCsIn cs = tam_cs_load<FULL>(d, W);
     const float alpha_prev = (d.flags & TAM_FLAG_HAS_STATE) ? tam_g(d.alpha)[0] : 0.0f;
+    if (ef) {
+      tam_ef_grad<FULL>(d, W, g, ge);
+    } else {
+#pragma unroll
+      for (int i = 0; i < TAM_EPL; ++i) ge[i] = g[i];
+    }
     tam_compiler_fence();
-    tam_costate_m<FULL>(d, W, cs, alpha_prev, g, m);
+    tam_costate_m<FULL>(d, W, cs, alpha_prev, g, ge, m);
 #pragma unroll
     for (int i = 0; i < TAM_EPL; ++i) {
       const bool ok = FULL || (uint32_t)i < W.nv;
@@ -1031,10 +1118,19 @@ __device__ __forceinline__ void tam_k2_quarter(const TamTensor& d, uint32_t wq, 
   const float nm = odd ? nx : ny;
   const float qv = nd / (odd ? nm : d.sqrt_block);  // costate.py:248 / :81-84
   if (FULL || W.bvalid) {
-    if (FULL || W.nv > 0) tam_g(d.signs)[W.e0 >> 3] = (uint8_t)sbyte;
+    uint8_t* signs = d.signs;
+    float* norms = d.norms;
+    uint16_t* amp = d.amp;
+    if (ef) {
+      const TamStage st = tam_stage(d, ws);
+      signs = st.signs;
+      norms = st.norms;
+      amp = st.amp;
+    }
+    if (FULL || W.nv > 0) tam_g(signs)[W.e0 >> 3] = (uint8_t)sbyte;
     if (W.l16 == 12u) {
-      tam_g(d.norms)[W.b] = nd;
-      tam_g(d.amp)[W.b] = tam_f32_to_f16(qv);
+      tam_g(norms)[W.b] = nd;
+      tam_g(amp)[W.b] = tam_f32_to_f16(qv);
     } else if (W.l16 == 13u) {
       tam_g(ratios)[d.ratio_off + W.b] = nm == 0.0f ? 0.0f : qv;
     }
@@ -1044,7 +1140,7 @@ __device__ __forceinline__ void tam_k2_quarter(const TamTensor& d, uint32_t wq, 
 __global__ __launch_bounds__(TAM_WG) void tam_k2_encode(const TamTensor* __restrict__ T, int nT,
                                                         uint32_t total_tiles,
                                                         const float* __restrict__ alpha_new,
-                                                        float* __restrict__ ratios) {
+                                                        float* __restrict__ ratios, char* __restrict__ ws) {
   const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
   int ti = tam_find_tensor(T, nT, blockIdx.x);
   for (uint32_t tile = blockIdx.x; tile < total_tiles; tile += gridDim.x) {
@@ -1056,16 +1152,16 @@ __global__ __launch_bounds__(TAM_WG) void tam_k2_encode(const TamTensor* __restr
     const bool full = tam_quarter_full(d, wq);
     switch (d.dtype) {
       case TAM_DTYPE_BF16:
-        if (full) tam_k2_quarter<TAM_DTYPE_BF16, true>(d, wq, lane, a, ratios);
-        else tam_k2_quarter<TAM_DTYPE_BF16, false>(d, wq, lane, a, ratios);
+        if (full) tam_k2_quarter<TAM_DTYPE_BF16, true>(d, wq, lane, a, ratios, ws);
+        else tam_k2_quarter<TAM_DTYPE_BF16, false>(d, wq, lane, a, ratios, ws);
         break;
       case TAM_DTYPE_F16:
-        if (full) tam_k2_quarter<TAM_DTYPE_F16, true>(d, wq, lane, a, ratios);
-        else tam_k2_quarter<TAM_DTYPE_F16, false>(d, wq, lane, a, ratios);
+        if (full) tam_k2_quarter<TAM_DTYPE_F16, true>(d, wq, lane, a, ratios, ws);
+        else tam_k2_quarter<TAM_DTYPE_F16, false>(d, wq, lane, a, ratios, ws);
         break;
       default:
-        if (full) tam_k2_quarter<TAM_DTYPE_F32, true>(d, wq, lane, a, ratios);
-        else tam_k2_quarter<TAM_DTYPE_F32, false>(d, wq, lane, a, ratios);
+        if (full) tam_k2_quarter<TAM_DTYPE_F32, true>(d, wq, lane, a, ratios, ws);
+        else tam_k2_quarter<TAM_DTYPE_F32, false>(d, wq, lane, a, ratios, ws);
         break;
     }
   }
@@ -1332,7 +1428,8 @@ __global__ __launch_bounds__(TAM_SEL_WG) void tam_k_sel_pick(const TamTensor* __
 __global__ __launch_bounds__(TAM_WG) void tam_k_sel_labels(const TamTensor* __restrict__ T, int nT,
                                                            const float* __restrict__ alpha_new,
                                                            const float* __restrict__ ratios,
-                                                           const TamSel* __restrict__ sel) {
+                                                           const TamSel* __restrict__ sel, char* __restrict__ ws,
+                                                           float* __restrict__ alpha_old) {
   const int t = tam_slice_tensor(T, nT, blockIdx.x);
   const TamTensor& d = T[t];
   const float tau0 = tam_u2f(sel[t].prefix[0]);
@@ -1340,11 +1437,101 @@ __global__ __launch_bounds__(TAM_WG) void tam_k_sel_labels(const TamTensor* __re
   const uint32_t k0 = (blockIdx.x - d.slice0) * TAM_SLICE;
   const uint32_t k1 = k0 + TAM_SLICE < d.nb ? k0 + TAM_SLICE : d.nb;
   const float* r = ratios + d.ratio_off;
+  const bool ef = (d.flags & TAM_FLAG_EF) != 0;  // error feedback: labels to the staging area
+  uint8_t* labels = ef ? tam_stage(d, ws).labels : d.labels;
   for (uint32_t i = k0 + threadIdx.x; i < k1; i += TAM_WG) {
     const float x = tam_g(r)[i];
-    tam_g(d.labels)[i] = x >= tau1 ? (uint8_t)2 : (x >= tau0 ? (uint8_t)1 : (uint8_t)0);
+    tam_g(labels)[i] = x >= tau1 ? (uint8_t)2 : (x >= tau0 ? (uint8_t)1 : (uint8_t)0);
   }
-  if (blockIdx.x == d.slice0 && threadIdx.x == 0) tam_g(d.alpha)[0] = alpha_new[t];
+  if (blockIdx.x == d.slice0 && threadIdx.x == 0) {
+    if (ef) alpha_old[t] = tam_g(d.alpha)[0];  // pass 4 decodes the previous encoding
+    tam_g(d.alpha)[0] = alpha_new[t];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Pass 4 (tensors with error feedback): costate.py:409-437
+// ---------------------------------------------------------------------------
+// m is recomputed from the previous encoding exactly as in passes 0 and 2,
+// delta = m - alpha*g with the new alpha, and the encoding loss
+// ef_error = delta - decode(new encoding, alpha = 0) updates the residual:
+// r = ef_error on the tensor's first step, fl(beta1*r) + fl((1-beta1)*ef_error)
+// after.  The staged encoding then replaces the previous one.  Each quarter
+// reads and writes only its own blocks and sign bytes (the stores follow the
+// residual store, which needs every load).
+template <uint32_t DT, bool FULL>
+__device__ __forceinline__ void tam_k4_quarter(const TamTensor& d, uint32_t wq, uint32_t lane, float a_old,
+                                               float a_new, char* __restrict__ ws) {
+  const TamWave W = tam_wave(d, wq, lane, FULL);
+  if (!(FULL || W.bvalid)) return;  // no cross-lane work below
+  const bool has_ef = (d.flags & TAM_FLAG_HAS_EF) != 0;
+  const TamStage st = tam_stage(d, ws);
+  float g[TAM_EPL], ge[TAM_EPL], m[TAM_EPL], r[TAM_EPL];
+  tam_ld8<DT, FULL>(d.grad, W.e0, W.nv, g);
+  const TamCsIn cs = tam_cs_load<FULL>(d, W);
+  TamCsIn cn;  // the staged new encoding of the lane's block
+  cn.label = tam_g(st.labels)[W.b];
+  cn.nrm = tam_g(st.norms)[W.b];
+  cn.amp = tam_g(st.amp)[W.b];
+  cn.byte = (FULL || W.nv > 0) ? tam_g(st.signs)[W.e0 >> 3] : 0u;
+  if (has_ef) {
+    tam_ld8_f32<FULL>(d.ef_residual, W.e0, W.nv, r);
+  } else {
+#pragma unroll
+    for (int i = 0; i < TAM_EPL; ++i) r[i] = 0.0f;
+  }
+  tam_compiler_fence();
+#pragma unroll
+  for (int i = 0; i < TAM_EPL; ++i) ge[i] = has_ef ? g[i] + r[i] : g[i];
+  tam_costate_m<FULL>(d, W, cs, a_old, g, ge, m);
+  const float sph = tam_div_sqrt_block(cn.nrm);
+  const float s = cn.label == 1u ? sph : (cn.label == 2u ? tam_f16_to_f32((uint16_t)cn.amp) : 0.0f);
+  float rn[TAM_EPL];
+#pragma unroll
+  for (int i = 0; i < TAM_EPL; ++i) {
+    const float delta = m[i] - a_new * g[i];  // costate.py:42
+    const float sd = tam_u2f((tam_f2u(s) & 0x7fffffffu) | ((cn.byte << (24 + i)) & 0x80000000u));
+    const float dh = 0.0f * g[i] + sd;        // decode with alpha = 0 (costate.py:428-432)
+    const float e = delta - dh;
+    rn[i] = has_ef ? d.beta1 * r[i] + d.one_minus_beta1 * e : e;
+  }
+  tam_st8_f32<FULL>(d.ef_residual, W.e0, W.nv, rn);
+  tam_compiler_fence();
+  if (W.l16 == 0) {
+    tam_g(d.labels)[W.b] = (uint8_t)cn.label;
+    tam_g(d.norms)[W.b] = cn.nrm;
+    tam_g(d.amp)[W.b] = (uint16_t)cn.amp;
+  }
+  if (FULL || W.nv > 0) tam_g(d.signs)[W.e0 >> 3] = (uint8_t)cn.byte;
+}
+
+__global__ __launch_bounds__(TAM_WG) void tam_k4_ef(const TamTensor* __restrict__ T, int nT, uint32_t total_tiles,
+                                                    const float* __restrict__ alpha_new,
+                                                    const float* __restrict__ alpha_old, char* __restrict__ ws) {
+  const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+  int ti = tam_find_tensor(T, nT, blockIdx.x);
+  for (uint32_t tile = blockIdx.x; tile < total_tiles; tile += gridDim.x) {
+    while (tile >= T[ti].tile0 + T[ti].ntiles) ++ti;
+    const TamTensor& d = T[ti];
+    if (!(d.flags & TAM_FLAG_EF)) continue;  // uniform over the workgroup
+    const uint32_t wq = (tile - d.tile0) * 4u + wave;
+    const float ao = alpha_old[ti], an = alpha_new[ti];
+    const bool full = tam_quarter_full(d, wq);
+    switch (d.dtype) {
+      case TAM_DTYPE_BF16:
+        if (full) tam_k4_quarter<TAM_DTYPE_BF16, true>(d, wq, lane, ao, an, ws);
+        else tam_k4_quarter<TAM_DTYPE_BF16, false>(d, wq, lane, ao, an, ws);
+        break;
+      case TAM_DTYPE_F16:
+        if (full) tam_k4_quarter<TAM_DTYPE_F16, true>(d, wq, lane, ao, an, ws);
+        else tam_k4_quarter<TAM_DTYPE_F16, false>(d, wq, lane, ao, an, ws);
+        break;
+      default:
+        if (full) tam_k4_quarter<TAM_DTYPE_F32, true>(d, wq, lane, ao, an, ws);
+        else tam_k4_quarter<TAM_DTYPE_F32, false>(d, wq, lane, ao, an, ws);
+        break;
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1401,7 +1588,7 @@ __global__ __launch_bounds__(TAM_WG) void tam_k_decode(const uint8_t* __restrict
   const TamCsIn cs = tam_cs_load<false>(d, W);
   const float a = has_state ? alpha[0] : 0.0f;
   if (ema) {
-    tam_costate_m<false>(d, W, cs, a, gv, m);
+    tam_costate_m<false>(d, W, cs, a, gv, gv, m);
   } else {
     // m_hat alone: fl(alpha*g) + s_b*sign (costate.py:317-323)
     const float sph = tam_div_sqrt_block(cs.nrm);
@@ -1688,13 +1875,18 @@ static int tam_device_cus(void) {
 
 static uint64_t tam_align_up(uint64_t x, uint64_t a) { return (x + a - 1) / a * a; }
 
+// Bytes of an error-feedback tensor's staged encoding in the workspace:
+// norms f32[nb] at 0, amplitudes f16[nb] at 4nb, labels u8[nb] at 6nb, sign
+// bytes u8[ceil(n/8)] at 7nb.
+static uint64_t tam_ef_stage_bytes(uint64_t n, uint64_t nb) { return 7u * nb + (n + 7) / 8; }
+
 // Workgroups of a kernel that fit on the device at once (CUs times the
 // occupancy its registers and LDS allow), cached per device and kernel.  The
 // tile loops launch TAM_GRID_ROUNDS times that many workgroups: measured on
 // MI355X (Llama-shaped bf16 set), pass 1 and pass 2 run 20-25% faster with 32
 // rounds of ~30 tiles per workgroup than with one resident round of
 // persistent workgroups, and slow down again beyond 64 rounds.
-enum { TAM_KS_K1_BF16, TAM_KS_K1_F16, TAM_KS_K1_F32, TAM_KS_K2, TAM_KS_COUNT };
+enum { TAM_KS_K1_BF16, TAM_KS_K1_F16, TAM_KS_K1_F32, TAM_KS_K2, TAM_KS_K1_EF, TAM_KS_K4_EF, TAM_KS_COUNT };
 #ifndef TAM_GRID_ROUNDS
 #define TAM_GRID_ROUNDS 32
 #endif
@@ -1726,9 +1918,9 @@ const char* tam_last_error(void) { return tam_err_buf; }
 int tam_prepare(TamTensor* tensors, int n_tensors, TamStepInfo* info) {
   tam_err_buf[0] = 0;
   if (!info || n_tensors < 0 || (n_tensors > 0 && !tensors)) return tam_fail(TAM_E_INVALID, "%snull argument", "");
-  uint64_t tiles = 0, ratio_blocks = 0, chunks = 0, slices = 0;
+  uint64_t tiles = 0, ratio_blocks = 0, chunks = 0, slices = 0, ef_bytes = 0;
   uint32_t dtype_mask = 0;
-  uint32_t ncs = 0;
+  uint32_t ncs = 0, nef = 0;
   for (int i = 0; i < n_tensors; ++i) {
     TamTensor& t = tensors[i];
     if (t.n == 0) return tam_fail(TAM_E_INVALID, "%stensor %ld has no elements", "", i);
@@ -1756,8 +1948,17 @@ int tam_prepare(TamTensor* tensors, int n_tensors, TamStepInfo* info) {
       t.ratio_off = ratio_blocks;
       ratio_blocks += (nb + 3) & ~3ull;  // 16-byte aligned per tensor
       ++ncs;
+      if (t.flags & TAM_FLAG_EF) {
+        if (!t.ef_residual || ((uintptr_t)t.ef_residual & 15u))
+          return tam_fail(TAM_E_INVALID, "%stensor %ld: ef_residual null or misaligned", "", i);
+        t.ef_off = ef_bytes;  // relative until the workspace layout is known
+        ef_bytes += tam_align_up(tam_ef_stage_bytes(t.n, nb), 256);
+        ++nef;
+      }
     } else if (!t.exp_avg || ((uintptr_t)t.exp_avg & 15u)) {
       return tam_fail(TAM_E_INVALID, "%stensor %ld: exp_avg null or misaligned", "", i);
+    } else if (t.flags & (TAM_FLAG_EF | TAM_FLAG_HAS_EF)) {
+      return tam_fail(TAM_E_INVALID, "%stensor %ld: error feedback needs CoState", "", i);
     }
     t.nb = (uint32_t)nb;
     t.ntiles = (uint32_t)nt;
@@ -1792,6 +1993,12 @@ int tam_prepare(TamTensor* tensors, int n_tensors, TamStepInfo* info) {
   off = tam_align_up(off + (uint64_t)n_tensors * sizeof(TamSel), 256);
   info->off_hist = off;
   off = tam_align_up(off + (uint64_t)n_tensors * 4096u * sizeof(uint32_t), 256);
+  info->n_ef = nef;
+  info->off_ef_alpha = off;
+  off = tam_align_up(off + (uint64_t)n_tensors * sizeof(float), 256);
+  for (int i = 0; i < n_tensors; ++i)
+    if (tensors[i].flags & TAM_FLAG_EF) tensors[i].ef_off += off;
+  off += ef_bytes;
   info->ws_bytes = off;
   return TAM_OK;
 }
@@ -1799,11 +2006,12 @@ int tam_prepare(TamTensor* tensors, int n_tensors, TamStepInfo* info) {
 static int tam_launch_pass(int pass, const TamTensor* d_tensors, const TamStepInfo* info, uint64_t seed,
                            void* workspace, size_t ws_bytes, hipStream_t s) {
   if (!info || (info->n_tensors > 0 && !d_tensors)) return tam_fail(TAM_E_INVALID, "%snull argument", "");
-  if (pass < 0 || pass > 3) return tam_fail(TAM_E_INVALID, "%sunknown pass %ld", "", pass);
+  if (pass < 0 || pass > 4) return tam_fail(TAM_E_INVALID, "%sunknown pass %ld", "", pass);
   if (info->n_tensors == 0 || info->total_tiles == 0) return TAM_OK;
   if (!workspace || ws_bytes < info->ws_bytes)
     return tam_fail(TAM_E_WORKSPACE, "%sworkspace too small: need %ld bytes", "", (long)info->ws_bytes);
   if (pass > 0 && info->n_costate == 0) return TAM_OK;
+  if (pass == 4 && info->n_ef == 0) return TAM_OK;
   char* ws = (char*)workspace;
   double2* partials = (double2*)(ws + info->off_partials);
   float* alpha_new = (float*)(ws + info->off_alpha);
@@ -1811,6 +2019,7 @@ static int tam_launch_pass(int pass, const TamTensor* d_tensors, const TamStepIn
   double2* chunk_sums = (double2*)(ws + info->off_chunks);
   TamSel* sel = (TamSel*)(ws + info->off_sel);
   uint32_t* hist = (uint32_t*)(ws + info->off_hist);
+  float* alpha_old = (float*)(ws + info->off_ef_alpha);
   auto grid_of = [&](int which, const void* kernel) {
     const uint32_t g = tam_resident_grid(which, kernel) * TAM_GRID_ROUNDS;
     return info->total_tiles < g ? info->total_tiles : g;
@@ -1829,6 +2038,10 @@ static int tam_launch_pass(int pass, const TamTensor* d_tensors, const TamStepIn
         hipLaunchKernelGGL(tam_k1_main_f32, dim3(grid_of(TAM_KS_K1_F32, (const void*)tam_k1_main_f32)),
                            dim3(TAM_WG), 0, s, d_tensors, info->n_tensors, info->total_tiles, (uint32_t)seed,
                            (uint32_t)(seed >> 32), partials);
+      if (info->n_ef)
+        hipLaunchKernelGGL(tam_k1_ef, dim3(grid_of(TAM_KS_K1_EF, (const void*)tam_k1_ef)), dim3(TAM_WG), 0, s,
+                           d_tensors, info->n_tensors, info->total_tiles, (uint32_t)seed, (uint32_t)(seed >> 32),
+                           partials);
       TAM_HIP_CHECK(hipGetLastError());
       hipLaunchKernelGGL(tam_k1_tail, dim3(info->n_tensors), dim3(TAM_WG), 0, s, d_tensors, (uint32_t)seed,
                          (uint32_t)(seed >> 32), partials);
@@ -1841,7 +2054,7 @@ static int tam_launch_pass(int pass, const TamTensor* d_tensors, const TamStepIn
       break;
     case 2:
       hipLaunchKernelGGL(tam_k2_encode, dim3(grid_of(TAM_KS_K2, (const void*)tam_k2_encode)), dim3(TAM_WG), 0, s,
-                         d_tensors, info->n_tensors, info->total_tiles, alpha_new, ratios);
+                         d_tensors, info->n_tensors, info->total_tiles, alpha_new, ratios, ws);
       break;
     default:
       hipLaunchKernelGGL(tam_k_sel_reset, dim3(info->n_tensors), dim3(TAM_WG), 0, s, d_tensors, sel, hist);
@@ -1857,7 +2070,11 @@ static int tam_launch_pass(int pass, const TamTensor* d_tensors, const TamStepIn
         TAM_HIP_CHECK(hipGetLastError());
       }
       hipLaunchKernelGGL(tam_k_sel_labels, dim3(info->total_slices), dim3(TAM_WG), 0, s, d_tensors,
-                         info->n_tensors, alpha_new, ratios, sel);
+                         info->n_tensors, alpha_new, ratios, sel, ws, alpha_old);
+      break;
+    case 4:
+      hipLaunchKernelGGL(tam_k4_ef, dim3(grid_of(TAM_KS_K4_EF, (const void*)tam_k4_ef)), dim3(TAM_WG), 0, s, d_tensors,
+                         info->n_tensors, info->total_tiles, alpha_new, alpha_old, ws);
       break;
   }
   TAM_HIP_CHECK(hipGetLastError());
@@ -1874,7 +2091,7 @@ int tam_multi_tensor_step(const TamTensor* d_tensors, const TamTensor* h_tensors
                           uint64_t seed, void* workspace, size_t ws_bytes, void* stream) {
   tam_err_buf[0] = 0;
   (void)h_tensors;
-  for (int pass = 0; pass < 4; ++pass) {
+  for (int pass = 0; pass < 5; ++pass) {  // pass 4 runs only with error feedback
     const int rc = tam_launch_pass(pass, d_tensors, info, seed, workspace, ws_bytes, (hipStream_t)stream);
     if (rc != TAM_OK) return rc;
   }

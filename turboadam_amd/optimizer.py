@@ -269,7 +269,8 @@ class TurboAdam(Optimizer):
                     else:
                         mgr.allocate(p.numel(), device)
                     if mgr._ef_residual is not None:
-                        mgr._ef_residual = mgr._ef_residual.to(device=device)
+                        mgr._ef_residual = mgr._ef_residual.to(device=device, dtype=torch.float32).clone() \
+                            .contiguous().reshape(p.shape)
                 for key in ("exp_avg", "exp_avg_sq"):
                     if key in state:
                         state[key] = state[key].to(device=device, dtype=torch.float32).clone()
@@ -297,8 +298,6 @@ class TurboAdam(Optimizer):
     def _describe(self, p, state, group, group_idx, tid) -> _lib.TamTensor:
         if group["block_size"] != BLOCK_SIZE:
             raise NotImplementedError("turboadam_amd kernels use 128-element blocks (block_size=128)")
-        if group["error_feedback"] and state["_compress_m"]:
-            raise NotImplementedError("turboadam_amd: CoState error feedback is not implemented")
         g = p.grad
         if g.is_sparse:
             raise RuntimeError("turboadam_amd.TurboAdam does not support sparse gradients")
@@ -346,6 +345,15 @@ class TurboAdam(Optimizer):
             t.amp = enc["scales"].data_ptr()
             t.alpha = mgr._alpha.data_ptr()
             t.k_lo, t.k_hi = mgr.ranks(nb)
+            if mgr._error_feedback:
+                # costate.py:409-437: the residual exists from the tensor's first
+                # update on; that update writes it without reading it
+                flags |= _lib.TAM_FLAG_EF
+                if mgr._ef_residual is None:
+                    mgr._ef_residual = torch.zeros_like(p, dtype=torch.float32)
+                else:
+                    flags |= _lib.TAM_FLAG_HAS_EF
+                t.ef_residual = mgr._ef_residual.data_ptr()
         else:
             t.exp_avg = state["exp_avg"].data_ptr()
         if wd != 0.0:
@@ -392,7 +400,7 @@ class TurboAdam(Optimizer):
                                                ws.data_ptr(), ws.numel(), stream)
                 _lib.check(rc, "tam_multi_tensor_step")
             else:
-                for k in range(4):
+                for k in range(5 if info.n_ef else 4):
                     self._pass_hook(k, "begin")
                     rc = lib.tam_step_pass(k, desc.data_ptr(), ctypes.byref(info), self.philox_seed,
                                            ws.data_ptr(), ws.numel(), stream)
