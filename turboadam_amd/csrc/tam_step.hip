@@ -854,8 +854,8 @@ __device__ __forceinline__ void tam_k1_quarter(const TamTensor& d, uint32_t wq, 
 // Full quarters (inside the tensor, aligned arrays) of one parameter dtype:
 // persistent workgroups stride over the tiles; the four waves of a workgroup
 // take the four quarters of each tile and never synchronise with each other.
-// One kernel per dtype holds only that dtype's full-quarter code, so the
-// register budget admits five waves per SIMD for 16-bit parameters.
+// One kernel per dtype holds only that dtype's full-quarter code, so each
+// gets its own register budget (waves per SIMD below).
 template <uint32_t DT>
 __device__ __forceinline__ void tam_k1_full_body(const TamTensor* __restrict__ T, int nT, uint32_t total_tiles,
                                                  uint32_t seed_lo, uint32_t seed_hi,
@@ -882,9 +882,12 @@ __device__ __forceinline__ void tam_k1_full_body(const TamTensor* __restrict__ T
       double2* __restrict__ partials) {                                                                    \
     tam_k1_full_body<DT>(T, nT, total_tiles, seed_lo, seed_hi, partials);                                  \
   }
+// Waves per SIMD, measured best per dtype: bf16 5 (96 VGPRs), fp16 4 (its
+// fp16 conversions spill at 96 VGPRs; 11% faster unspilled), fp32 5 (4%
+// faster than 4 despite three spilled registers).
 TAM_K1_FULL_KERNEL(tam_k1_main_bf16, TAM_DTYPE_BF16, 5)
-TAM_K1_FULL_KERNEL(tam_k1_main_f16, TAM_DTYPE_F16, 5)
-TAM_K1_FULL_KERNEL(tam_k1_main_f32, TAM_DTYPE_F32, 4)
+TAM_K1_FULL_KERNEL(tam_k1_main_f16, TAM_DTYPE_F16, 4)
+TAM_K1_FULL_KERNEL(tam_k1_main_f32, TAM_DTYPE_F32, 5)
 
 // The quarters that are not full: the last (at most four) quarters of each
 // tensor, or every quarter of a tensor whose parameter or gradient is not
