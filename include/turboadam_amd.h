@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define TAM_ABI_VERSION 4
+#define TAM_ABI_VERSION 5
 #define TAM_BLOCK_SIZE 128 /* elements per quantisation / CoState block */
 
 /* error codes */
@@ -48,6 +48,8 @@ extern "C" {
 #define TAM_FLAG_WD 0x8u         /* apply decoupled weight decay p *= c_wd     */
 #define TAM_FLAG_EF 0x10u        /* COSTATE with error feedback (ef_residual)  */
 #define TAM_FLAG_HAS_EF 0x20u    /* EF: ef_residual holds a residual           */
+#define TAM_FLAG_DEVICE_STEP 0x40u /* step, bias corrections, HAS_STATE and     */
+                                 /* HAS_EF come from device counters (capture) */
 
 /* One parameter tensor of one optimizer step.  The caller fills the fields
  * marked [in]; tam_prepare() fills the fields marked [derived].  The array is
@@ -92,6 +94,18 @@ typedef struct TamTensor {
   float* ef_residual;   /* [in] EF: f32[n] error-feedback residual (in/out;  */
                         /*      written, not read, without HAS_EF)           */
   uint64_t ef_off;      /* [derived] EF: workspace offset of the staged encoding */
+  /* DEVICE_STEP (a step that can be captured in a graph and replayed): the
+   * first launch of the step fills step, bias_correction1/2, inv_bc2,
+   * inv_bc2_f32, c_lr and the HAS_STATE / HAS_EF flags of this descriptor in
+   * device memory from the counters below, then increments *step_dev.  The
+   * host values of those fields are ignored. */
+  uint32_t* step_dev;       /* [in] updates of this tensor so far (device)      */
+  const uint32_t* bc_step;  /* [in] counter whose next value indexes bc_table:   */
+                            /*      the group's last parameter with state       */
+                            /*      (reference optimizer.py:172-188)            */
+  const float* bc_table;    /* [in] f32 pairs (1-beta1^t, 1-beta2^t), t = 1..bc_len */
+  uint32_t bc_len;          /* [in] pairs in bc_table; later steps use the last */
+  uint32_t dev_pad;
 } TamTensor;
 
 /* Launch summary and workspace layout, filled by tam_prepare(). */
@@ -111,7 +125,7 @@ typedef struct TamStepInfo {
   uint64_t off_sel;
   uint64_t off_hist;
   uint32_t n_ef;           /* tensors with error feedback (a fifth pass runs) */
-  uint32_t info_pad;
+  uint32_t n_device_step;  /* DEVICE_STEP tensors (pass 0 starts with their prologue) */
   uint64_t off_ef_alpha;   /* EF: previous alpha of each tensor (f32 per tensor) */
 } TamStepInfo;
 
@@ -131,15 +145,17 @@ const char* tam_last_error(void);
 int tam_prepare(TamTensor* tensors, int n_tensors, TamStepInfo* info);
 
 /* One fused optimizer step over every tensor of `d_tensors` (device copy of
- * the array prepared by tam_prepare) in four launches: pass 1 (decode, EMA,
- * 1Q re-quantisation, AdamW update, dot partials), alpha, pass 2 (CoState
- * encode, block ratios), selection + classification.
- * Replaces TurboAdam._full_step_kernel (reference optimizer.py:88-170) with
- * CoStateManager.update (costate.py:367-464) and fused_v_update
- * (quantize.py:222-299 / triton_kernels.py:105-165) inlined.  `workspace`
- * must hold info->ws_bytes bytes of device memory (contents need not be kept
- * between calls).  `h_tensors` is the host array tam_prepare() filled; it is
- * read for launch sizes only. */
+ * the array prepared by tam_prepare) in four passes: the fused update
+ * (decode, EMA, 1Q re-quantisation, AdamW update, dot partials), alpha,
+ * CoState encode + block ratios, selection + classification; a fifth for
+ * error feedback.  Replaces TurboAdam._full_step_kernel (reference
+ * optimizer.py:88-170) with CoStateManager.update (costate.py:367-464) and
+ * fused_v_update (quantize.py:222-299 / triton_kernels.py:105-165) inlined.
+ * `workspace` must hold info->ws_bytes bytes of device memory (contents need
+ * not be kept between calls).  `h_tensors` is the host array tam_prepare()
+ * filled; it is not read.  DEVICE_STEP descriptors are completed in place in
+ * d_tensors.  No host synchronisation and no allocation: the call can be
+ * captured in a HIP graph (with DEVICE_STEP tensors, each replay is a step). */
 int tam_multi_tensor_step(const TamTensor* d_tensors, const TamTensor* h_tensors,
                           const TamStepInfo* info, uint64_t seed, void* workspace,
                           size_t ws_bytes, void* stream);

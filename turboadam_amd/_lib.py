@@ -26,8 +26,9 @@ TAM_FLAG_HAS_STATE = 0x4
 TAM_FLAG_WD = 0x8
 TAM_FLAG_EF = 0x10
 TAM_FLAG_HAS_EF = 0x20
+TAM_FLAG_DEVICE_STEP = 0x40
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 
 class TamTensor(ctypes.Structure):
@@ -72,6 +73,11 @@ class TamTensor(ctypes.Structure):
         ("c_lr", ctypes.c_float),
         ("ef_residual", ctypes.c_void_p),
         ("ef_off", ctypes.c_uint64),
+        ("step_dev", ctypes.c_void_p),
+        ("bc_step", ctypes.c_void_p),
+        ("bc_table", ctypes.c_void_p),
+        ("bc_len", ctypes.c_uint32),
+        ("dev_pad", ctypes.c_uint32),
     ]
 
 
@@ -92,7 +98,7 @@ class TamStepInfo(ctypes.Structure):
         ("off_sel", ctypes.c_uint64),
         ("off_hist", ctypes.c_uint64),
         ("n_ef", ctypes.c_uint32),
-        ("info_pad", ctypes.c_uint32),
+        ("n_device_step", ctypes.c_uint32),
         ("off_ef_alpha", ctypes.c_uint64),
     ]
 

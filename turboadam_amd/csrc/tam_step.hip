@@ -768,6 +768,44 @@ __device__ __forceinline__ bool tam_quarter_full(const TamTensor& d, uint32_t wq
 }
 
 // ---------------------------------------------------------------------------
+// Device-side step scalars (TAM_FLAG_DEVICE_STEP; a step captured in a graph)
+// ---------------------------------------------------------------------------
+// One workgroup.  First every DEVICE_STEP descriptor gets the fields the host
+// fills otherwise, from the counters as they stand before this step: the step
+// number (Philox counter word), the bias corrections of the group's step
+// (reference optimizer.py:172-188, from the host-built table), 1/bc2 in fp64
+// and fp32, -lr/bc1, and HAS_STATE / HAS_EF once the tensor has been updated;
+// after a barrier the counters advance.  The divisions are the correctly
+// rounded ones tam_prepare and the host perform.
+__global__ __launch_bounds__(1024) void tam_k_device_step(TamTensor* __restrict__ T, int nT) {
+  for (int i = threadIdx.x; i < nT; i += blockDim.x) {
+    TamTensor& d = T[i];
+    if (!(d.flags & TAM_FLAG_DEVICE_STEP)) continue;
+    const uint32_t own = *d.step_dev;
+    const uint32_t t = *d.bc_step + 1u;
+    const uint32_t k = (t < d.bc_len ? t : d.bc_len) - 1u;
+    const float bc1 = d.bc_table[2u * k], bc2 = d.bc_table[2u * k + 1u];
+    d.step = own + 1u;
+    d.bias_correction1 = bc1;
+    d.bias_correction2 = bc2;
+    d.inv_bc2 = 1.0 / (double)bc2;
+    d.inv_bc2_f32 = (float)d.inv_bc2;
+    d.c_lr = d.neg_lr / bc1;
+    uint32_t f = d.flags & ~(TAM_FLAG_HAS_STATE | TAM_FLAG_HAS_EF);
+    if (own > 0u) {
+      if (f & TAM_FLAG_COSTATE) f |= TAM_FLAG_HAS_STATE;
+      if (f & TAM_FLAG_EF) f |= TAM_FLAG_HAS_EF;
+    }
+    d.flags = f;
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < nT; i += blockDim.x) {
+    const TamTensor& d = T[i];
+    if (d.flags & TAM_FLAG_DEVICE_STEP) *d.step_dev = d.step;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Pass 0: the fused update
 // ---------------------------------------------------------------------------
 // Per quarter tile: loads, first moment (CoState or fp32), second moment (1Q or
@@ -1923,7 +1961,7 @@ int tam_prepare(TamTensor* tensors, int n_tensors, TamStepInfo* info) {
   if (!info || n_tensors < 0 || (n_tensors > 0 && !tensors)) return tam_fail(TAM_E_INVALID, "%snull argument", "");
   uint64_t tiles = 0, ratio_blocks = 0, chunks = 0, slices = 0, ef_bytes = 0;
   uint32_t dtype_mask = 0;
-  uint32_t ncs = 0, nef = 0;
+  uint32_t ncs = 0, nef = 0, ndev = 0;
   for (int i = 0; i < n_tensors; ++i) {
     TamTensor& t = tensors[i];
     if (t.n == 0) return tam_fail(TAM_E_INVALID, "%stensor %ld has no elements", "", i);
@@ -1931,6 +1969,11 @@ int tam_prepare(TamTensor* tensors, int n_tensors, TamStepInfo* info) {
     if (t.sqrt_block != TAM_SQRT_BLOCK_F)
       return tam_fail(TAM_E_INVALID, "%stensor %ld: sqrt_block must be f32(sqrt(128))", "", i);
     if (!t.param || !t.grad) return tam_fail(TAM_E_INVALID, "%stensor %ld: null param/grad", "", i);
+    if (t.flags & TAM_FLAG_DEVICE_STEP) {
+      if (!t.step_dev || !t.bc_step || !t.bc_table || t.bc_len == 0)
+        return tam_fail(TAM_E_INVALID, "%stensor %ld: device step counters or table missing", "", i);
+      ++ndev;
+    }
     const uint64_t nb = (t.n + TAM_BLOCK_SIZE - 1) / TAM_BLOCK_SIZE;
     if (nb > (1ull << 31)) return tam_fail(TAM_E_INVALID, "%stensor %ld too large", "", i);
     const uint64_t nt = (nb + TAM_BPT - 1) / TAM_BPT;
@@ -1997,6 +2040,7 @@ int tam_prepare(TamTensor* tensors, int n_tensors, TamStepInfo* info) {
   info->off_hist = off;
   off = tam_align_up(off + (uint64_t)n_tensors * 4096u * sizeof(uint32_t), 256);
   info->n_ef = nef;
+  info->n_device_step = ndev;
   info->off_ef_alpha = off;
   off = tam_align_up(off + (uint64_t)n_tensors * sizeof(float), 256);
   for (int i = 0; i < n_tensors; ++i)
@@ -2029,6 +2073,10 @@ static int tam_launch_pass(int pass, const TamTensor* d_tensors, const TamStepIn
   };
   switch (pass) {
     case 0:
+      if (info->n_device_step) {  // the descriptors of DEVICE_STEP tensors are completed on the device
+        hipLaunchKernelGGL(tam_k_device_step, dim3(1), dim3(1024), 0, s, (TamTensor*)d_tensors, info->n_tensors);
+        TAM_HIP_CHECK(hipGetLastError());
+      }
       if (info->dtype_mask & (1u << TAM_DTYPE_BF16))
         hipLaunchKernelGGL(tam_k1_main_bf16, dim3(grid_of(TAM_KS_K1_BF16, (const void*)tam_k1_main_bf16)),
                            dim3(TAM_WG), 0, s, d_tensors, info->n_tensors, info->total_tiles, (uint32_t)seed,

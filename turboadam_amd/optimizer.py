@@ -41,12 +41,31 @@ def _f32(x: float) -> float:
 
 
 class _DeviceBuffers:
-    """Per-device descriptor and workspace buffers, grown on demand."""
+    """Per-device descriptor and workspace buffers, grown on demand, and the
+    persistent pinned upload buffer of capturable steps."""
 
     def __init__(self, device):
         self.device = device
         self.desc = None
         self.ws = None
+        self.pinned = None
+        self.pinned_bytes = b""
+
+    def upload_static(self, raw: bytes) -> torch.Tensor:
+        """Pinned host copy of `raw` that a captured graph re-reads on every
+        replay.  It is rewritten only when the descriptors change; a pending
+        copy from it is waited for first (not possible during a capture)."""
+        if raw != self.pinned_bytes:
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError("turboadam_amd: capturable step changed its tensors during graph capture; "
+                                   "run an eager warm-up step with the same parameters and gradients first")
+            if self.pinned is not None:
+                torch.cuda.current_stream(self.device).synchronize()
+            if self.pinned is None or self.pinned.numel() < len(raw):
+                self.pinned = torch.empty(max(len(raw), 4096), dtype=torch.uint8, pin_memory=True)
+            ctypes.memmove(self.pinned.data_ptr(), raw, len(raw))
+            self.pinned_bytes = raw
+        return self.pinned[: len(raw)]
 
     def desc_buffer(self, nbytes: int) -> torch.Tensor:
         if self.desc is None or self.desc.numel() < nbytes:
@@ -93,8 +112,6 @@ class TurboAdam(Optimizer):
     ):
         if v_bits not in (2, 3, 4, 6, 8):
             raise ValueError(f"v_bits must be one of {{2, 3, 4, 6, 8}}, got {v_bits}")
-        if capturable:
-            raise NotImplementedError("CUDA graph capture is not yet supported. Set capturable=False.")
         defaults = dict(
             lr=lr,
             betas=betas,
@@ -108,6 +125,7 @@ class TurboAdam(Optimizer):
             amp_pct=amp_pct,
             error_feedback=error_feedback,
             min_m_compress_elements=min_m_compress_elements,
+            capturable=capturable,
         )
         super().__init__(params, defaults)
         self._group_step_tensors = {}
@@ -116,6 +134,7 @@ class TurboAdam(Optimizer):
         self.philox_seed = int(philox_seed)
         self._buffers = {}
         self._bc_values = {}
+        self._bc_tables = {}
         # Optional callable(pass_index, "begin"|"end") run around each of the four
         # launches (the step is then issued pass by pass); used to time kernels.
         self._pass_hook = None
@@ -131,7 +150,8 @@ class TurboAdam(Optimizer):
         if p.numel() == 0:
             raise RuntimeError("turboadam_amd.TurboAdam: cannot optimise a parameter with no elements")
         block_size = group["block_size"]
-        state["step"] = 0
+        # capturable: the step counter lives on the device and the step advances it
+        state["step"] = torch.zeros((), dtype=torch.int32, device=p.device) if group.get("capturable") else 0
         compress_this_m = group["compress_m"] and p.numel() >= group["min_m_compress_elements"]
         state["_compress_m"] = compress_this_m
         if compress_this_m:
@@ -173,6 +193,8 @@ class TurboAdam(Optimizer):
         """
         self._bc_values = {}
         for group_idx, group in enumerate(self.param_groups):
+            if group.get("capturable"):
+                continue  # computed on the device (tam_k_device_step)
             beta1, beta2 = group["betas"]
             for p in group["params"]:
                 if p not in self.state:
@@ -245,6 +267,11 @@ class TurboAdam(Optimizer):
                     continue
                 state = self.state[p]
                 device = p.device
+                step = state.get("step", 0)
+                if group.get("capturable"):  # torch's loader makes it f32 on the device
+                    state["step"] = torch.as_tensor(step).to(device=device, dtype=torch.int32).reshape(()).clone()
+                else:
+                    state["step"] = int(step.item()) if isinstance(step, torch.Tensor) else int(step)
                 cv = state.get("compressed_v")
                 if isinstance(cv, dict):
                     cv.pop("rand_buf", None)
@@ -290,7 +317,8 @@ class TurboAdam(Optimizer):
                 if p.grad is None:
                     continue
                 state = self.state[p]
-                state["step"] += 1
+                if not group.get("capturable"):
+                    state["step"] += 1  # capturable: the step's first launch counts it
                 per_device.setdefault(p.device, []).append((p, state, group, group_idx, tid))
         for device, items in per_device.items():
             self._launch(device, items)
@@ -360,8 +388,9 @@ class TurboAdam(Optimizer):
             flags |= _lib.TAM_FLAG_WD
         t.flags = flags
         t.tensor_id = tid & 0xFFFFFFFF
-        t.step = state["step"] & 0xFFFFFFFF
-        bc1, bc2 = self._bc_values[(group_idx, p.device.type, p.device.index)]
+        step = state["step"]
+        t.step = 0 if isinstance(step, torch.Tensor) else step & 0xFFFFFFFF  # capturable: filled on the device
+        bc1, bc2 = self._bc_values.get((group_idx, p.device.type, p.device.index), (1.0, 1.0))
         t.c_wd = _f32(1.0 - lr * wd)
         t.beta1 = _f32(beta1)
         t.one_minus_beta1 = _f32(1.0 - beta1)
@@ -374,7 +403,59 @@ class TurboAdam(Optimizer):
         t.eps = _f32(group["eps"])
         t.neg_lr = _f32(-lr)
         t.sqrt_block = _f32(math.sqrt(BLOCK_SIZE))
+        if group.get("capturable"):
+            self._describe_device_step(t, p, state, group)
         return t
+
+    # ------------------------------------------------------------------
+    # capturable steps (the step counter and bias corrections on the device)
+    # ------------------------------------------------------------------
+    _BC_MAX_STEPS = 1 << 22
+
+    def _bc_table(self, beta1: float, beta2: float, device):
+        """fp32 (1 - beta1^t, 1 - beta2^t) for t = 1.. until both are exactly 1
+        (they stay 1 after), computed as the reference does (Python floats,
+        optimizer.py:172-188), as a device tensor."""
+        key = (float(beta1), float(beta2), device)
+        if key not in self._bc_tables:
+            vals = []
+            t = 0
+            while True:
+                t += 1
+                b1, b2 = 1.0 - beta1**t, 1.0 - beta2**t
+                vals += [b1, b2]
+                if (_f32(b1) == 1.0 and _f32(b2) == 1.0) or t >= self._BC_MAX_STEPS:
+                    break
+            if _f32(vals[-2]) != 1.0 or _f32(vals[-1]) != 1.0:
+                raise NotImplementedError(f"turboadam_amd: capturable with betas {beta1, beta2} needs bias "
+                                          f"corrections beyond {self._BC_MAX_STEPS} steps")
+            table = torch.tensor(vals, dtype=torch.float64).to(torch.float32).to(device)
+            self._bc_tables[key] = (table, t)
+        return self._bc_tables[key]
+
+    def _describe_device_step(self, t, p, state, group):
+        """Fields of a capturable step: the kernels' first launch fills step,
+        the bias corrections and the HAS_* flags from device counters, so the
+        descriptor itself stays the same from step to step."""
+        step = state["step"]
+        if not (isinstance(step, torch.Tensor) and step.dtype == torch.int32 and step.device == p.device):
+            raise RuntimeError("turboadam_amd: a capturable parameter's state['step'] must be an int32 tensor "
+                               "on its device")
+        beta1, beta2 = group["betas"]
+        table, n = self._bc_table(beta1, beta2, p.device)
+        src = None  # the group's last parameter with state on this device (optimizer.py:172-188)
+        for q in group["params"]:
+            if q in self.state and q.device == p.device:
+                src = self.state[q]["step"]
+        t.flags = (t.flags & ~(_lib.TAM_FLAG_HAS_STATE | _lib.TAM_FLAG_HAS_EF)) | _lib.TAM_FLAG_DEVICE_STEP
+        t.step_dev = step.data_ptr()
+        t.bc_step = src.data_ptr()
+        t.bc_table = table.data_ptr()
+        t.bc_len = n
+        t.step = 0
+        t.bias_correction1 = t.bias_correction2 = 1.0
+        t.inv_bc2 = 1.0
+        t.inv_bc2_f32 = 1.0
 
     def _launch(self, device, items):
         lib = _lib.load()
@@ -388,8 +469,12 @@ class TurboAdam(Optimizer):
         if bufs is None:
             bufs = self._buffers[device] = _DeviceBuffers(device)
         nbytes = ctypes.sizeof(arr)
-        host = torch.empty(nbytes, dtype=torch.uint8, pin_memory=True)
-        ctypes.memmove(host.data_ptr(), ctypes.addressof(arr), nbytes)
+        if info.n_device_step:
+            # a captured graph replays this copy: the same pinned bytes every time
+            host = bufs.upload_static(bytes(arr))
+        else:
+            host = torch.empty(nbytes, dtype=torch.uint8, pin_memory=True)
+            ctypes.memmove(host.data_ptr(), ctypes.addressof(arr), nbytes)
         desc = bufs.desc_buffer(nbytes)
         ws = bufs.workspace(info.ws_bytes)
         with torch.cuda.device(device):
