@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define TAM_ABI_VERSION 5
+#define TAM_ABI_VERSION 6
 #define TAM_BLOCK_SIZE 128 /* elements per quantisation / CoState block */
 
 /* error codes */
@@ -96,7 +96,7 @@ typedef struct TamTensor {
   uint64_t ef_off;      /* [derived] EF: workspace offset of the staged encoding */
   /* DEVICE_STEP (a step that can be captured in a graph and replayed): the
    * first launch of the step fills step, bias_correction1/2, inv_bc2,
-   * inv_bc2_f32, c_lr and the HAS_STATE / HAS_EF flags of this descriptor in
+   * inv_bc2_f32, c_lr, k_abs and the HAS_STATE / HAS_EF flags of this descriptor in
    * device memory from the counters below, then increments *step_dev.  The
    * host values of those fields are ignored. */
   uint32_t* step_dev;       /* [in] updates of this tensor so far (device)      */
@@ -105,7 +105,8 @@ typedef struct TamTensor {
                             /*      (reference optimizer.py:172-188)            */
   const float* bc_table;    /* [in] f32 pairs (1-beta1^t, 1-beta2^t), t = 1..bc_len */
   uint32_t bc_len;          /* [in] pairs in bc_table; later steps use the last */
-  uint32_t dev_pad;
+  float k_abs;              /* [derived] f32(2^-147 / bias_correction1): absolute */
+                            /*      error term of the certified 16-bit update   */
 } TamTensor;
 
 /* Launch summary and workspace layout, filled by tam_prepare(). */

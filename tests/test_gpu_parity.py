@@ -250,3 +250,138 @@ def test_error_feedback_grad_none_unaligned_and_large():
                             grad_none=lambda s, i: i == 1 and s == 1, lr=1e-3, null_pct=0.05, amp_pct=0.95))
     _check(run_side_by_side([8192 * 128 * 2 + 777], [BF16], steps=3, error_feedback=True, lr=1e-3,
                             weight_decay=0.1))
+
+
+def _nan_mask(a: np.ndarray, kind: str) -> np.ndarray:
+    if a.dtype == np.float32:
+        return np.isnan(a)
+    if kind == "bf16":
+        return (a & 0x7FFF) > 0x7F80
+    if kind == "f16":
+        return (a & 0x7FFF) > 0x7C00
+    return np.zeros(a.shape, bool)
+
+
+def _same(a: np.ndarray, b: np.ndarray, kind: str) -> np.ndarray:
+    """Equal bit patterns, or NaN in both (NaN payloads are not part of parity)."""
+    av = a.view(np.uint32) if a.dtype == np.float32 else a
+    bv = b.view(np.uint32) if b.dtype == np.float32 else b
+    return (av == bv) | (_nan_mask(a, kind) & _nan_mask(b, kind))
+
+
+def _edge_run(dt, init, grads, **kw):
+    """Step the GPU optimizer and the oracle through `grads` (per step, per
+    tensor: fp32 arrays or None) from `init`; NaN-aware bit comparison."""
+    from turboadam_amd import TurboAdam
+    from tests.helpers import from_torch, gpu_state, to_bits, to_torch
+
+    dev = torch.device("cuda:0")
+    pkind = {BF16: "bf16", F16: "f16", F32: "f32"}[dt]
+    o_params = [to_bits(a, dt) for a in init]
+    g_params = [torch.nn.Parameter(to_torch(a.copy(), dt, (a.size,), dev)) for a in o_params]
+    opt = TurboAdam(g_params, philox_seed=99, **kw)
+    orc = O.OracleTurboAdam(o_params, dtypes=[dt] * len(init), seed=99, **kw)
+    bad = []
+    for s, gs in enumerate(grads):
+        gb = [None if g is None else to_bits(g, dt) for g in gs]
+        for p, g in zip(g_params, gb):
+            p.grad = None if g is None else to_torch(g, dt, (g.size,), dev)
+        opt.step()
+        orc.step(gb)
+        torch.cuda.synchronize()
+        for i, p in enumerate(g_params):
+            where = f"step {s + 1} tensor {i}"
+            ok = _same(from_torch(p.data), o_params[i], pkind)
+            if not ok.all():
+                j = int(np.flatnonzero(~ok)[0])
+                bad.append(f"{where}: param differs in {int((~ok).sum())} (first {j}: gpu {from_torch(p.data)[j]:#x} "
+                           f"oracle {o_params[i][j]:#x})")
+            if i not in orc.state:
+                continue
+            gst, ost = gpu_state(opt, p), orc.state[i]
+            for k, b in ost.items():
+                if k not in gst or not isinstance(b, np.ndarray) or k in ("has_ef",):
+                    continue
+                a = gst[k]
+                kind = "f16" if k in ("amp", "scales") else "raw"
+                if a.shape != b.shape or not _same(a, b, kind).all():
+                    bad.append(f"{where}: {k} differs")
+    return bad
+
+
+def _edge_grads(rng, sizes, steps, scale, edit=None):
+    out = []
+    for s in range(steps):
+        gs = [(rng.standard_normal(n) * scale).astype(np.float32) for n in sizes]
+        if edit is not None:
+            edit(s, gs)
+        out.append(gs)
+    return out
+
+
+@pytest.mark.parametrize("dt", [BF16, F16])
+def test_update_tiny_moments_zero_params(dt):
+    # fl(-lr*m) and c*m in or near the subnormal range while bc1 = 1 - 0.99^t is
+    # small, parameters exactly zero or tiny: the certificate's absolute terms
+    log(f"edge: tiny moments, zero params, dtype={dt}")
+    rng = np.random.default_rng(71)
+    sizes = [4096 + 77, 2048]
+    init = [np.zeros(sizes[0], np.float32), (rng.standard_normal(sizes[1]) * 1e-30).astype(np.float32)]
+    scale = 1e-34 if dt == BF16 else 3e-6
+    lr = 1e-3 if dt == BF16 else 1e-4
+    grads = _edge_grads(rng, sizes, 4, scale)
+    _check(_edge_run(dt, init, grads, lr=lr, betas=(0.99, 0.999)))
+
+
+def test_update_zero_blocks_nan_and_inf_gradients():
+    # a block of exact zeros at step 1 (v = 0: the q range fails), NaN of both
+    # signs and infinities in later steps (NaN blocks, NaN parameters)
+    log("edge: zero blocks, NaN / inf gradients, bf16")
+    rng = np.random.default_rng(72)
+    sizes = [4096 + 77, 5000]
+
+    def edit(s, gs):
+        if s == 0:
+            gs[0][128:256] = 0.0
+            gs[1][:512] = 0.0
+        if s >= 1:
+            gs[0][300] = np.nan
+            gs[0][301] = -np.float32(np.nan)
+            gs[0][700] = np.inf
+            gs[1][1000] = -np.inf
+    init = [(rng.standard_normal(n) * 0.02).astype(np.float32) for n in sizes]
+    grads = _edge_grads(rng, sizes, 3, 1e-3, edit)
+    _check(_edge_run(BF16, init, grads, lr=1e-3, weight_decay=0.1))
+
+
+@pytest.mark.parametrize("eps", [0.0, -1e-8])
+def test_update_eps_zero_and_negative(eps):
+    log(f"edge: eps={eps}, bf16")
+    rng = np.random.default_rng(73)
+    sizes = [4096 + 77, 3000]
+    init = [(rng.standard_normal(n) * 0.02).astype(np.float32) for n in sizes]
+    grads = _edge_grads(rng, sizes, 3, 1e-4)
+    _check(_edge_run(BF16, init, grads, lr=1e-3, eps=eps))
+
+
+@pytest.mark.parametrize("betas", [(0.9, 1.5), (0.9, -0.5)])
+def test_update_betas_outside_unit_interval(betas):
+    # the reference does not validate betas: v may be negative (clamped path)
+    log(f"edge: betas={betas}, bf16")
+    rng = np.random.default_rng(74)
+    sizes = [4096 + 77]
+    init = [(rng.standard_normal(n) * 0.02).astype(np.float32) for n in sizes]
+    grads = _edge_grads(rng, sizes, 3, 1e-3)
+    _check(_edge_run(BF16, init, grads, lr=1e-3, betas=betas))
+
+
+def test_update_near_overflow():
+    # parameters near the bf16 maximum and updates near fp32 overflow
+    log("edge: near-overflow parameters and updates, bf16")
+    rng = np.random.default_rng(75)
+    n = 4096 + 77
+    p = (rng.standard_normal(n) * 0.02).astype(np.float32)
+    p[::7] = np.float32(3.3e38)
+    p[3::7] = -np.float32(3.3e38)
+    grads = _edge_grads(rng, [n], 3, 1.0)
+    _check(_edge_run(BF16, [p], grads, lr=3e37))

@@ -220,6 +220,13 @@ __device__ __forceinline__ double tam_readlane_d(double v, int l) {
 __device__ __forceinline__ double tam_pair8(const double* x) {
   return ((x[0] + x[1]) + (x[2] + x[3])) + ((x[4] + x[5]) + (x[6] + x[7]));
 }
+// The same sum of the products a[i]*b[i] of fp32 values: each product is exact
+// in fp64, so the first level fl(a0*b0 + a1*b1) is one fma (zero signs
+// included, as fma and the sum follow the same rule for an exact zero).
+__device__ __forceinline__ double tam_pair8_dot(const double* a, const double* b) {
+  return (__builtin_fma(a[0], b[0], a[1] * b[1]) + __builtin_fma(a[2], b[2], a[3] * b[3])) +
+         (__builtin_fma(a[4], b[4], a[5] * b[5]) + __builtin_fma(a[6], b[6], a[7] * b[7]));
+}
 
 // Sum over the 16 lanes of a block with adjacent pairing.  After the two quad
 // steps every lane of a quad holds the same value, so the mirrors pair quad 0
@@ -493,11 +500,17 @@ __device__ __forceinline__ float tam_expf_lds(float x, const TamLdsTabs* t) {
   return tam_expf_with(x, [t](int j) { return t->exp[j]; });
 }
 
-// Block extremes of the clamped v: bit patterns of the minimum and maximum
-// (valid elements only) and whether any is NaN.
+// Block extremes of v (valid elements only).  When v >= +0 or NaN (0 <= beta2
+// <= 1): kmn / kmx are the bit patterns of the smallest and largest v before
+// the clamp, and nan_seen is 1 when a v is NaN.  Otherwise (v may be
+// negative): kmn / kmx are the extremes of the clamped v, and nan_seen has bit
+// 1 set (no bound on the unclamped v; the update takes its exact sequence).
 struct TamVExt {
   uint32_t kmn, kmx, nan_seen;
 };
+#define TAM_VEXT_NAN 1u
+#define TAM_VEXT_CLAMPED 2u
+#define TAM_BITS_1EM38 0x006ce3eeu  // f32(1e-38) (subnormal)
 
 // First half: decode, EMA, clamp, block extremes.  The parameter update runs
 // between the halves (it needs v, not the new indices), so that p, m and v are
@@ -544,28 +557,80 @@ __device__ __forceinline__ TamVExt tam_vpath_a(const TamTensor& d, const TamWave
 #pragma unroll
     for (int i = 0; i < TAM_EPL; ++i) vo[i] = tam_expf_lds(lmin0 + ((float)idx[i] + 0.5f) * inv_nbk * span0, tabs);
   }
-  // EMA (quantize.py:259-270) and the clamp of :275.  A clamped v is
-  // positive or NaN: the block extremes are taken on bit patterns (NaN
-  // patterns order above +inf and are handled by nan_seen).
-  uint32_t kmn = 0x7f800000u, kmx = 0u;
-  uint32_t nan_seen = 0;
+  // EMA (quantize.py:259-270) and the clamp of :275.
+  TamVExt x;
+  if (d.beta2 >= 0.0f && d.one_minus_beta2 >= 0.0f) {  // uniform
+    // v >= +0 or NaN.  The extremes are taken on the bit patterns of v shifted
+    // left by one: the sign bit drops out and a NaN of either sign orders
+    // above +inf.  The clamp commutes with min and max, so vpath_b clamps the
+    // extremes; vc = max(v, 1e-38) equals the clamp except for a NaN, whose
+    // block is re-quantised from its NaN extremes whatever vc holds.
+    uint32_t xmn = 0xffffffffu, xmx = 0u;
+#pragma unroll
+    for (int i = 0; i < TAM_EPL; ++i) {
+      const bool valid = FULL || (uint32_t)i < W.nv;
+      const float g2 = valid ? g[i] * g[i] : 0.0f;
+      v[i] = __builtin_fmaf(d.one_minus_beta2, g2, vo[i] * d.beta2);
+      vc[i] = __builtin_fmaxf(v[i], 1e-38f);
+      const uint32_t k2 = tam_f2u(v[i]) << 1;
+      if (valid && bvalid) {
+        xmn = __builtin_elementwise_min(xmn, k2);
+        xmx = __builtin_elementwise_max(xmx, k2);
+      }
+    }
+    x.kmn = tam_block_umin(xmn) >> 1;
+    x.kmx = tam_block_umax(xmx) >> 1;
+    x.nan_seen = x.kmx > 0x7f800000u ? TAM_VEXT_NAN : 0u;
+  } else {
+    // v may be negative: extremes of the clamped v, NaN tested per element
+    uint32_t kmn = 0x7f800000u, kmx = 0u;
+    uint32_t nan_seen = 0;
+#pragma unroll
+    for (int i = 0; i < TAM_EPL; ++i) {
+      const bool valid = FULL || (uint32_t)i < W.nv;
+      const float g2 = valid ? g[i] * g[i] : 0.0f;
+      v[i] = __builtin_fmaf(d.one_minus_beta2, g2, vo[i] * d.beta2);
+      vc[i] = v[i] < 1e-38f ? 1e-38f : v[i];
+      if (valid && bvalid) {
+        nan_seen |= tam_isnan(vc[i]) ? 1u : 0u;
+        kmn = __builtin_elementwise_min(kmn, tam_f2u(vc[i]));
+        kmx = __builtin_elementwise_max(kmx, tam_f2u(vc[i]));
+      }
+    }
+    x.kmn = tam_block_umin(kmn);
+    x.kmx = tam_block_umax(kmx);
+    x.nan_seen = (tam_block_or(nan_seen) ? TAM_VEXT_NAN : 0u) | TAM_VEXT_CLAMPED;
+  }
+  return x;
+}
+
+// Extremes of |v| over the lane's valid elements (an fp32 second moment): a
+// negative q gives a NaN in the fast update and fails its own test, so
+// magnitudes bound the range test.
+template <bool FULL>
+__device__ __forceinline__ TamVExt tam_lane_extremes(const float* v, uint32_t nv) {
+  uint32_t xmn = 0xffffffffu, xmx = 0u;
 #pragma unroll
   for (int i = 0; i < TAM_EPL; ++i) {
-    const bool valid = FULL || (uint32_t)i < W.nv;
-    const float g2 = valid ? g[i] * g[i] : 0.0f;
-    v[i] = __builtin_fmaf(d.one_minus_beta2, g2, vo[i] * d.beta2);
-    vc[i] = v[i] < 1e-38f ? 1e-38f : v[i];
-    if (valid && bvalid) {
-      nan_seen |= tam_isnan(vc[i]) ? 1u : 0u;
-      kmn = __builtin_elementwise_min(kmn, tam_f2u(vc[i]));
-      kmx = __builtin_elementwise_max(kmx, tam_f2u(vc[i]));
+    if (FULL || (uint32_t)i < nv) {
+      xmn = __builtin_elementwise_min(xmn, tam_f2u(v[i]) << 1);
+      xmx = __builtin_elementwise_max(xmx, tam_f2u(v[i]) << 1);
     }
   }
   TamVExt x;
-  x.kmn = tam_block_umin(kmn);
-  x.kmx = tam_block_umax(kmx);
-  x.nan_seen = tam_block_or(nan_seen);
+  x.kmn = xmn >> 1;
+  x.kmx = xmx >> 1;
+  x.nan_seen = x.kmx > 0x7f800000u ? TAM_VEXT_NAN : 0u;
   return x;
+}
+
+// Whether q = fl(v * f32(1/bc2)) is a positive normal for every v of the
+// block (the certified 16-bit update's input range): q is monotone in v, so
+// the block's smallest and largest v decide.  False when the extremes bound
+// only the clamped v or a v is NaN.
+__device__ __forceinline__ bool tam_q_in_range(const TamTensor& d, const TamVExt& x) {
+  return x.nan_seen == 0u && tam_u2f(x.kmn) * d.inv_bc2_f32 >= 0x1p-126f &&
+         tam_u2f(x.kmx) * d.inv_bc2_f32 <= 0x1.fffffep127f;
 }
 
 // Second half: logs of the extremes, scales, stochastic re-quantisation.
@@ -575,7 +640,10 @@ __device__ __forceinline__ void tam_vpath_b(const TamTensor& d, const TamWave& W
   const uint32_t nbk = 1u << d.v_bits;
   const float fnb = (float)nbk;
   const bool bvalid = FULL || W.bvalid;
-  const uint32_t kmn = x.kmn, kmx = x.kmx, nan_seen = x.nan_seen;
+  // extremes of the clamped v (quantize.py:275-280)
+  const uint32_t kmn = __builtin_elementwise_max(x.kmn, TAM_BITS_1EM38);
+  const uint32_t kmx = __builtin_elementwise_max(x.kmx, TAM_BITS_1EM38);
+  const bool nan_seen = (x.nan_seen & TAM_VEXT_NAN) != 0u;
   // correctly rounded logs of the extremes: even lanes log(vmin), odd lanes log(vmax)
   const float lx = tam_logf_lds(tam_u2f((W.l16 & 1u) ? kmx : kmn), tabs);
   const float ly = tam_dppf<TAM_DPP_XOR1>(lx);
@@ -601,33 +669,39 @@ __device__ __forceinline__ void tam_vpath_b(const TamTensor& d, const TamWave& W
   const TamU4 r1 = tam_philox_quad(quad0 + 1, d.tensor_id, d.step, seed_lo, seed_hi);
   const uint32_t rw[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
   // indices go straight into their bytes (v_cvt_pk_u8_f32 of an integral
-  // value in [0, 255]); acceptance per element as lane masks
+  // value in [0, 255]); partial blocks accept per element (lane masks)
   uint32_t ow[2] = {0u, 0u};
   bool okv[TAM_EPL];
   bool all_ok = true;
+  // Full blocks: every element lies in [vmin, vmax] (normal, no NaN checked
+  // once here), so |log2 v| <= L and, when B < 1/4, |c~| <= 2^bits + 1 (c lies
+  // in [0, 2^bits]); one bound B serves the block.  The fast path evaluates
+  // d = fl(c~ + 1/2 - u) (C + 1/2 rounded once: its error and the roundings of
+  // values up to 2^bits + 3/2 are inside the (2^bits + 2) 2^-21 and |C| 2^-21
+  // terms) and q = rndne(d), which is ceil(c - u) when d lies farther than B
+  // from every half-integer; t = d - q is exact.  A lane is accepted when
+  // max |t| < H = 1/2 - (B + 2^-22); otherwise its elements are tested one by
+  // one in the exact path below.
+  float Cp = 0.0f, H = -1.0f;
   if (FULL) {
-    // Every element of a full block lies in [vmin, vmax] (normal, no NaN
-    // checked once here), so |log2 v| <= L and, when B < 1/4, |c~| <= 2^bits + 1
-    // (c lies in [0, 2^bits]); one bound B serves the block.  Accept when
-    // |(q - 1/2) - d| < H = 1/2 - (B + 2^-22): then r = q - d lies in (B, 1 - B)
-    // (q - 1/2 - d is exact, or above 1/4 and within 2^-26 of its value).
     const float la = __builtin_amdgcn_logf(tam_u2f(kmn)), lb = __builtin_amdgcn_logf(tam_u2f(kmx));
     const float L = __builtin_fmaxf(__builtin_fabsf(la), __builtin_fabsf(lb)) * (1.0f + 0x1p-18f) + 0x1p-20f;
-    const float Bb = __builtin_fmaf(L, KB, __builtin_fmaf(fnb + 1.0f, 0x1p-21f, CB));
+    const float Bb = __builtin_fmaf(L, KB, __builtin_fmaf(fnb + 2.0f, 0x1p-21f, CB));
     const bool blk_ok = (tam_u2f(kmn) >= 0x1p-126f) && !nan_seen && (Bb < 0.25f);
-    const float H = blk_ok ? 0.5f - (Bb + 0x1p-22f) : -1.0f;
+    H = blk_ok ? 0.5f - (Bb + 0x1p-22f) : -1.0f;
+    Cp = C + 0.5f;
+    float tmax = 0.0f;
 #pragma unroll
     for (int i = 0; i < TAM_EPL; ++i) {
       const float l2 = __builtin_amdgcn_logf(vc[i]);
-      const float ct = __builtin_fmaf(l2, K, C);
+      const float ct = __builtin_fmaf(l2, K, Cp);
       const float dd = __builtin_fmaf(-(float)(rw[i] >> 8), 0x1p-24f, ct);  // fl(ct - u), u exact
-      const float q = __builtin_ceilf(dd);
-      const float t = (q - 0.5f) - dd;
-      okv[i] = __builtin_fabsf(t) < H;
-      all_ok &= okv[i];
-      // the exact path overwrites !ok
+      const float q = __builtin_rintf(dd);
+      tmax = __builtin_fmaxf(tmax, __builtin_fabsf(dd - q));
+      // the exact path overwrites rejected elements
       ow[i >> 2] = __builtin_amdgcn_cvt_pk_u8_f32(__builtin_amdgcn_fmed3f(q, 0.0f, fnb - 1.0f), i & 3, ow[i >> 2]);
     }
+    all_ok = tmax < H;  // false for a NaN bound (then H = -1)
   } else {
 #pragma unroll
     for (int i = 0; i < TAM_EPL; ++i) {
@@ -646,6 +720,11 @@ __device__ __forceinline__ void tam_vpath_b(const TamTensor& d, const TamWave& W
     // exact path: the reference's own sequence with correctly rounded log and division
 #pragma unroll
     for (int i = 0; i < TAM_EPL; ++i) {
+      if (FULL) {  // the element's own test, as in the lane's
+        const float dd = __builtin_fmaf(-(float)(rw[i] >> 8), 0x1p-24f,
+                                        __builtin_fmaf(__builtin_amdgcn_logf(vc[i]), K, Cp));
+        okv[i] = __builtin_fabsf(dd - __builtin_rintf(dd)) < H;
+      }
       if (!okv[i]) {
         const float l = tam_logf_lds(vc[i], tabs);
         const float c = ((l - lmn) / sp) * fnb;  // quantize.py:284-285
@@ -670,23 +749,35 @@ __device__ __forceinline__ void tam_vpath_b(const TamTensor& d, const TamWave& W
 // Exact sequence: q1 = fl(v/bc2), s = fl(sqrt(q1)), den = fl(s + eps),
 // t2 = fl(den*bc1), a = fl(-lr*m), upd = fl(a/t2), p = R_p(fl(p + upd)).
 // fp32 parameters: q1 comes from the fp64 reciprocal of bc2 when a rounding
-// test proves the fp32 rounding, else from the division.  bf16 / fp16
-// parameters: a fast sequence, u~ = fl(fl(c*m) * rcp(fl(s~ + eps))) with
-// c = fl(-lr/bc1) and s~ = fl(q * rsq(q)), q = fl(v * fl(1/bc2)), gives
-// |u~ - upd| <= 2^-19 |u~| + 2^-148 (the exact sequence's six roundings and
-// the fast sequence's seven are each 2^-24 relative, both hardware results
-// are within 2^-23 -- checked exhaustively on gfx950; 17 units of 2^-24 in
-// all, inside 2^-19).  With s~ = fl(p + u~),
-// fl(p + upd) lies within E = 2^-19 |u~| + 2^-22 |s~| + 2^-148 of s~, so
-// R_p(fl(p + upd)) is accepted when R_p(fl(s~ - E)) == R_p(fl(s~ + E)) (R_p and
-// fl are monotone); otherwise the exact sequence runs.  The result of a
-// 16-bit parameter is returned as its bit pattern in pb.
-// v_cmp_class_f32 masks: +normal; +-normal or +-zero
-#define TAM_CLASS_POS_NORMAL 0x100
-#define TAM_CLASS_NORMAL_OR_ZERO 0x168
+// test proves the fp32 rounding, else from the division.
+//
+// bf16 / fp16 parameters: a fast sequence u~ = fl(fl(c*m) * r) with
+// r = rcp(fl(s~ + eps)), s~ = fl(q * rsq(q)), q = fl(v * fl(1/bc2)),
+// c = fl(-lr/bc1).  In the model fl(x) = x(1 + d) + e (|d| <= 2^-24,
+// |e| <= 2^-150 and e != 0 only below 2^-126), with q a positive normal and
+// 0 <= eps < 2^124 (so 2^-63 <= den < 2^125 and r is a normal):
+//  * relative parts: the exact sequence's six roundings, the fast
+//    sequence's seven and the two hardware results (each within 2^-23 on
+//    normal inputs -- checked exhaustively on gfx950), 17 units of 2^-24,
+//    inside 2^-19;
+//  * absolute parts: e of fl(-lr*m) divided by t2 (at most
+//    2^-150 r/bc1 (1 + 2^-21)), e of c*m times r, and e of upd and u~, below
+//    k_abs r + 2^-149 with k_abs = fl(2^-147/bc1).
+// So |u~ - upd| <= 2^-19 |u~| + k_abs r + 2^-149, and when |u~| < 2^126 (upd
+// then finite), fl(p + upd) lies within
+//   E = 2^-19 |u~| + 2^-22 |s| + k_abs r + 2^-148
+// of s = fl(p + u~).  R_p and fl are monotone (overflow included), so
+// R_p(fl(p + upd)) is accepted when R_p(fl(s - E)) == R_p(fl(s + E)) and
+// |s| < 2^126 (which rejects a NaN: the hardware rounding is used only on
+// non-NaN values).  q_ok tells that every q of the block is a positive normal
+// (tam_q_in_range); |u~| < 2^126 is tested per lane.  A lane that fails
+// either, and an element that fails its own test, takes the exact sequence.
+// The result of a 16-bit parameter is returned as its bit pattern in pb.
+typedef float TamF2 __attribute__((ext_vector_type(2)));
+typedef __bf16 TamBf2 __attribute__((ext_vector_type(2)));
 template <uint32_t DT>
 __device__ __forceinline__ void tam_update(const TamTensor& d, float* p, const float* m, const float* v,
-                                           uint16_t* pb) {
+                                           uint16_t* pb, bool q_ok) {
   const bool wd = (d.flags & TAM_FLAG_WD) != 0;
   if (DT == TAM_DTYPE_F32) {
 #pragma unroll
@@ -703,7 +794,15 @@ __device__ __forceinline__ void tam_update(const TamTensor& d, float* p, const f
   }
   float pw[TAM_EPL];
   // weight decay rounds to the parameter dtype (p.mul_ on a 16-bit tensor)
-  if (wd) {
+  if (wd && DT == TAM_DTYPE_BF16) {
+#pragma unroll
+    for (int k = 0; k < TAM_EPL / 2; ++k) {  // two elements per conversion
+      const uint32_t r2 = __builtin_bit_cast(
+          uint32_t, __builtin_convertvector((TamF2){p[2 * k] * d.c_wd, p[2 * k + 1] * d.c_wd}, TamBf2));
+      pw[2 * k] = tam_u2f(r2 << 16);
+      pw[2 * k + 1] = tam_u2f(r2 & 0xffff0000u);
+    }
+  } else if (wd) {
 #pragma unroll
     for (int i = 0; i < TAM_EPL; ++i) pw[i] = tam_h2f<DT>(tam_round16_hw<DT>(p[i] * d.c_wd));
   } else {
@@ -712,38 +811,30 @@ __device__ __forceinline__ void tam_update(const TamTensor& d, float* p, const f
   }
   // c_lr = fl(-lr / bc1), from tam_prepare (one more rounding in the fast
   // sequence, inside the 2^-19 bound)
-  const float c_lr = d.c_lr;
-  // per-element acceptance as lane masks (no per-element VALU to combine them)
+  const float c_lr = d.c_lr, k_abs = d.k_abs;
+  // per-element acceptance as lane masks
   bool okv[TAM_EPL];
   bool all_ok = true;
+  float umax = 0.0f;
 #pragma unroll
   for (int i = 0; i < TAM_EPL; ++i) {
     const float q = v[i] * d.inv_bc2_f32;
     const float s = q * __builtin_amdgcn_rsqf(q);
-    const float den = s + d.eps;
-    const float cm = c_lr * m[i];
-    const float u = cm * __builtin_amdgcn_rcpf(den);
+    const float r = __builtin_amdgcn_rcpf(s + d.eps);
+    const float u = (c_lr * m[i]) * r;
     const float st = pw[i] + u;
-    const float E = __builtin_fmaf(__builtin_fabsf(u), 0x1p-19f, __builtin_fmaf(__builtin_fabsf(st), 0x1p-22f, 0x1p-148f));
-    // finite, normal hardware inputs and outputs (q a positive normal; then
-    // den < 2^125), and c*m exact zero or normal (its relative error bound);
-    // NaN fails every test
-    const bool ok0 = __builtin_amdgcn_classf(q, TAM_CLASS_POS_NORMAL) & (__builtin_fabsf(st) < 0x1p126f) &
-                     __builtin_amdgcn_classf(cm, TAM_CLASS_NORMAL_OR_ZERO);
-    okv[i] = tam_same16<DT>(st - E, st + E, &pb[i]) & ok0;
+    const float E = __builtin_fmaf(__builtin_fabsf(u), 0x1p-19f,
+                                   __builtin_fmaf(__builtin_fabsf(st), 0x1p-22f, __builtin_fmaf(r, k_abs, 0x1p-148f)));
+    umax = __builtin_fmaxf(umax, __builtin_fabsf(u));  // a NaN u makes st NaN
+    okv[i] = tam_same16<DT>(st - E, st + E, &pb[i]) & (__builtin_fabsf(st) < 0x1p126f);
     all_ok &= okv[i];
   }
-  // with q finite, s < 2^64, so den = s + eps < 2^125 when eps < 2^124
-  // (a uniform condition: otherwise every element takes the exact sequence)
-  if (!(d.eps < 0x1p124f)) {
-#pragma unroll
-    for (int i = 0; i < TAM_EPL; ++i) okv[i] = false;
-    all_ok = false;
-  }
-  if (!all_ok) {
+  // eps is uniform: 0 <= eps < 2^124 (no cancellation in s + eps; den < 2^125)
+  const bool lane_ok = q_ok && umax < 0x1p126f && d.eps >= 0.0f && d.eps < 0x1p124f;
+  if (!(lane_ok && all_ok)) {
 #pragma unroll
     for (int i = 0; i < TAM_EPL; ++i) {
-      if (!okv[i]) {
+      if (!(lane_ok && okv[i])) {
         const float den = __builtin_sqrtf(v[i] / d.bias_correction2) + d.eps;
         pb[i] = tam_round16(pw[i] + (d.neg_lr * m[i]) / (den * d.bias_correction1), DT);
       }
@@ -791,6 +882,7 @@ __global__ __launch_bounds__(1024) void tam_k_device_step(TamTensor* __restrict_
     d.inv_bc2 = 1.0 / (double)bc2;
     d.inv_bc2_f32 = (float)d.inv_bc2;
     d.c_lr = d.neg_lr / bc1;
+    d.k_abs = 0x1p-147f / bc1;
     uint32_t f = d.flags & ~(TAM_FLAG_HAS_STATE | TAM_FLAG_HAS_EF);
     if (own > 0u) {
       if (f & TAM_FLAG_COSTATE) f |= TAM_FLAG_HAS_STATE;
@@ -843,16 +935,16 @@ __device__ __forceinline__ void tam_k1_quarter(const TamTensor& d, uint32_t wq, 
     } else if (FULL || W.bvalid) {
       tam_costate_m<FULL>(d, W, cs, alpha_prev, g, g, m);
     }
-    double gg[TAM_EPL], mg[TAM_EPL];
+    double gd[TAM_EPL], md[TAM_EPL];
 #pragma unroll
     for (int i = 0; i < TAM_EPL; ++i) {
       const bool ok = FULL || (W.bvalid && (uint32_t)i < W.nv);
-      gg[i] = ok ? (double)g[i] * (double)g[i] : 0.0;
-      mg[i] = ok ? (double)m[i] * (double)g[i] : 0.0;
+      gd[i] = ok ? (double)g[i] : 0.0;
+      md[i] = ok ? (double)m[i] : 0.0;
     }
     // per block, then the wave's 4 blocks (block k in lanes 16k..16k+15):
     // adjacent pairs, then the two pairs; lane 12 stores g.g, lane 13 m.g
-    const double t = tam_quarter_sum2(tam_pair8(gg), tam_pair8(mg), lane);
+    const double t = tam_quarter_sum2(tam_pair8_dot(gd, gd), tam_pair8_dot(md, gd), lane);
     if (lane - 12u < 2u) tam_g((double*)part)[lane - 12u] = t;
   } else if (FULL || W.bvalid) {
     // fp32 exp_avg (optimizer.py:113): m = fma(1-b1, g, fl(m*b1))
@@ -880,7 +972,9 @@ __device__ __forceinline__ void tam_k1_quarter(const TamTensor& d, uint32_t wq, 
   // ---- parameter update -----------------------------------------------
   if (FULL || W.bvalid) {
     uint16_t pb[TAM_EPL];
-    tam_update<DT>(d, p, m, v, pb);
+    bool q_ok = false;
+    if (DT != TAM_DTYPE_F32) q_ok = tam_q_in_range(d, compress_v ? vx : tam_lane_extremes<FULL>(v, W.nv));
+    tam_update<DT>(d, p, m, v, pb, q_ok);
     if (DT == TAM_DTYPE_F32) tam_st8_f32<FULL>((float*)d.param, W.e0, W.nv, p);
     else tam_st8_bits<FULL>(d.param, W.e0, W.nv, pb);
   }
@@ -1121,7 +1215,7 @@ __device__ __forceinline__ void tam_k2_quarter(const TamTensor& d, uint32_t wq, 
                                                float* __restrict__ ratios, char* __restrict__ ws) {
   const TamWave W = tam_wave(d, wq, lane, FULL);
   const bool ef = (d.flags & TAM_FLAG_EF) != 0;  // uniform
-  double dd[TAM_EPL], mm[TAM_EPL];
+  double dl[TAM_EPL], md[TAM_EPL];
   uint32_t sbyte = 0;
   if (FULL || W.bvalid) {
     float g[TAM_EPL], ge[TAM_EPL], m[TAM_EPL];
@@ -1140,20 +1234,20 @@ __device__ __forceinline__ void tam_k2_quarter(const TamTensor& d, uint32_t wq, 
     for (int i = 0; i < TAM_EPL; ++i) {
       const bool ok = FULL || (uint32_t)i < W.nv;
       const float delta = ok ? m[i] - a * g[i] : 0.0f;  // costate.py:42
-      dd[i] = (double)delta * (double)delta;
-      mm[i] = ok ? (double)m[i] * (double)m[i] : 0.0;
+      dl[i] = (double)delta;
+      md[i] = ok ? (double)m[i] : 0.0;
       sbyte = 2u * sbyte + (delta < 0.0f ? 1u : 0u);  // element 8j+i is bit 7-i, costate.py:170-181
     }
   } else {
 #pragma unroll
-    for (int i = 0; i < TAM_EPL; ++i) dd[i] = mm[i] = 0.0;
+    for (int i = 0; i < TAM_EPL; ++i) dl[i] = md[i] = 0.0;
   }
-  // Block sums with the tree of tam_block_sum: the sum of dd in lane 12 of the
-  // block's row, of mm in lane 13.  Each lane of a pair evaluates one square
+  // Block sums of squares with the tree of tam_block_sum: the sum of delta^2 in
+  // lane 12 of the block's row, of m^2 in lane 13.  Each lane of a pair evaluates one square
   // root and one division: lane 12 the residual norm and the amplitude, lane 13
   // the norm of m and the ratio.
   const bool odd = (W.l16 & 1u) != 0;
-  const float nx = (float)__builtin_sqrt(tam_row_sum2(tam_pair8(dd), tam_pair8(mm), odd));
+  const float nx = (float)__builtin_sqrt(tam_row_sum2(tam_pair8_dot(dl, dl), tam_pair8_dot(md, md), odd));
   const float ny = tam_dppf<TAM_DPP_XOR1>(nx);
   const float nd = odd ? ny : nx;  // costate.py:241
   const float nm = odd ? nx : ny;
@@ -2013,6 +2107,7 @@ int tam_prepare(TamTensor* tensors, int n_tensors, TamStepInfo* info) {
     t.chunk0 = (uint32_t)chunks;
     t.slice0 = (uint32_t)slices;
     t.c_lr = t.neg_lr / t.bias_correction1;  // fp32 division, correctly rounded
+    t.k_abs = 0x1p-147f / t.bias_correction1;
     tiles += nt;
     chunks += tam_alpha_chunks(t.flags, t.ntiles);
     slices += tam_sel_slices(t.flags, t.nb);
