@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define TAM_ABI_VERSION 6
+#define TAM_ABI_VERSION 7
 #define TAM_BLOCK_SIZE 128 /* elements per quantisation / CoState block */
 
 /* error codes */
@@ -50,6 +50,8 @@ extern "C" {
 #define TAM_FLAG_HAS_EF 0x20u    /* EF: ef_residual holds a residual           */
 #define TAM_FLAG_DEVICE_STEP 0x40u /* step, bias corrections, HAS_STATE and     */
                                  /* HAS_EF come from device counters (capture) */
+#define TAM_FLAG_SKIP 0x80u      /* [derived, device] DEVICE_STEP: *found_inf was */
+                                 /* nonzero; every launch of the step returns   */
 
 /* One parameter tensor of one optimizer step.  The caller fills the fields
  * marked [in]; tam_prepare() fills the fields marked [derived].  The array is
@@ -107,6 +109,11 @@ typedef struct TamTensor {
   uint32_t bc_len;          /* [in] pairs in bc_table; later steps use the last */
   float k_abs;              /* [derived] f32(2^-147 / bias_correction1): absolute */
                             /*      error term of the certified 16-bit update   */
+  const float* found_inf;   /* [in] DEVICE_STEP, or NULL: the step leaves every */
+                            /*      tensor and counter unchanged when           */
+                            /*      *found_inf != 0 (a GradScaler skip).  Given */
+                            /*      for one descriptor, given for all (the same */
+                            /*      pointer): the launches test descriptor 0.   */
 } TamTensor;
 
 /* Launch summary and workspace layout, filled by tam_prepare(). */

@@ -35,7 +35,7 @@ def test_library_exports_every_declared_symbol():
 def test_load_checks_abi_and_struct_layout():
     lib = _lib.load()
     assert lib.tam_abi_version() == _lib.ABI_VERSION
-    assert lib.tam_struct_size(0) == ctypes.sizeof(_lib.TamTensor) == 256
+    assert lib.tam_struct_size(0) == ctypes.sizeof(_lib.TamTensor) == 264
     assert lib.tam_struct_size(1) == ctypes.sizeof(_lib.TamStepInfo)
 
 
@@ -90,12 +90,34 @@ def test_prepare_layout():
     (lambda t: setattr(t, "v_idx", 0x30001), "misaligned"),
     (lambda t: setattr(t, "k_hi", 10_000), "rank"),
     (lambda t: setattr(t, "sqrt_block", 11.0), "sqrt_block"),
+    (lambda t: setattr(t, "found_inf", 0x4000), "found_inf"),  # a skip flag needs DEVICE_STEP
 ])
 def test_prepare_rejects_bad_input(mutate, msg):
     t = _tensor(5000)
     mutate(t)
     rc, _, _, err = _prepare([t])
     assert rc == 1 and msg in err
+
+
+def test_prepare_requires_one_found_inf_for_all_tensors():
+    # the launches test descriptor 0's skip flag for the whole step
+    ts = [_tensor(5000), _tensor(300)]
+    for t in ts:
+        t.flags |= _lib.TAM_FLAG_DEVICE_STEP
+        t.step_dev = t.bc_step = t.bc_table = 0x4000
+        t.bc_len = 1
+    ts[0].found_inf = 0x5000
+    rc, _, _, err = _prepare(ts)
+    assert rc == 1 and "found_inf" in err
+    ts[1].found_inf = 0x5000
+    rc, arr, _, _ = _prepare(ts)
+    assert rc == 0 and arr[0].flags & 0x80 == 0  # TAM_FLAG_SKIP is set on the device only
+
+
+def test_optimizer_declares_amp_scaling_support():
+    from turboadam_amd import TurboAdam
+
+    assert TurboAdam._step_supports_amp_scaling is True
 
 
 def test_step_rejects_small_workspace_without_launching():

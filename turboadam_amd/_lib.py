@@ -28,7 +28,7 @@ TAM_FLAG_EF = 0x10
 TAM_FLAG_HAS_EF = 0x20
 TAM_FLAG_DEVICE_STEP = 0x40
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 
 class TamTensor(ctypes.Structure):
@@ -78,6 +78,7 @@ class TamTensor(ctypes.Structure):
         ("bc_table", ctypes.c_void_p),
         ("bc_len", ctypes.c_uint32),
         ("k_abs", ctypes.c_float),
+        ("found_inf", ctypes.c_void_p),
     ]
 
 

@@ -867,11 +867,14 @@ __device__ __forceinline__ bool tam_quarter_full(const TamTensor& d, uint32_t wq
 // (reference optimizer.py:172-188, from the host-built table), 1/bc2 in fp64
 // and fp32, -lr/bc1, and HAS_STATE / HAS_EF once the tensor has been updated;
 // after a barrier the counters advance.  The divisions are the correctly
-// rounded ones tam_prepare and the host perform.
+// rounded ones tam_prepare and the host perform.  When *found_inf is nonzero
+// (a GradScaler skip) the descriptors get TAM_FLAG_SKIP instead, every later
+// launch of the step returns at once, and the counters stay.
 __global__ __launch_bounds__(1024) void tam_k_device_step(TamTensor* __restrict__ T, int nT) {
   for (int i = threadIdx.x; i < nT; i += blockDim.x) {
     TamTensor& d = T[i];
     if (!(d.flags & TAM_FLAG_DEVICE_STEP)) continue;
+    const bool skip = d.found_inf != nullptr && *d.found_inf != 0.0f;
     const uint32_t own = *d.step_dev;
     const uint32_t t = *d.bc_step + 1u;
     const uint32_t k = (t < d.bc_len ? t : d.bc_len) - 1u;
@@ -888,13 +891,19 @@ __global__ __launch_bounds__(1024) void tam_k_device_step(TamTensor* __restrict_
       if (f & TAM_FLAG_COSTATE) f |= TAM_FLAG_HAS_STATE;
       if (f & TAM_FLAG_EF) f |= TAM_FLAG_HAS_EF;
     }
-    d.flags = f;
+    d.flags = f | (skip ? TAM_FLAG_SKIP : 0u);
   }
   __syncthreads();
   for (int i = threadIdx.x; i < nT; i += blockDim.x) {
     const TamTensor& d = T[i];
-    if (d.flags & TAM_FLAG_DEVICE_STEP) *d.step_dev = d.step;
+    if ((d.flags & (TAM_FLAG_DEVICE_STEP | TAM_FLAG_SKIP)) == TAM_FLAG_DEVICE_STEP) *d.step_dev = d.step;
   }
+}
+
+// A step skipped on the device (TAM_FLAG_SKIP; found_inf is given for every
+// descriptor or for none, so descriptor 0 decides for the whole step).
+__device__ __forceinline__ bool tam_step_skipped(const TamTensor* __restrict__ T) {
+  return (T[0].flags & TAM_FLAG_SKIP) != 0u;
 }
 
 // ---------------------------------------------------------------------------
@@ -992,6 +1001,7 @@ template <uint32_t DT>
 __device__ __forceinline__ void tam_k1_full_body(const TamTensor* __restrict__ T, int nT, uint32_t total_tiles,
                                                  uint32_t seed_lo, uint32_t seed_hi,
                                                  double2* __restrict__ partials) {
+  if (tam_step_skipped(T)) return;
   __shared__ float lut[TAM_WG / 64][4 * 64];
   __shared__ TamLdsTabs tabs;
   tam_lds_tabs_fill(&tabs);
@@ -1026,6 +1036,7 @@ TAM_K1_FULL_KERNEL(tam_k1_main_f32, TAM_DTYPE_F32, 5)
 // 16-byte aligned.  One workgroup per tensor; wave w takes every fourth quarter.
 __global__ __launch_bounds__(TAM_WG) void tam_k1_tail(const TamTensor* __restrict__ T, uint32_t seed_lo,
                                                       uint32_t seed_hi, double2* __restrict__ partials) {
+  if (tam_step_skipped(T)) return;
   if (T[blockIdx.x].flags & TAM_FLAG_EF) return;  // the whole workgroup: tam_k1_ef covers the tensor
   __shared__ float lut[TAM_WG / 64][4 * 64];
   __shared__ TamLdsTabs tabs;
@@ -1056,6 +1067,7 @@ __global__ __launch_bounds__(TAM_WG) void tam_k1_tail(const TamTensor* __restric
 __global__ __launch_bounds__(TAM_WG) void tam_k1_ef(const TamTensor* __restrict__ T, int nT, uint32_t total_tiles,
                                                     uint32_t seed_lo, uint32_t seed_hi,
                                                     double2* __restrict__ partials) {
+  if (tam_step_skipped(T)) return;
   __shared__ float lut[TAM_WG / 64][4 * 64];
   __shared__ TamLdsTabs tabs;
   tam_lds_tabs_fill(&tabs);
@@ -1132,6 +1144,7 @@ __device__ double2 tam_wg_tree(double2* sh, uint32_t n) {
 __global__ __launch_bounds__(TAM_WG) void tam_k_alpha_chunks(const TamTensor* __restrict__ T, int nT,
                                                              const double2* __restrict__ partials,
                                                              double2* __restrict__ chunk_sums) {
+  if (tam_step_skipped(T)) return;
   __shared__ double2 sh[TAM_WG];
   const uint32_t c = blockIdx.x;
   // tensor owning chunk c: the first whose chunk range ends after c
@@ -1171,6 +1184,7 @@ __global__ __launch_bounds__(TAM_WG) void tam_k_alpha_chunks(const TamTensor* __
 __global__ __launch_bounds__(TAM_WG) void tam_k_alpha(const TamTensor* __restrict__ T,
                                                       const double2* __restrict__ chunk_sums,
                                                       float* __restrict__ alpha_new) {
+  if (tam_step_skipped(T)) return;
   __shared__ double2 sh[2048];
   const TamTensor& d = T[blockIdx.x];
   const uint32_t nch = tam_alpha_chunks(d.flags, d.ntiles);
@@ -1276,6 +1290,7 @@ __global__ __launch_bounds__(TAM_WG) void tam_k2_encode(const TamTensor* __restr
                                                         uint32_t total_tiles,
                                                         const float* __restrict__ alpha_new,
                                                         float* __restrict__ ratios, char* __restrict__ ws) {
+  if (tam_step_skipped(T)) return;
   const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
   int ti = tam_find_tensor(T, nT, blockIdx.x);
   for (uint32_t tile = blockIdx.x; tile < total_tiles; tile += gridDim.x) {
@@ -1374,6 +1389,7 @@ __device__ __forceinline__ void tam_sel_start(const TamSel& s, uint32_t* prefix,
 
 __global__ __launch_bounds__(TAM_WG) void tam_k_sel_reset(const TamTensor* __restrict__ T, TamSel* __restrict__ sel,
                                                           uint32_t* __restrict__ hist) {
+  if (tam_step_skipped(T)) return;
   const TamTensor& d = T[blockIdx.x];
   if (!(d.flags & TAM_FLAG_COSTATE)) return;
   uint32_t* h = hist + (uint64_t)blockIdx.x * 4096u;
@@ -1393,6 +1409,7 @@ __global__ __launch_bounds__(TAM_WG) void tam_k_sel_reset(const TamTensor* __res
 
 __global__ __launch_bounds__(TAM_WG) void tam_k_sel_minmax(const TamTensor* __restrict__ T, int nT,
                                                            const float* __restrict__ ratios, TamSel* __restrict__ sel) {
+  if (tam_step_skipped(T)) return;
   __shared__ uint32_t red[2][TAM_WG / 64];
   const int t = tam_slice_tensor(T, nT, blockIdx.x);
   const TamTensor& d = T[t];
@@ -1433,6 +1450,7 @@ __device__ __forceinline__ void tam_sel_window(int top, int& sh, uint32_t& dmask
 __global__ __launch_bounds__(TAM_WG) void tam_k_sel_hist(const TamTensor* __restrict__ T, int nT,
                                                          const float* __restrict__ ratios,
                                                          const TamSel* __restrict__ sel, uint32_t* __restrict__ hist) {
+  if (tam_step_skipped(T)) return;
   __shared__ uint32_t h[2][2048];
   const int t = tam_slice_tensor(T, nT, blockIdx.x);
   const TamTensor& d = T[t];
@@ -1498,6 +1516,7 @@ __device__ uint32_t tam_wg_excl_scan(uint32_t v, uint32_t* wsum) {
 
 __global__ __launch_bounds__(TAM_SEL_WG) void tam_k_sel_pick(const TamTensor* __restrict__ T, TamSel* __restrict__ sel,
                                                              uint32_t* __restrict__ hist) {
+  if (tam_step_skipped(T)) return;
   __shared__ uint32_t wsum[TAM_SEL_WG / 64];
   __shared__ uint32_t new_prefix[2], new_k[2];
   const TamTensor& d = T[blockIdx.x];
@@ -1565,6 +1584,7 @@ __global__ __launch_bounds__(TAM_WG) void tam_k_sel_labels(const TamTensor* __re
                                                            const float* __restrict__ ratios,
                                                            const TamSel* __restrict__ sel, char* __restrict__ ws,
                                                            float* __restrict__ alpha_old) {
+  if (tam_step_skipped(T)) return;
   const int t = tam_slice_tensor(T, nT, blockIdx.x);
   const TamTensor& d = T[t];
   const float tau0 = tam_u2f(sel[t].prefix[0]);
@@ -1643,6 +1663,7 @@ __device__ __forceinline__ void tam_k4_quarter(const TamTensor& d, uint32_t wq, 
 __global__ __launch_bounds__(TAM_WG) void tam_k4_ef(const TamTensor* __restrict__ T, int nT, uint32_t total_tiles,
                                                     const float* __restrict__ alpha_new,
                                                     const float* __restrict__ alpha_old, char* __restrict__ ws) {
+  if (tam_step_skipped(T)) return;
   const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
   int ti = tam_find_tensor(T, nT, blockIdx.x);
   for (uint32_t tile = blockIdx.x; tile < total_tiles; tile += gridDim.x) {
@@ -2068,6 +2089,9 @@ int tam_prepare(TamTensor* tensors, int n_tensors, TamStepInfo* info) {
         return tam_fail(TAM_E_INVALID, "%stensor %ld: device step counters or table missing", "", i);
       ++ndev;
     }
+    if (t.found_inf != tensors[0].found_inf || (t.found_inf && !(t.flags & TAM_FLAG_DEVICE_STEP)))
+      return tam_fail(TAM_E_INVALID, "%stensor %ld: found_inf needs DEVICE_STEP and one pointer for all", "", i);
+    t.flags &= ~TAM_FLAG_SKIP;
     const uint64_t nb = (t.n + TAM_BLOCK_SIZE - 1) / TAM_BLOCK_SIZE;
     if (nb > (1ull << 31)) return tam_fail(TAM_E_INVALID, "%stensor %ld too large", "", i);
     const uint64_t nt = (nb + TAM_BPT - 1) / TAM_BPT;

@@ -50,6 +50,15 @@ class _DeviceBuffers:
         self.ws = None
         self.pinned = None
         self.pinned_bytes = b""
+        self.skip = None
+
+    def skip_flag(self, found_inf: torch.Tensor) -> torch.Tensor:
+        """A persistent copy of GradScaler's found_inf (its tensor is new every
+        step; the descriptors of a captured step keep one address)."""
+        if self.skip is None:
+            self.skip = torch.zeros(1, dtype=torch.float32, device=self.device)
+        self.skip.copy_(found_inf.reshape(1))
+        return self.skip
 
     def upload_static(self, raw: bytes) -> torch.Tensor:
         """Pinned host copy of `raw` that a captured graph re-reads on every
@@ -129,6 +138,7 @@ class TurboAdam(Optimizer):
         )
         super().__init__(params, defaults)
         self._group_step_tensors = {}
+        self._found_inf = None
         if not 0 <= int(philox_seed) < (1 << 64):
             raise ValueError(f"philox_seed must be a 64-bit unsigned integer, got {philox_seed}")
         self.philox_seed = int(philox_seed)
@@ -216,6 +226,13 @@ class TurboAdam(Optimizer):
     def state_dict(self):
         """torch's optimizer state dict plus the Philox key ("philox_seed"), so
         that a resumed run draws the same stochastic rounding."""
+        for group in self.param_groups:
+            if not group.get("capturable"):
+                continue
+            for p in group["params"]:  # a device-skipped first step leaves no encoding
+                st = self.state.get(p, {})
+                if st.get("_compress_m") and isinstance(st.get("step"), torch.Tensor):
+                    st["m_mgr"]._has_state = int(st["step"]) > 0
         sd = super().state_dict()
         sd["philox_seed"] = self.philox_seed
         return sd
@@ -452,6 +469,8 @@ class TurboAdam(Optimizer):
         t.bc_step = src.data_ptr()
         t.bc_table = table.data_ptr()
         t.bc_len = n
+        if self._found_inf is not None:
+            t.found_inf = self._skip_ptr
         t.step = 0
         t.bias_correction1 = t.bias_correction2 = 1.0
         t.inv_bc2 = 1.0
@@ -459,15 +478,18 @@ class TurboAdam(Optimizer):
 
     def _launch(self, device, items):
         lib = _lib.load()
+        bufs = self._buffers.get(device)
+        if bufs is None:
+            bufs = self._buffers[device] = _DeviceBuffers(device)
+        if self._found_inf is not None:
+            with torch.cuda.device(device):
+                self._skip_ptr = bufs.skip_flag(self._found_inf).data_ptr()
         n = len(items)
         arr = (_lib.TamTensor * n)()
         for i, (p, state, group, group_idx, tid) in enumerate(items):
             arr[i] = self._describe(p, state, group, group_idx, tid)
         info = _lib.TamStepInfo()
         _lib.check(lib.tam_prepare(arr, n, ctypes.byref(info)), "tam_prepare")
-        bufs = self._buffers.get(device)
-        if bufs is None:
-            bufs = self._buffers[device] = _DeviceBuffers(device)
         nbytes = ctypes.sizeof(arr)
         if info.n_device_step:
             # a captured graph replays this copy: the same pinned bytes every time
@@ -498,13 +520,48 @@ class TurboAdam(Optimizer):
                 mgr._has_state = True
                 mgr._original_numel = p.numel()
 
+    # GradScaler hands this optimizer grad_scale and found_inf (attributes set
+    # around step()) instead of unscaling and checking on the host.
+    _step_supports_amp_scaling = True
+
+    def _unscale_grads(self, grad_scale: torch.Tensor) -> None:
+        """Gradients times f32(1/scale), the op and rounding of GradScaler.unscale_."""
+        inv = grad_scale.double().reciprocal().float()
+        per = {}
+        for group in self.param_groups:
+            for p in group["params"]:
+                if p.grad is not None:
+                    per.setdefault((p.grad.device, p.grad.dtype), []).append(p.grad)
+        for (device, _), grads in per.items():
+            dummy = torch.zeros(1, dtype=torch.float32, device=device)
+            torch._amp_foreach_non_finite_check_and_unscale_(grads, dummy, inv.to(device))
+
     @torch.no_grad()
     def step(self, closure=None):
-        """Perform a single optimization step (reference optimizer.py:224-292)."""
+        """Perform a single optimization step (reference optimizer.py:224-292).
+
+        Under a GradScaler (torch.amp), the attributes grad_scale and found_inf
+        are set: gradients are unscaled first, and the step is skipped when
+        found_inf is nonzero -- on the device, without a host sync, when every
+        group with gradients is capturable; otherwise after one host read of
+        found_inf, as GradScaler itself does for other optimizers."""
         loss = None
         if closure is not None:
             with torch.enable_grad():
                 loss = closure()
+        grad_scale = getattr(self, "grad_scale", None)
+        found_inf = getattr(self, "found_inf", None)
+        self._found_inf = None
+        if found_inf is not None:
+            active = [g for g in self.param_groups if any(p.grad is not None for p in g["params"])]
+            if active and all(g.get("capturable") for g in active):
+                if found_inf.dtype != torch.float32 or found_inf.numel() != 1:
+                    raise RuntimeError("turboadam_amd: found_inf must be a one-element float32 tensor")
+                self._found_inf = found_inf
+            elif float(found_inf) != 0.0:
+                return loss
+        if grad_scale is not None:
+            self._unscale_grads(grad_scale)
         for group_idx, group in enumerate(self.param_groups):
             for p in group["params"]:
                 if p.grad is None:
@@ -515,5 +572,8 @@ class TurboAdam(Optimizer):
                 if group["compress_v"] and "compressed_v" not in state:
                     state["compressed_v"] = init_v_state(p, group["v_bits"], group["block_size"])
         self._prepare_step_scalars()
-        self._full_step_kernel()
+        try:
+            self._full_step_kernel()
+        finally:
+            self._found_inf = None
         return loss
