@@ -204,7 +204,8 @@ def test_thresholds_order_statistics():
         s = np.sort(_f32(r))
         lo, hi = max(0, int(0.1 * nb) - 1), min(nb - 1, int(0.9 * nb))
         assert _thr(r) == (s[lo], s[hi])
-    # probe 6 of the survey: n = 4608 -> ranks 459 and 4147
+    # Python's int(0.1 * 4608) is 460 and int(0.9 * 4608) is 4147 (0.9 * 4608 = 4147.2):
+    # ranks 459 and 4147
     assert O.ranks(4608, 0.10, 0.90) == (459, 4147)
 
 
