@@ -385,3 +385,17 @@ def test_update_near_overflow():
     p[3::7] = -np.float32(3.3e38)
     grads = _edge_grads(rng, [n], 3, 1.0)
     _check(_edge_run(BF16, [p], grads, lr=3e37))
+
+
+def test_200_step_trajectory_bit_exact():
+    # a long run: every packed state byte and every parameter bit after 50, 100,
+    # 150 and 200 steps (mixed dtypes, tails, an fp32-m tensor)
+    log("200 steps, mixed dtypes, bit-exact every 50 steps")
+    sizes = [5000, 4096 + 77, 300, 20_000]
+    _check(run_side_by_side(sizes, [BF16, F16, F32, F32], steps=200, check_every=50, lr=6e-4, weight_decay=0.01))
+
+
+def test_200_step_trajectory_error_feedback_bit_exact():
+    log("200 steps with error feedback, bf16, bit-exact every 50 steps")
+    _check(run_side_by_side([9000, 4608 + 77], [BF16, BF16], steps=200, check_every=50, error_feedback=True,
+                            lr=6e-4, weight_decay=0.01))
