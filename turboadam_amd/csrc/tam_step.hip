@@ -2109,11 +2109,15 @@ static uint64_t tam_ef_stage_bytes(uint64_t n, uint64_t nb) { return 7u * nb + (
 
 // Workgroups of a kernel that fit on the device at once (CUs times the
 // occupancy its registers and LDS allow), cached per device and kernel.  The
-// tile loops launch TAM_GRID_ROUNDS times that many workgroups: measured on
-// MI355X (Llama-shaped bf16 set), pass 1 and pass 2 run 20-25% faster with 32
-// rounds of ~30 tiles per workgroup than with one resident round of
-// persistent workgroups, and slow down again beyond 64 rounds.
+// tile loops launch TAM_GRID_ROUNDS times that many workgroups, pass 2
+// TAM_K2_GRID_ROUNDS times.  Measured on MI355X (Llama-shaped bf16 set): pass 0
+// is 14% faster with 32 rounds than with one resident round of persistent
+// workgroups (8 rounds: 1% slower than 32); pass 2, which loads each quarter
+// one ahead, is fastest with 8 rounds (7% faster than 32, 15% than 1).
 enum { TAM_KS_K1_BF16, TAM_KS_K1_F16, TAM_KS_K1_F32, TAM_KS_K2, TAM_KS_K1_EF, TAM_KS_K4_EF, TAM_KS_COUNT };
+#ifndef TAM_K2_GRID_ROUNDS
+#define TAM_K2_GRID_ROUNDS 8
+#endif
 #ifndef TAM_GRID_ROUNDS
 #define TAM_GRID_ROUNDS 32
 #endif
@@ -2258,7 +2262,8 @@ static int tam_launch_pass(int pass, const TamTensor* d_tensors, const TamStepIn
   uint32_t* hist = (uint32_t*)(ws + info->off_hist);
   float* alpha_old = (float*)(ws + info->off_ef_alpha);
   auto grid_of = [&](int which, const void* kernel) {
-    const uint32_t g = tam_resident_grid(which, kernel) * TAM_GRID_ROUNDS;
+    const uint32_t rounds = which == TAM_KS_K2 ? TAM_K2_GRID_ROUNDS : TAM_GRID_ROUNDS;
+    const uint32_t g = tam_resident_grid(which, kernel) * rounds;
     return info->total_tiles < g ? info->total_tiles : g;
   };
   switch (pass) {
