@@ -857,6 +857,26 @@ __device__ __forceinline__ int tam_find_tensor(const TamTensor* __restrict__ T, 
   return lo;
 }
 
+// The tensor holding `tile`, given that tensor ti or a later one holds it
+// (persistent workgroups visit their tiles in increasing order).  A grid
+// stride spans a few large tensors but can span hundreds of small ones, so a
+// few steps forward come first and a binary search over the rest after: each
+// step is a dependent load of a descriptor.
+__device__ __forceinline__ int tam_advance_tensor(const TamTensor* __restrict__ T, int nT, int ti, uint32_t tile) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const TamTensor& d = T[__builtin_amdgcn_readfirstlane(ti)];
+    if (tile < d.tile0 + d.ntiles) return ti;
+    ++ti;  // a later tensor holds the tile, so ti + 1 < nT
+  }
+  int lo = ti, hi = nT - 1;  // the last tensor starting at or before the tile
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (T[__builtin_amdgcn_readfirstlane(mid)].tile0 <= tile) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
 // Whether a wave's quarter of tile `wq` lies inside the tensor with aligned arrays.
 __device__ __forceinline__ bool tam_quarter_full(const TamTensor& d, uint32_t wq) {
   const bool aligned = (((uintptr_t)d.param | (uintptr_t)d.grad) & 15u) == 0;
@@ -1014,7 +1034,7 @@ __device__ __forceinline__ void tam_k1_full_body(const TamTensor* __restrict__ T
   float* lutw = lut[wave];
   int ti = tam_find_tensor(T, nT, blockIdx.x);
   for (uint32_t tile = blockIdx.x; tile < total_tiles; tile += gridDim.x) {
-    while (tile >= T[ti].tile0 + T[ti].ntiles) ++ti;
+    ti = tam_advance_tensor(T, nT, ti, tile);
     const TamTensor& d = T[ti];
     if (d.dtype != DT || (d.flags & TAM_FLAG_EF)) continue;  // uniform; EF: tam_k1_ef
     const uint32_t wq = (tile - d.tile0) * 4u + wave;        // quarter tile within the tensor
@@ -1079,7 +1099,7 @@ __global__ __launch_bounds__(TAM_WG) void tam_k1_ef(const TamTensor* __restrict_
   const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
   int ti = tam_find_tensor(T, nT, blockIdx.x);
   for (uint32_t tile = blockIdx.x; tile < total_tiles; tile += gridDim.x) {
-    while (tile >= T[ti].tile0 + T[ti].ntiles) ++ti;
+    ti = tam_advance_tensor(T, nT, ti, tile);
     const TamTensor& d = T[ti];
     if (!(d.flags & TAM_FLAG_EF)) continue;  // uniform over the workgroup
     const uint32_t wq = (tile - d.tile0) * 4u + wave;
@@ -1356,7 +1376,7 @@ __global__ __launch_bounds__(TAM_WG) __attribute__((amdgpu_waves_per_eu(7, 7))) 
   // the next tile at or after `tile` of a CoState tensor (uniform)
   const auto next = [&](uint32_t& tile, int& ti) -> bool {
     for (; tile < total_tiles; tile += gridDim.x) {
-      while (tile >= desc(ti).tile0 + desc(ti).ntiles) ++ti;
+      ti = tam_advance_tensor(T, nT, ti, tile);
       if (desc(ti).flags & TAM_FLAG_COSTATE) return true;
     }
     return false;
@@ -1738,7 +1758,7 @@ __global__ __launch_bounds__(TAM_WG) void tam_k4_ef(const TamTensor* __restrict_
   const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
   int ti = tam_find_tensor(T, nT, blockIdx.x);
   for (uint32_t tile = blockIdx.x; tile < total_tiles; tile += gridDim.x) {
-    while (tile >= T[ti].tile0 + T[ti].ntiles) ++ti;
+    ti = tam_advance_tensor(T, nT, ti, tile);
     const TamTensor& d = T[ti];
     if (!(d.flags & TAM_FLAG_EF)) continue;  // uniform over the workgroup
     const uint32_t wq = (tile - d.tile0) * 4u + wave;

@@ -13,6 +13,7 @@ loop.  Parameters must live on a HIP device; there is no CPU path.
 import ctypes
 import math
 
+import numpy as np
 import torch
 from torch.optim import Optimizer
 
@@ -38,6 +39,17 @@ _F32 = ctypes.c_float
 def _f32(x: float) -> float:
     """Round a Python float (double) to fp32, as torch does for a scalar operand."""
     return _F32(x).value
+
+
+# numpy view of the descriptor layout (include/turboadam_amd.h TamTensor)
+_DESC = np.dtype(_lib.TamTensor)
+# the fields gathered per tensor, in the order _describe collects them
+_ROW_FIELDS = ("param", "grad", "v_idx", "v_scales", "exp_avg_sq", "exp_avg", "signs", "labels", "norms", "amp",
+               "alpha", "ef_residual", "n", "dtype", "flags", "v_bits", "tensor_id", "step", "k_lo", "k_hi")
+# the fields a parameter group shares, in the order _group_fields returns them
+_GROUP_FIELDS = ("c_wd", "beta1", "one_minus_beta1", "beta2", "one_minus_beta2", "bias_correction1",
+                 "bias_correction2", "inv_bc2", "inv_bc2_f32", "eps", "neg_lr", "sqrt_block")
+_SQRT_BLOCK_F32 = _f32(math.sqrt(BLOCK_SIZE))
 
 
 class _DeviceBuffers:
@@ -139,6 +151,7 @@ class TurboAdam(Optimizer):
         super().__init__(params, defaults)
         self._group_step_tensors = {}
         self._found_inf = None
+        self._keepalive = []  # states holding a contiguous copy of their gradient for this step
         if not 0 <= int(philox_seed) < (1 << 64):
             raise ValueError(f"philox_seed must be a 64-bit unsigned integer, got {philox_seed}")
         self.philox_seed = int(philox_seed)
@@ -193,30 +206,51 @@ class TurboAdam(Optimizer):
     # ------------------------------------------------------------------
     # bias corrections (reference optimizer.py:172-188)
     # ------------------------------------------------------------------
-    def _prepare_step_scalars(self):
-        """Bias corrections for the coming step, per (group, device).
+    def _collect(self):
+        """One pass over the parameters (reference optimizer.py:224-292).
 
-        The reference fills one shared 1-element tensor per (group, device) once
-        per parameter in the group, so the value every parameter uses is the one
-        of the last parameter with state; the same value is computed here and
-        written to the shared tensors.
+        Parameters with a gradient get their lazy state and are grouped per
+        device with their tensor ids (their position in the parameter list).
+        The bias corrections of the coming step are computed per (group,
+        device): the reference fills one shared 1-element tensor per (group,
+        device) once per parameter in the group (optimizer.py:172-188), so the
+        value every parameter uses is the one of the group's last parameter
+        with state; that value is computed here and written to the shared
+        tensors.  Step counters advance only once the step is launched.
         """
+        per_device = {}
         self._bc_values = {}
+        tid = -1
         for group_idx, group in enumerate(self.param_groups):
-            if group.get("capturable"):
-                continue  # computed on the device (tam_k_device_step)
-            beta1, beta2 = group["betas"]
+            device_step = group.get("capturable")  # computed on the device (tam_k_device_step)
+            last = {}
             for p in group["params"]:
-                if p not in self.state:
-                    continue
-                next_step = self.state[p]["step"] + 1
-                key = (group_idx, p.device.type, p.device.index)
-                self._bc_values[key] = (1.0 - beta1**next_step, 1.0 - beta2**next_step)
+                tid += 1
+                if p.grad is None:
+                    state = self.state.get(p)
+                    if state is None:
+                        continue
+                else:
+                    state = self.state[p]
+                    if len(state) == 0:
+                        self._init_state(p, group, group_idx, state)
+                    if group["compress_v"] and "compressed_v" not in state:
+                        state["compressed_v"] = init_v_state(p, group["v_bits"], group["block_size"])
+                    per_device.setdefault(p.device, []).append((p, state, group, group_idx, tid))
+                if not device_step:
+                    dev = p.device
+                    last[(dev.type, dev.index)] = state["step"]
+            if last:
+                beta1, beta2 = group["betas"]
+                for (dtype_, index), step in last.items():
+                    next_step = step + 1
+                    self._bc_values[(group_idx, dtype_, index)] = (1.0 - beta1**next_step, 1.0 - beta2**next_step)
         for key, (bc1, bc2) in self._bc_values.items():
             t = self._group_step_tensors.get(key)
             if t is not None:
                 t["bc1"].fill_(bc1)
                 t["bc2"].fill_(bc2)
+        return per_device
 
     # ------------------------------------------------------------------
     # state dict (reference optimizer.py:194-218)
@@ -323,106 +357,115 @@ class TurboAdam(Optimizer):
     # ------------------------------------------------------------------
     # the step
     # ------------------------------------------------------------------
-    def _full_step_kernel(self):
-        """One fused step of every parameter with a gradient (reference optimizer.py:88-170)."""
-        per_device = {}
-        tensor_id = 0
-        for group_idx, group in enumerate(self.param_groups):
-            for p in group["params"]:
-                tid = tensor_id
-                tensor_id += 1
-                if p.grad is None:
-                    continue
-                state = self.state[p]
-                if not group.get("capturable"):
-                    state["step"] += 1  # capturable: the step's first launch counts it
-                per_device.setdefault(p.device, []).append((p, state, group, group_idx, tid))
-        for device, items in per_device.items():
-            self._launch(device, items)
-
-    def _describe(self, p, state, group, group_idx, tid) -> _lib.TamTensor:
-        if group["block_size"] != BLOCK_SIZE:
-            raise NotImplementedError("turboadam_amd kernels use 128-element blocks (block_size=128)")
-        g = p.grad
-        if g.is_sparse:
-            raise RuntimeError("turboadam_amd.TurboAdam does not support sparse gradients")
-        if p.dtype not in _DTYPES:
-            raise NotImplementedError(f"turboadam_amd: unsupported parameter dtype {p.dtype}")
-        if g.dtype != p.dtype or g.device != p.device:
-            raise RuntimeError("turboadam_amd: gradient dtype/device must match the parameter")
-        if not p.is_contiguous():
-            raise RuntimeError("turboadam_amd: parameters must be contiguous")
-        if not g.is_contiguous():
-            g = g.contiguous()
-            state["_grad_keepalive"] = g
-        t = _lib.TamTensor()
-        n = p.numel()
-        nb = num_blocks(n)
-        t.param = p.data_ptr()
-        t.grad = g.data_ptr()
-        t.n = n
-        t.dtype = _DTYPES[p.dtype]
-        flags = 0
+    def _group_fields(self, group, group_idx, device):
+        """The descriptor fields one group shares on one device, each rounded
+        to fp32 once (the kernels' scalars; reference optimizer.py:88-170)."""
         lr = group["lr"]
         beta1, beta2 = group["betas"]
         wd = group["weight_decay"]
-        if group["compress_v"]:
-            cv = state["compressed_v"]
-            if cv["indices"].dtype != torch.uint8 or cv["scales"].dtype != torch.float16:
-                raise RuntimeError("turboadam_amd: compressed_v tensors have unexpected dtypes")
-            if cv["indices"].numel() != nb * BLOCK_SIZE or cv["scales"].numel() != nb * 2:
-                raise RuntimeError("turboadam_amd: compressed_v does not match the parameter size")
-            flags |= _lib.TAM_FLAG_COMPRESS_V
-            t.v_idx = cv["indices"].data_ptr()
-            t.v_scales = cv["scales"].data_ptr()
-            t.v_bits = cv["n_bits"]
-        else:
-            t.exp_avg_sq = state["exp_avg_sq"].data_ptr()
-        if state["_compress_m"]:
-            mgr = state["m_mgr"]
-            enc = mgr._encoded
-            flags |= _lib.TAM_FLAG_COSTATE
-            if mgr._has_state:
-                flags |= _lib.TAM_FLAG_HAS_STATE
-            t.signs = enc["sign_packed"].data_ptr()
-            t.labels = enc["labels"].data_ptr()
-            t.norms = enc["block_norms"].data_ptr()
-            t.amp = enc["scales"].data_ptr()
-            t.alpha = mgr._alpha.data_ptr()
-            t.k_lo, t.k_hi = mgr.ranks(nb)
-            if mgr._error_feedback:
-                # costate.py:409-437: the residual exists from the tensor's first
-                # update on; that update writes it without reading it
-                flags |= _lib.TAM_FLAG_EF
-                if mgr._ef_residual is None:
-                    mgr._ef_residual = torch.zeros_like(p, dtype=torch.float32)
-                else:
-                    flags |= _lib.TAM_FLAG_HAS_EF
-                t.ef_residual = mgr._ef_residual.data_ptr()
-        else:
-            t.exp_avg = state["exp_avg"].data_ptr()
-        if wd != 0.0:
-            flags |= _lib.TAM_FLAG_WD
-        t.flags = flags
-        t.tensor_id = tid & 0xFFFFFFFF
-        step = state["step"]
-        t.step = 0 if isinstance(step, torch.Tensor) else step & 0xFFFFFFFF  # capturable: filled on the device
-        bc1, bc2 = self._bc_values.get((group_idx, p.device.type, p.device.index), (1.0, 1.0))
-        t.c_wd = _f32(1.0 - lr * wd)
-        t.beta1 = _f32(beta1)
-        t.one_minus_beta1 = _f32(1.0 - beta1)
-        t.beta2 = _f32(beta2)
-        t.one_minus_beta2 = _f32(1.0 - beta2)
-        t.bias_correction1 = _f32(bc1)
-        t.bias_correction2 = _f32(bc2)
-        t.inv_bc2 = 1.0 / t.bias_correction2
-        t.inv_bc2_f32 = _f32(t.inv_bc2)
-        t.eps = _f32(group["eps"])
-        t.neg_lr = _f32(-lr)
-        t.sqrt_block = _f32(math.sqrt(BLOCK_SIZE))
         if group.get("capturable"):
-            self._describe_device_step(t, p, state, group)
-        return t
+            bc1 = bc2 = 1.0  # the first launch takes them from the device table
+        else:
+            bc1, bc2 = self._bc_values.get((group_idx, device.type, device.index), (1.0, 1.0))
+        bc2_f = _f32(bc2)
+        inv_bc2 = 1.0 / bc2_f
+        return (_f32(1.0 - lr * wd), _f32(beta1), _f32(1.0 - beta1), _f32(beta2), _f32(1.0 - beta2), _f32(bc1),
+                bc2_f, inv_bc2, _f32(inv_bc2), _f32(group["eps"]), _f32(-lr), _SQRT_BLOCK_F32)
+
+    def _describe(self, device, items) -> np.ndarray:
+        """The descriptor table (TamTensor rows) of one device's step.
+
+        The per-tensor fields are gathered in one pass over the items and
+        written column by column; the scalars a group shares are computed
+        once per group.  The derived fields stay zero for tam_prepare."""
+        rows = []
+        group_rows = []
+        groups = {}
+        device_step = []
+        for p, state, group, group_idx, tid in items:
+            gi = groups.get(group_idx)
+            if gi is None:
+                if group["block_size"] != BLOCK_SIZE:
+                    raise NotImplementedError("turboadam_amd kernels use 128-element blocks (block_size=128)")
+                gi = groups[group_idx] = (len(group_rows), group["compress_v"],
+                                          _lib.TAM_FLAG_WD if group["weight_decay"] != 0.0 else 0,
+                                          bool(group.get("capturable")))
+                group_rows.append(self._group_fields(group, group_idx, device))
+            gk, compress_v, flags, capturable = gi
+            g = p.grad
+            if g.is_sparse:
+                raise RuntimeError("turboadam_amd.TurboAdam does not support sparse gradients")
+            code = _DTYPES.get(p.dtype)
+            if code is None:
+                raise NotImplementedError(f"turboadam_amd: unsupported parameter dtype {p.dtype}")
+            if g.dtype != p.dtype or g.device != p.device:
+                raise RuntimeError("turboadam_amd: gradient dtype/device must match the parameter")
+            if not p.is_contiguous():
+                raise RuntimeError("turboadam_amd: parameters must be contiguous")
+            if not g.is_contiguous():
+                g = g.contiguous()
+                state["_grad_keepalive"] = g
+                self._keepalive.append(state)
+            n = p.numel()
+            nb = num_blocks(n)
+            v_idx = v_scales = v_bits = exp_avg_sq = exp_avg = 0
+            signs = labels = norms = amp = alpha = ef = 0
+            k_lo = k_hi = 0
+            if compress_v:
+                cv = state["compressed_v"]
+                idx, scl = cv["indices"], cv["scales"]
+                if idx.dtype != torch.uint8 or scl.dtype != torch.float16:
+                    raise RuntimeError("turboadam_amd: compressed_v tensors have unexpected dtypes")
+                if idx.numel() != nb * BLOCK_SIZE or scl.numel() != nb * 2:
+                    raise RuntimeError("turboadam_amd: compressed_v does not match the parameter size")
+                flags |= _lib.TAM_FLAG_COMPRESS_V
+                v_idx, v_scales, v_bits = idx.data_ptr(), scl.data_ptr(), cv["n_bits"]
+            else:
+                exp_avg_sq = state["exp_avg_sq"].data_ptr()
+            if state["_compress_m"]:
+                mgr = state["m_mgr"]
+                enc = mgr._encoded
+                flags |= _lib.TAM_FLAG_COSTATE
+                if mgr._has_state:
+                    flags |= _lib.TAM_FLAG_HAS_STATE
+                signs = enc["sign_packed"].data_ptr()
+                labels = enc["labels"].data_ptr()
+                norms = enc["block_norms"].data_ptr()
+                amp = enc["scales"].data_ptr()
+                alpha = mgr._alpha.data_ptr()
+                k_lo, k_hi = mgr.ranks(nb)
+                if mgr._error_feedback:
+                    # costate.py:409-437: the residual exists from the tensor's first
+                    # update on; that update writes it without reading it
+                    flags |= _lib.TAM_FLAG_EF
+                    if mgr._ef_residual is None:
+                        mgr._ef_residual = torch.zeros_like(p, dtype=torch.float32)
+                    else:
+                        flags |= _lib.TAM_FLAG_HAS_EF
+                    ef = mgr._ef_residual.data_ptr()
+            else:
+                exp_avg = state["exp_avg"].data_ptr()
+            if capturable:
+                device_step.append((len(rows), p, state, group))
+                step = 0  # filled on the device
+            else:
+                step = state["step"] + 1  # the counter advances once the step is launched
+            rows.append((p.data_ptr(), g.data_ptr(), v_idx, v_scales, exp_avg_sq, exp_avg, signs, labels, norms,
+                         amp, alpha, ef, n, code, flags, v_bits, tid & 0xFFFFFFFF, step & 0xFFFFFFFF, k_lo, k_hi,
+                         gk))
+        table = np.zeros(len(rows), dtype=_DESC)
+        if not rows:
+            return table
+        cols = list(zip(*rows))
+        for name, col in zip(_ROW_FIELDS, cols):
+            table[name] = col
+        gsel = np.asarray(cols[-1], dtype=np.intp)
+        gvals = np.asarray(group_rows, dtype=np.float64)
+        for j, name in enumerate(_GROUP_FIELDS):
+            table[name] = gvals[gsel, j]
+        if device_step:
+            self._describe_device_step(table, device, device_step)
+        return table
 
     # ------------------------------------------------------------------
     # capturable steps (the step counter and bias corrections on the device)
@@ -450,31 +493,33 @@ class TurboAdam(Optimizer):
             self._bc_tables[key] = (table, t)
         return self._bc_tables[key]
 
-    def _describe_device_step(self, t, p, state, group):
+    def _describe_device_step(self, table, device, rows):
         """Fields of a capturable step: the kernels' first launch fills step,
         the bias corrections and the HAS_* flags from device counters, so the
         descriptor itself stays the same from step to step."""
-        step = state["step"]
-        if not (isinstance(step, torch.Tensor) and step.dtype == torch.int32 and step.device == p.device):
-            raise RuntimeError("turboadam_amd: a capturable parameter's state['step'] must be an int32 tensor "
-                               "on its device")
-        beta1, beta2 = group["betas"]
-        table, n = self._bc_table(beta1, beta2, p.device)
-        src = None  # the group's last parameter with state on this device (optimizer.py:172-188)
-        for q in group["params"]:
-            if q in self.state and q.device == p.device:
-                src = self.state[q]["step"]
-        t.flags = (t.flags & ~(_lib.TAM_FLAG_HAS_STATE | _lib.TAM_FLAG_HAS_EF)) | _lib.TAM_FLAG_DEVICE_STEP
-        t.step_dev = step.data_ptr()
-        t.bc_step = src.data_ptr()
-        t.bc_table = table.data_ptr()
-        t.bc_len = n
-        if self._found_inf is not None:
-            t.found_inf = self._skip_ptr
-        t.step = 0
-        t.bias_correction1 = t.bias_correction2 = 1.0
-        t.inv_bc2 = 1.0
-        t.inv_bc2_f32 = 1.0
+        bc_src = {}  # per group: the last parameter with state on this device (optimizer.py:172-188)
+        for i, p, state, group in rows:
+            step = state["step"]
+            if not (isinstance(step, torch.Tensor) and step.dtype == torch.int32 and step.device == p.device):
+                raise RuntimeError("turboadam_amd: a capturable parameter's state['step'] must be an int32 tensor "
+                                   "on its device")
+            src = bc_src.get(id(group))
+            if src is None:
+                for q in group["params"]:
+                    if q in self.state and q.device == device:
+                        src = self.state[q]["step"]
+                bc_src[id(group)] = src
+            beta1, beta2 = group["betas"]
+            bc_table, bc_len = self._bc_table(beta1, beta2, device)
+            r = table[i:i + 1]
+            r["flags"] = (r["flags"] & ~np.uint32(_lib.TAM_FLAG_HAS_STATE | _lib.TAM_FLAG_HAS_EF)) \
+                | np.uint32(_lib.TAM_FLAG_DEVICE_STEP)
+            r["step_dev"] = step.data_ptr()
+            r["bc_step"] = src.data_ptr()
+            r["bc_table"] = bc_table.data_ptr()
+            r["bc_len"] = bc_len
+            if self._found_inf is not None:
+                r["found_inf"] = self._skip_ptr
 
     def _launch(self, device, items):
         lib = _lib.load()
@@ -484,10 +529,9 @@ class TurboAdam(Optimizer):
         if self._found_inf is not None:
             with torch.cuda.device(device):
                 self._skip_ptr = bufs.skip_flag(self._found_inf).data_ptr()
+        table = self._describe(device, items)
         n = len(items)
-        arr = (_lib.TamTensor * n)()
-        for i, (p, state, group, group_idx, tid) in enumerate(items):
-            arr[i] = self._describe(p, state, group, group_idx, tid)
+        arr = (_lib.TamTensor * n).from_buffer(table)
         info = _lib.TamStepInfo()
         _lib.check(lib.tam_prepare(arr, n, ctypes.byref(info)), "tam_prepare")
         nbytes = ctypes.sizeof(arr)
@@ -514,7 +558,8 @@ class TurboAdam(Optimizer):
                     _lib.check(rc, f"tam_step_pass({k})")
                     self._pass_hook(k, "end")
         for p, state, group, group_idx, tid in items:
-            state.pop("_grad_keepalive", None)
+            if not group.get("capturable"):
+                state["step"] += 1  # capturable: the step's first launch counts it
             if state["_compress_m"]:
                 mgr = state["m_mgr"]
                 mgr._has_state = True
@@ -562,18 +607,13 @@ class TurboAdam(Optimizer):
                 return loss
         if grad_scale is not None:
             self._unscale_grads(grad_scale)
-        for group_idx, group in enumerate(self.param_groups):
-            for p in group["params"]:
-                if p.grad is None:
-                    continue
-                state = self.state[p]
-                if len(state) == 0:
-                    self._init_state(p, group, group_idx, state)
-                if group["compress_v"] and "compressed_v" not in state:
-                    state["compressed_v"] = init_v_state(p, group["v_bits"], group["block_size"])
-        self._prepare_step_scalars()
         try:
-            self._full_step_kernel()
+            # one fused step of every parameter with a gradient (reference optimizer.py:88-170)
+            for device, items in self._collect().items():
+                self._launch(device, items)
         finally:
             self._found_inf = None
+            for state in self._keepalive:
+                state.pop("_grad_keepalive", None)
+            self._keepalive = []
         return loss
