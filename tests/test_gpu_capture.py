@@ -101,3 +101,44 @@ def test_captured_step_replays_equal_eager_steps():
         torch.randn(1 << 20, device=dev).sum().item()
         bad = compare(f"replay {s - 1}")
         assert not bad, "\n".join(bad[:20])
+
+
+def test_steps_on_alternating_streams_equal_one_stream():
+    """The descriptor and workspace buffers are reused from step to step; a step
+    issued on another stream than the previous one is ordered after it."""
+    from turboadam_amd import TurboAdam
+
+    dev = torch.device("cuda:0")
+    sizes = [4_000_003, 70_001, 5000, 300]
+    dts = [BF16, BF16, F32, F32]
+    rng = np.random.default_rng(33)
+    init = [to_bits((rng.standard_normal(n) * 0.02).astype(np.float32), dt) for n, dt in zip(sizes, dts)]
+    steps = 6
+    grads = [[to_torch(to_bits((rng.standard_normal(n) * 1e-3).astype(np.float32), dt), dt, (n,), dev)
+              for n, dt in zip(sizes, dts)] for _ in range(steps)]
+    pa = [torch.nn.Parameter(to_torch(a, dt, (n,), dev)) for a, dt, n in zip(init, dts, sizes)]
+    pb = [torch.nn.Parameter(to_torch(a, dt, (n,), dev)) for a, dt, n in zip(init, dts, sizes)]
+    kw = dict(lr=1e-3, weight_decay=0.05, philox_seed=99)
+    oa, ob = TurboAdam(pa, **kw), TurboAdam(pb, **kw)
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    main = torch.cuda.current_stream()
+    for s in range(steps):
+        for p, g in zip(pa, grads[s]):
+            p.grad = g
+        oa.step()
+        st = streams[s % 2]
+        st.wait_stream(main)  # the gradients were written on the main stream
+        with torch.cuda.stream(st):
+            for p, g in zip(pb, grads[s]):
+                p.grad = g
+            ob.step()
+    for st in streams:
+        main.wait_stream(st)
+    torch.cuda.synchronize()
+    log(f"{steps} steps, alternating streams")
+    bad = []
+    for i, (a, b) in enumerate(zip(pa, pb)):
+        if not np.array_equal(_bits(from_torch(a)), _bits(from_torch(b))):
+            bad.append(f"tensor {i}: params differ")
+        bad += compare_states(gpu_state(ob, b), gpu_state(oa, a), f"tensor {i}")
+    assert not bad, "\n".join(bad[:20])

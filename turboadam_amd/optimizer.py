@@ -63,6 +63,16 @@ class _DeviceBuffers:
         self.pinned = None
         self.pinned_bytes = b""
         self.skip = None
+        self.stream = None  # the stream of the last step that used these buffers
+
+    def order_on(self, stream) -> None:
+        """The buffers are reused from step to step, not reallocated: a step on
+        another stream than the last one first waits for that stream's work.
+        (torch.cuda.graph synchronises before a capture, so a capture needs no
+        wait, and may not wait on a stream outside it.)"""
+        if self.stream is not None and self.stream != stream and not torch.cuda.is_current_stream_capturing():
+            stream.wait_stream(self.stream)
+        self.stream = stream
 
     def skip_flag(self, found_inf: torch.Tensor) -> torch.Tensor:
         """A persistent copy of GradScaler's found_inf (its tensor is new every
@@ -81,7 +91,7 @@ class _DeviceBuffers:
                 raise RuntimeError("turboadam_amd: capturable step changed its tensors during graph capture; "
                                    "run an eager warm-up step with the same parameters and gradients first")
             if self.pinned is not None:
-                torch.cuda.current_stream(self.device).synchronize()
+                torch.cuda.synchronize(self.device)  # a copy from it may be pending on any stream
             if self.pinned is None or self.pinned.numel() < len(raw):
                 self.pinned = torch.empty(max(len(raw), 4096), dtype=torch.uint8, pin_memory=True)
             ctypes.memmove(self.pinned.data_ptr(), raw, len(raw))
@@ -526,8 +536,9 @@ class TurboAdam(Optimizer):
         bufs = self._buffers.get(device)
         if bufs is None:
             bufs = self._buffers[device] = _DeviceBuffers(device)
-        if self._found_inf is not None:
-            with torch.cuda.device(device):
+        with torch.cuda.device(device):
+            bufs.order_on(torch.cuda.current_stream(device))
+            if self._found_inf is not None:
                 self._skip_ptr = bufs.skip_flag(self._found_inf).data_ptr()
         table = self._describe(device, items)
         n = len(items)
