@@ -28,6 +28,7 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <atomic>
 #include <stdio.h>
 #include <string.h>
 
@@ -2108,16 +2109,17 @@ __global__ void tam_k_math_eval(int fn, const float* __restrict__ in, float* __r
 // ---------------------------------------------------------------------------
 // host entry points
 // ---------------------------------------------------------------------------
+// Per-device launch figures, computed once (threads that race store the same value).
 static int tam_device_cus(void) {
-  static int cus[64] = {0};
+  static std::atomic<int> cus[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cus[dev] == 0) {
-    int v = 0;
+  int v = cus[dev].load(std::memory_order_relaxed);
+  if (v == 0) {
     if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
-    cus[dev] = v;
+    cus[dev].store(v, std::memory_order_relaxed);
   }
-  return cus[dev];
+  return v;
 }
 
 static uint64_t tam_align_up(uint64_t x, uint64_t a) { return (x + a - 1) / a * a; }
@@ -2142,16 +2144,18 @@ enum { TAM_KS_K1_BF16, TAM_KS_K1_F16, TAM_KS_K1_F32, TAM_KS_K2, TAM_KS_K1_EF, TA
 #define TAM_GRID_ROUNDS 32
 #endif
 static uint32_t tam_resident_grid(int which, const void* kernel) {
-  static uint32_t cache[64][TAM_KS_COUNT];
+  static std::atomic<uint32_t> cache[64][TAM_KS_COUNT];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-  if (cache[dev][which] == 0) {
+  uint32_t g = cache[dev][which].load(std::memory_order_relaxed);
+  if (g == 0) {
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, TAM_WG, 0) != hipSuccess || per_cu <= 0)
       per_cu = 4;
-    cache[dev][which] = (uint32_t)(per_cu * tam_device_cus());
+    g = (uint32_t)(per_cu * tam_device_cus());
+    cache[dev][which].store(g, std::memory_order_relaxed);
   }
-  return cache[dev][which];
+  return g;
 }
 
 extern "C" {
