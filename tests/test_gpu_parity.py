@@ -7,12 +7,15 @@ oracle to finish in seconds; full-size configurations are covered by the
 size-independent checks in test_gpu_invariants.py.
 """
 
+import math
+
 import numpy as np
 import pytest
 import torch
 
 from oracle import oracle as O
-from tests.helpers import log, run_side_by_side
+from tests.helpers import compare_states, from_torch, gpu_state, log, make_grads, run_side_by_side, to_bits, \
+    to_torch
 
 pytestmark = pytest.mark.gpu
 
@@ -399,3 +402,56 @@ def test_200_step_trajectory_error_feedback_bit_exact():
     log("200 steps with error feedback, bf16, bit-exact every 50 steps")
     _check(run_side_by_side([9000, 4608 + 77], [BF16, BF16], steps=200, check_every=50, error_feedback=True,
                             lr=6e-4, weight_decay=0.01))
+
+
+def test_param_groups_with_own_hyperparameters_and_lr_schedule():
+    """Four groups, each with its own lr, betas, eps, weight decay, v_bits,
+    thresholds and compression switches, and every group's lr changed before
+    each step as a scheduler does (param_groups[i]["lr"] mutated): bit-exact
+    against the oracle after every step."""
+    from turboadam_amd import TurboAdam
+
+    dev = torch.device("cuda:0")
+    spec = [
+        (dict(lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01, v_bits=4), [(70_001, BF16), (5000, F32)]),
+        (dict(lr=3e-4, betas=(0.8, 0.99), eps=1e-6, weight_decay=0.0, v_bits=2, null_pct=0.05, amp_pct=0.95),
+         [(20_000, F32), (300, BF16)]),
+        (dict(lr=5e-4, betas=(0.95, 0.9999), eps=1e-7, weight_decay=0.1, v_bits=8, compress_m=False),
+         [(9000, F16), (4000, F32)]),
+        (dict(lr=1e-3, weight_decay=0.05, v_bits=3, compress_v=False), [(6000, F32), (12_345, BF16)]),
+    ]
+    sizes = [n for _, ts in spec for n, _ in ts]
+    dts = [dt for _, ts in spec for _, dt in ts]
+    rng = np.random.default_rng(51)
+    init = [to_bits((rng.standard_normal(n) * 0.02).astype(np.float32), dt) for n, dt in zip(sizes, dts)]
+    g_params = [torch.nn.Parameter(to_torch(a, dt, (n,), dev)) for a, dt, n in zip(init, dts, sizes)]
+    o_params = [a.copy() for a in init]
+    g_groups, o_groups, k = [], [], 0
+    for hp, ts in spec:
+        g_groups.append(dict(params=g_params[k:k + len(ts)], **hp))
+        o_groups.append(dict(params=o_params[k:k + len(ts)], **hp))
+        k += len(ts)
+    opt = TurboAdam(g_groups, philox_seed=4242)
+    orc = O.OracleTurboAdam(o_groups, dtypes=dts, seed=4242)
+    sigmas = np.exp(np.log(1e-3) + rng.standard_normal(len(sizes)))
+    drifts = [rng.standard_normal(n).astype(np.float32) for n in sizes]
+    steps = 6
+    for s in range(steps):
+        scale = 0.1 + 0.9 * 0.5 * (1.0 + math.cos(math.pi * s / steps))  # cosine decay
+        for gi, (hp, _) in enumerate(spec):
+            opt.param_groups[gi]["lr"] = orc.param_groups[gi]["lr"] = hp["lr"] * scale
+        grads = make_grads(rng, sizes, dts, sigmas, drifts)
+        for p, g, dt, n in zip(g_params, grads, dts, sizes):
+            p.grad = to_torch(g, dt, (n,), dev)
+        opt.step()
+        orc.step(grads)
+        torch.cuda.synchronize()
+        log(f"groups: step {s + 1}, lr scale {scale:.4f}")
+        bad = []
+        for i, p in enumerate(g_params):
+            a, b = from_torch(p.data), o_params[i]
+            if not np.array_equal(a.view(np.uint32) if a.dtype == np.float32 else a,
+                                  b.view(np.uint32) if b.dtype == np.float32 else b):
+                bad.append(f"step {s + 1} tensor {i}: params differ")
+            bad += compare_states(gpu_state(opt, p), orc.state[i], f"step {s + 1} tensor {i}")
+        assert not bad, "\n".join(bad[:20])
