@@ -455,3 +455,60 @@ def test_param_groups_with_own_hyperparameters_and_lr_schedule():
                 bad.append(f"step {s + 1} tensor {i}: params differ")
             bad += compare_states(gpu_state(opt, p), orc.state[i], f"step {s + 1} tensor {i}")
         assert not bad, "\n".join(bad[:20])
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("lmin,lmax", [(-69.0, -68.75), (-69.0, -67.0), (22.0, 22.125), (-0.25, 0.25),
+                                       (-20.0, -19.9375)])
+def test_requantisation_of_narrow_log_spans(bits, lmin, lmax):
+    """Blocks whose v spans a narrow log range at large |ln v| (the state 1Q's
+    repeated re-quantisation converges to): the certified index path is at
+    its tightest there.  After one normal step both sides get the same
+    synthetic v state (fp16 log bounds lmin, lmax; random indices), then take
+    steps with gradients small enough to keep v in that range; bit-exact
+    against the oracle after every step."""
+    from turboadam_amd import TurboAdam
+
+    dev = torch.device("cuda:0")
+    sizes, dts = [40_000, 40_064, 3000], [F32, BF16, F32]
+    rng = np.random.default_rng(61 + bits)
+    init = [to_bits((rng.standard_normal(n) * 0.02).astype(np.float32), dt) for n, dt in zip(sizes, dts)]
+    g_params = [torch.nn.Parameter(to_torch(a, dt, (n,), dev)) for a, dt, n in zip(init, dts, sizes)]
+    o_params = [a.copy() for a in init]
+    kw = dict(lr=1e-3, weight_decay=0.01, v_bits=bits)
+    opt = TurboAdam(g_params, philox_seed=777 + bits, **kw)
+    orc = O.OracleTurboAdam(o_params, dtypes=dts, seed=777 + bits, **kw)
+    gscale = float(np.exp(0.5 * lmin)) * 1e-2  # (1 - beta2) g^2 ~ 1e-7 v: v stays in the span
+
+    def grads():
+        return [to_bits((rng.standard_normal(n) * gscale).astype(np.float32), dt) for n, dt in zip(sizes, dts)]
+
+    def step(gs):
+        for p, g, dt, n in zip(g_params, gs, dts, sizes):
+            p.grad = to_torch(g, dt, (n,), dev)
+        opt.step()
+        orc.step(gs)
+        torch.cuda.synchronize()
+
+    step(grads())
+    sc = np.array([lmin, lmax], dtype=np.float16).view(np.uint16)
+    for i, (p, n) in enumerate(zip(g_params, sizes)):
+        nb = (n + 127) // 128
+        idx = rng.integers(0, 1 << bits, size=nb * 128, dtype=np.uint8)
+        scales = np.tile(sc, nb)
+        cv = opt.state[p]["compressed_v"]
+        cv["indices"].copy_(torch.from_numpy(idx).to(dev))
+        cv["scales"].copy_(torch.from_numpy(scales.view(np.int16).copy()).view(torch.float16).reshape(nb, 2).to(dev))
+        orc.state[i]["indices"][:] = idx
+        orc.state[i]["scales"][:] = scales
+    for s in range(4):
+        step(grads())
+        bad = []
+        for i, p in enumerate(g_params):
+            a, b = from_torch(p.data), o_params[i]
+            if not np.array_equal(a.view(np.uint32) if a.dtype == np.float32 else a,
+                                  b.view(np.uint32) if b.dtype == np.float32 else b):
+                bad.append(f"step {s + 2} tensor {i}: params differ")
+            bad += compare_states(gpu_state(opt, p), orc.state[i], f"step {s + 2} tensor {i}")
+        log(f"narrow spans bits={bits} [{lmin}, {lmax}]: step {s + 2}, {len(bad)} mismatches")
+        assert not bad, "\n".join(bad[:20])

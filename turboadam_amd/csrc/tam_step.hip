@@ -680,27 +680,42 @@ __device__ __forceinline__ void tam_vpath_b(const TamTensor& d, const TamWave& W
   bool okv[TAM_EPL];
   bool all_ok = true;
   // Full blocks: every element lies in [vmin, vmax] (normal, no NaN checked
-  // once here), so |log2 v| <= L and, when B < 1/4, |c~| <= 2^bits + 1 (c lies
-  // in [0, 2^bits]); one bound B serves the block.  The fast path evaluates
-  // d = fl(c~ + 1/2 - u) (C + 1/2 rounded once: its error and the roundings of
-  // values up to 2^bits + 3/2 are inside the (2^bits + 2) 2^-21 and |C| 2^-21
-  // terms) and q = rndne(d), which is ceil(c - u) when d lies farther than B
-  // from every half-integer; t = d - q is exact.  A lane is accepted when
-  // max |t| < H = 1/2 - (B + 2^-22); otherwise its elements are tested one by
-  // one in the exact path below.
-  float Cp = 0.0f, H = -1.0f;
+  // once here), so one bound B serves the block.  With F = 2^bits the exact
+  // path's index is ceil(c - u), c = F fl(fl(l - lmin)/sp), l = fl(ln v).  The
+  // fast path takes c~ = K log2(t) from the hardware log2 of t = fl(v rcp(vmin)),
+  // which lies within 2^-22 of [1, vmax/vmin]: the hardware log's error is
+  // relative to log2 t <= (lmax - lmin)/ln2 rather than to |log2 v|, so the
+  // bound stays small when a block's log span sp is small (as 1Q's repeated
+  // re-quantisation makes it).  |c~ - c| is within:
+  //   F 2^-24 (Lm + |lmin|)/sp   the roundings of l and of lmin to fp32
+  //                              (Lm = max(|lmin|, |lmax|) bounds |l|);
+  //   F 2^-22 / sp               rcp(vmin) (2^-23.3) and the product (2^-24);
+  //   F 2^-21                    the hardware log2 (2^-21 relative; measured 2^-22.6);
+  //   F 2^-20                    the exact path's roundings of l - lmin and of
+  //                              the division, and K's (ln2 in fp32, rcp(sp));
+  //   (F + 2) 2^-21              the fma roundings of values up to F + 3/2,
+  // all times 1 + 2^-16 for the fp32 evaluation of the bound.  When B < 1/4,
+  // |c~| <= F + 1 (c lies in [0, F]).  The fast path evaluates d = fl(c~ + 1/2 - u)
+  // and q = rndne(d), which is ceil(c - u) when d lies farther than B from every
+  // half-integer; t = d - q is exact.  A lane is accepted when max |t| < H =
+  // 1/2 - (B + 2^-22); otherwise its elements are tested one by one in the exact
+  // path below.  Blocks with sp > 64 or vmax >= 2^100 (t or rcp(vmin) out of
+  // range) take the exact path.
+  float H = -1.0f, rmin = 0.0f;
   if (FULL) {
-    const float la = __builtin_amdgcn_logf(tam_u2f(kmn)), lb = __builtin_amdgcn_logf(tam_u2f(kmx));
-    const float L = __builtin_fmaxf(__builtin_fabsf(la), __builtin_fabsf(lb)) * (1.0f + 0x1p-18f) + 0x1p-20f;
-    const float Bb = __builtin_fmaf(L, KB, __builtin_fmaf(fnb + 2.0f, 0x1p-21f, CB));
-    const bool blk_ok = (tam_u2f(kmn) >= 0x1p-126f) && !nan_seen && (Bb < 0.25f);
+    rmin = __builtin_amdgcn_rcpf(tam_u2f(kmn));
+    const float Lm = __builtin_fmaxf(__builtin_fabsf(lmn), __builtin_fabsf(lmx));
+    const float per_sp = __builtin_fmaf(Lm + __builtin_fabsf(lmn), 0x1p-24f, 0x1p-22f);
+    const float flat = __builtin_fmaf(fnb, 0x1p-21f + 0x1p-20f, (fnb + 2.0f) * 0x1p-21f);
+    const float Bb = __builtin_fmaf(fnb * rsp, per_sp, flat) * (1.0f + 0x1p-16f);
+    const bool blk_ok = (tam_u2f(kmn) >= 0x1p-126f) && (tam_u2f(kmx) < 0x1p100f) && !nan_seen && (sp <= 64.0f) &&
+                        (Bb < 0.25f);
     H = blk_ok ? 0.5f - (Bb + 0x1p-22f) : -1.0f;
-    Cp = C + 0.5f;
     float tmax = 0.0f;
 #pragma unroll
     for (int i = 0; i < TAM_EPL; ++i) {
-      const float l2 = __builtin_amdgcn_logf(vc[i]);
-      const float ct = __builtin_fmaf(l2, K, Cp);
+      const float l2 = __builtin_amdgcn_logf(vc[i] * rmin);
+      const float ct = __builtin_fmaf(l2, K, 0.5f);
       const float dd = __builtin_fmaf(-(float)(rw[i] >> 8), 0x1p-24f, ct);  // fl(ct - u), u exact
       const float q = __builtin_rintf(dd);
       tmax = __builtin_fmaxf(tmax, __builtin_fabsf(dd - q));
@@ -728,7 +743,7 @@ __device__ __forceinline__ void tam_vpath_b(const TamTensor& d, const TamWave& W
     for (int i = 0; i < TAM_EPL; ++i) {
       if (FULL) {  // the element's own test, as in the lane's
         const float dd = __builtin_fmaf(-(float)(rw[i] >> 8), 0x1p-24f,
-                                        __builtin_fmaf(__builtin_amdgcn_logf(vc[i]), K, Cp));
+                                        __builtin_fmaf(__builtin_amdgcn_logf(vc[i] * rmin), K, 0.5f));
         okv[i] = __builtin_fabsf(dd - __builtin_rintf(dd)) < H;
       }
       if (!okv[i]) {
@@ -1040,7 +1055,11 @@ __device__ __forceinline__ void tam_k1_full_body(const TamTensor* __restrict__ T
     if (d.dtype != DT || (d.flags & TAM_FLAG_EF)) continue;  // uniform; EF: tam_k1_ef
     const uint32_t wq = (tile - d.tile0) * 4u + wave;        // quarter tile within the tensor
     if (!tam_quarter_full(d, wq)) continue;                 // left to tam_k1_tail
-    tam_k1_quarter<DT, true>(d, wq, lane, lutw, &tabs, seed_lo, seed_hi, partials + (uint64_t)tile * 4u + wave);
+    // a wave-uniform partials address: a per-lane one is spilled in the 16-bit
+    // kernels, and its reload waits for every load in flight (the fp32 kernel
+    // spills more with the scalar form, so it keeps the per-lane one)
+    double2* part = partials + (uint64_t)tile * 4u + (DT == TAM_DTYPE_F32 ? wave : __builtin_amdgcn_readfirstlane(wave));
+    tam_k1_quarter<DT, true>(d, wq, lane, lutw, &tabs, seed_lo, seed_hi, part);
   }
 }
 
