@@ -13,6 +13,7 @@ oracle/torch_mirror.py) timed on a bounded sample on this host.
 """
 
 import argparse
+import gc
 import json
 import math
 import os
@@ -249,6 +250,9 @@ def main():
 
     opt._pass_hook = hook
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    # a full collection of the warmup's garbage (tens of ms) would otherwise
+    # fire inside the first timed steps, while the GPU waits on an empty queue
+    gc.collect()
     torch.cuda.synchronize()
     start.record()
     for s in range(args.steps):
