@@ -2253,7 +2253,8 @@ int tam_prepare(TamTensor* tensors, int n_tensors, TamStepInfo* info) {
     tiles += nt;
     chunks += tam_alpha_chunks(t.flags, t.ntiles);
     slices += tam_sel_slices(t.flags, t.nb);
-    if (tiles > 0xffffffffull) return tam_fail(TAM_E_INVALID, "%stoo many tiles", "", 0);
+    // below 2^31, so that a tile index plus a grid stride cannot wrap
+    if (tiles > (1ull << 31)) return tam_fail(TAM_E_INVALID, "%stoo many tiles", "", 0);
   }
   memset(info, 0, sizeof(*info));
   info->n_tensors = n_tensors;
