@@ -507,29 +507,35 @@ class TurboAdam(Optimizer):
         """Fields of a capturable step: the kernels' first launch fills step,
         the bias corrections and the HAS_* flags from device counters, so the
         descriptor itself stays the same from step to step."""
-        bc_src = {}  # per group: the last parameter with state on this device (optimizer.py:172-188)
+        per_group = {}  # id(group) -> (bias-correction source pointer, table pointer, table length)
+        idx, step_ptrs, cols = [], [], []
         for i, p, state, group in rows:
             step = state["step"]
             if not (isinstance(step, torch.Tensor) and step.dtype == torch.int32 and step.device == p.device):
                 raise RuntimeError("turboadam_amd: a capturable parameter's state['step'] must be an int32 tensor "
                                    "on its device")
-            src = bc_src.get(id(group))
-            if src is None:
+            g = per_group.get(id(group))
+            if g is None:
+                src = None  # the group's last parameter with state on this device (optimizer.py:172-188)
                 for q in group["params"]:
                     if q in self.state and q.device == device:
                         src = self.state[q]["step"]
-                bc_src[id(group)] = src
-            beta1, beta2 = group["betas"]
-            bc_table, bc_len = self._bc_table(beta1, beta2, device)
-            r = table[i:i + 1]
-            r["flags"] = (r["flags"] & ~np.uint32(_lib.TAM_FLAG_HAS_STATE | _lib.TAM_FLAG_HAS_EF)) \
-                | np.uint32(_lib.TAM_FLAG_DEVICE_STEP)
-            r["step_dev"] = step.data_ptr()
-            r["bc_step"] = src.data_ptr()
-            r["bc_table"] = bc_table.data_ptr()
-            r["bc_len"] = bc_len
-            if self._found_inf is not None:
-                r["found_inf"] = self._skip_ptr
+                beta1, beta2 = group["betas"]
+                bc_table, bc_len = self._bc_table(beta1, beta2, device)
+                g = per_group[id(group)] = (src.data_ptr(), bc_table.data_ptr(), bc_len)
+            idx.append(i)
+            step_ptrs.append(step.data_ptr())
+            cols.append(g)
+        sel = np.asarray(idx, dtype=np.intp)
+        clear = np.uint32(_lib.TAM_FLAG_HAS_STATE | _lib.TAM_FLAG_HAS_EF)
+        table["flags"][sel] = (table["flags"][sel] & ~clear) | np.uint32(_lib.TAM_FLAG_DEVICE_STEP)
+        table["step_dev"][sel] = step_ptrs
+        src_ptr, tab_ptr, tab_len = zip(*cols)
+        table["bc_step"][sel] = src_ptr
+        table["bc_table"][sel] = tab_ptr
+        table["bc_len"][sel] = tab_len
+        if self._found_inf is not None:
+            table["found_inf"][sel] = self._skip_ptr
 
     def _launch(self, device, items):
         lib = _lib.load()
