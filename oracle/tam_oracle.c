@@ -22,6 +22,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include "tam_oracle.h"
+
 #define OR_BS 128
 
 /* ---------------------------------------------------------------- bits */
@@ -427,34 +429,7 @@ void or_quantize_logscale(const float* v, uint64_t npad, int bits, int stochasti
 }
 
 /* ------------------------------------------------------ one parameter's step */
-typedef struct OrTensor {
-  void* param;
-  const void* grad;
-  uint8_t* v_idx;
-  uint16_t* v_scales;
-  float* exp_avg_sq;
-  float* exp_avg;
-  uint8_t* signs;
-  uint8_t* labels;
-  float* norms;
-  uint16_t* amp;
-  float* alpha;
-  float* ef_residual; /* EF: f32[n] error-feedback residual (in/out) */
-  uint64_t n;
-  /* block0: first block of this tensor within the parameter it is a
-   * block-aligned slice of (0 for a whole parameter); only the stochastic
-   * rounding draws depend on it */
-  uint32_t dtype, flags, v_bits, tensor_id, step, k_lo, k_hi, block0;
-  float c_wd, beta1, one_minus_beta1, beta2, one_minus_beta2, bias_correction1, bias_correction2, eps,
-      neg_lr, sqrt_block;
-} OrTensor;
-
-#define OR_FLAG_COSTATE 1u
-#define OR_FLAG_COMPRESS_V 2u
-#define OR_FLAG_HAS_STATE 4u
-#define OR_FLAG_WD 8u
-#define OR_FLAG_EF 16u
-#define OR_FLAG_HAS_EF 32u
+/* OrTensor and the OR_FLAG_* values: tam_oracle.h */
 
 /* TurboAdam._full_step_kernel body for one parameter, reference
  * optimizer.py:97-170 (the caller increments the step counter and supplies
