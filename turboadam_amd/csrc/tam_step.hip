@@ -664,7 +664,9 @@ __device__ __forceinline__ void tam_vpath_b(const TamTensor& d, const TamWave& W
   }
   // certified stochastic rounding.  K and C from the hardware reciprocal of
   // sp (within 2^-23): K within 2^-22 of ln2*2^bits/sp, C within 2^-22.4 of
-  // -lmin*2^bits/sp; the bound below takes |log2 v| K 2^-20 and |C| 2^-21.
+  // -lmin*2^bits/sp.  Partial blocks (c~ = K log2 v + C, per element) take
+  // |log2 v| K 2^-20 and |C| 2^-21 into their bound; full blocks use K with
+  // the ratio form below.
   const float rsp = __builtin_amdgcn_rcpf(sp);
   const float K = (0x1.62e430p-1f * fnb) * rsp;
   const float C = (-lmn * fnb) * rsp;
