@@ -60,6 +60,20 @@ def gpt2_124m_shapes():
     return s
 
 
+def llama3_8b_rank0_of8_shapes():
+    """Rank 0's share of the Llama-3-8B-shaped set when whole tensors are dealt
+    to 8 ranks by greedy bin packing on size (largest first, to the lightest
+    rank): the per-GPU shape of tensor-granular data-parallel sharding."""
+    shapes = llama3_8b_shapes()
+    load, bins = [0] * 8, [[] for _ in range(8)]
+    for name, shp in sorted(shapes, key=lambda x: -math.prod(x[1])):
+        r = min(range(8), key=lambda i: load[i])
+        bins[r].append((name, shp))
+        load[r] += math.prod(shp)
+    order = {name: i for i, (name, _) in enumerate(shapes)}
+    return sorted(bins[0], key=lambda x: order[x[0]])
+
+
 def ragged_shapes(seed=0, count=1000):
     rng = np.random.default_rng(seed)
     sizes = np.maximum(1, np.round(2.0 ** (20 * rng.random(count)))).astype(np.int64)
@@ -78,6 +92,8 @@ WORKLOADS = {
            "gpt2-block fp32 m+v v_bits=4"),
     "c4": (ragged_shapes, torch.float32, dict(lr=1e-3, v_bits=4), math.log(1e-3),
            "ragged 1000 tensors fp32 m+v v_bits=4"),
+    "c3-rank0of8": (llama3_8b_rank0_of8_shapes, torch.bfloat16, dict(lr=3e-4, weight_decay=0.1, v_bits=4),
+                    math.log(1e-4), "llama3-8b-shaped bf16 m+v v_bits=4, rank 0 of 8 (tensor sharding)"),
 }
 
 
@@ -148,7 +164,7 @@ TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "tam_k1_main_c3_fetch_write.md"
 
 
 def measured_traffic(workload: str):
-    """HBM bytes per pass-1 launch from the committed rocprofv3 FETCH_SIZE /
+    """HBM bytes per pass-0 launch from the committed rocprofv3 FETCH_SIZE /
     WRITE_SIZE summary (counters scaled by their plain-copy calibration), or
     None when no summary covers this workload."""
     if workload != "c3" or not os.path.exists(TRAFFIC_PROFILE):
