@@ -92,24 +92,29 @@ WORKLOADS = {
            "gpt2-block fp32 m+v v_bits=4"),
     "c4": (ragged_shapes, torch.float32, dict(lr=1e-3, v_bits=4), math.log(1e-3),
            "ragged 1000 tensors fp32 m+v v_bits=4"),
+    "c3-ef": (llama3_8b_shapes, torch.bfloat16, dict(lr=3e-4, weight_decay=0.1, v_bits=4, error_feedback=True),
+              math.log(1e-4), "llama3-8b-shaped bf16 m+v v_bits=4, error feedback"),
     "c3-rank0of8": (llama3_8b_rank0_of8_shapes, torch.bfloat16, dict(lr=3e-4, weight_decay=0.1, v_bits=4),
                     math.log(1e-4), "llama3-8b-shaped bf16 m+v v_bits=4, rank 0 of 8 (tensor sharding)"),
 }
 
 
-def bytes_per_param(dtype_bytes: int, costate: bool, compress_v: bool = True):
+def bytes_per_param(dtype_bytes: int, costate: bool, compress_v: bool = True, ef: bool = False):
     """Algorithmic HBM bytes per parameter per step (whole step and pass 0 alone).
 
     pass 0 reads p, g, the 1Q indices and scales and (CoState) the previous
     signs/labels/norms/amplitudes and writes p, indices and scales; an fp32-m
     tensor reads and writes exp_avg instead.  CoState adds pass 2 (g, the
     previous encoding, new encoding, ratios) and the selection (ratios, labels).
+    Error feedback adds the fp32 residual to pass 0's reads, and a fifth pass
+    that reads g, the residual and both encodings and writes the residual and
+    the committed encoding (14 + G bytes in all).
     """
     P = G = dtype_bytes
     v = (2.0 + 8.0 / 128) if compress_v else 8.0
     if costate:
-        k1 = 2 * P + G + v + (1.0 / 8 + 7.0 / 128)
-        total = 2 * P + 2 * G + 2.0 + 3.0 / 8 + 37.0 / 128
+        k1 = 2 * P + G + v + (1.0 / 8 + 7.0 / 128) + (4.0 if ef else 0.0)
+        total = 2 * P + 2 * G + 2.0 + 3.0 / 8 + 37.0 / 128 + ((14.0 + G) if ef else 0.0)
     else:
         k1 = 2 * P + G + v + 8.0
         total = k1
@@ -287,7 +292,8 @@ def main():
     step_bytes = 0.0
     for p in params:
         st = opt.state[p]
-        k1, tot = bytes_per_param(dbytes, st["_compress_m"], "compressed_v" in st)
+        ef = st["_compress_m"] and st["m_mgr"]._error_feedback
+        k1, tot = bytes_per_param(dbytes, st["_compress_m"], "compressed_v" in st, ef)
         k1_bytes += k1 * p.numel()
         step_bytes += tot * p.numel()
     k1_gbps = k1_bytes / (k1_avg * 1e-3) / 1e9

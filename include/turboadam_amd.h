@@ -123,7 +123,7 @@ typedef struct TamStepInfo {
   uint32_t n_costate;
   uint32_t total_chunks;   /* alpha-reduction chunks (8192 partial sums each) */
   uint32_t total_slices;   /* selection slices (8192 block ratios each) */
-  uint32_t dtype_mask;     /* bit TAM_DTYPE_x set when a tensor of that dtype is present */
+  uint32_t dtype_mask;     /* bit TAM_DTYPE_x set when a tensor of that dtype without TAM_FLAG_EF is present */
   uint64_t ratio_blocks;   /* sum of nb over CoState tensors */
   uint64_t off_partials;   /* workspace byte offsets */
   uint64_t off_alpha;

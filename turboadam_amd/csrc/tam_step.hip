@@ -2247,7 +2247,7 @@ int tam_prepare(TamTensor* tensors, int n_tensors, TamStepInfo* info) {
     t.nb = (uint32_t)nb;
     t.ntiles = (uint32_t)nt;
     t.tile0 = (uint32_t)tiles;
-    dtype_mask |= 1u << t.dtype;
+    if (!(t.flags & TAM_FLAG_EF)) dtype_mask |= 1u << t.dtype;  // pass 0's per-dtype kernels skip EF tensors
     t.chunk0 = (uint32_t)chunks;
     t.slice0 = (uint32_t)slices;
     t.c_lr = t.neg_lr / t.bias_correction1;  // fp32 division, correctly rounded
