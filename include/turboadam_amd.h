@@ -26,8 +26,9 @@
 extern "C" {
 #endif
 
-#define TAM_ABI_VERSION 7
+#define TAM_ABI_VERSION 8
 #define TAM_BLOCK_SIZE 128 /* elements per quantisation / CoState block */
+#define TAM_TAIL_TILES 4   /* tiles per tail workgroup of an unaligned tensor */
 
 /* error codes */
 #define TAM_OK 0
@@ -114,6 +115,12 @@ typedef struct TamTensor {
                             /*      *found_inf != 0 (a GradScaler skip).  Given */
                             /*      for one descriptor, given for all (the same */
                             /*      pointer): the launches test descriptor 0.   */
+  uint32_t tail0;           /* [derived] first workgroup of this tensor in pass 0's */
+                            /*      kernel for quarters that are not full        */
+  uint32_t tail_wgs;        /* [derived] its workgroups there: 1, or one per    */
+                            /*      TAM_TAIL_TILES tiles when param or grad is  */
+                            /*      not 16-byte aligned (every quarter is then  */
+                            /*      bounds-checked)                             */
 } TamTensor;
 
 /* Launch summary and workspace layout, filled by tam_prepare(). */
@@ -135,6 +142,7 @@ typedef struct TamStepInfo {
   uint32_t n_ef;           /* tensors with error feedback (a fifth pass runs) */
   uint32_t n_device_step;  /* DEVICE_STEP tensors (pass 0 starts with their prologue) */
   uint64_t off_ef_alpha;   /* EF: previous alpha of each tensor (f32 per tensor) */
+  uint32_t tail_blocks;    /* workgroups of pass 0's kernel for quarters that are not full */
 } TamStepInfo;
 
 /* Version of this ABI (TAM_ABI_VERSION). */

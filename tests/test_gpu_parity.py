@@ -189,6 +189,14 @@ def test_unaligned_parameter_views(dt):
     _check(run_side_by_side(sizes, [dt] * 3, steps=4, offset=1, lr=1e-3, weight_decay=0.05))
 
 
+def test_large_unaligned_tensor_spreads_over_workgroups():
+    # 1.2M elements one past a 16-byte boundary: 586 tiles over 147 tail
+    # workgroups (TAM_TAIL_TILES tiles each, the last one partial); a second,
+    # smaller unaligned tensor follows in the tail grid
+    log("large unaligned view")
+    _check(run_side_by_side([1_200_001, 9000], [BF16, BF16], steps=2, offset=1, lr=1e-3, weight_decay=0.05))
+
+
 @pytest.mark.parametrize("bits,pct", [(2, (0.10, 0.90)), (3, (0.05, 0.95)), (6, (0.10, 0.90)), (8, (0.05, 0.95))])
 def test_ragged_multi_tensor_sweep(bits, pct):
     # the ragged-config pattern at a size the oracle finishes in seconds: 120 fp32

@@ -35,7 +35,7 @@ def test_library_exports_every_declared_symbol():
 def test_load_checks_abi_and_struct_layout():
     lib = _lib.load()
     assert lib.tam_abi_version() == _lib.ABI_VERSION
-    assert lib.tam_struct_size(0) == ctypes.sizeof(_lib.TamTensor) == 264
+    assert lib.tam_struct_size(0) == ctypes.sizeof(_lib.TamTensor) == 272
     assert lib.tam_struct_size(1) == ctypes.sizeof(_lib.TamStepInfo)
 
 

@@ -28,7 +28,7 @@ TAM_FLAG_EF = 0x10
 TAM_FLAG_HAS_EF = 0x20
 TAM_FLAG_DEVICE_STEP = 0x40
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 
 class TamTensor(ctypes.Structure):
@@ -79,6 +79,8 @@ class TamTensor(ctypes.Structure):
         ("bc_len", ctypes.c_uint32),
         ("k_abs", ctypes.c_float),
         ("found_inf", ctypes.c_void_p),
+        ("tail0", ctypes.c_uint32),
+        ("tail_wgs", ctypes.c_uint32),
     ]
 
 
@@ -101,6 +103,7 @@ class TamStepInfo(ctypes.Structure):
         ("n_ef", ctypes.c_uint32),
         ("n_device_step", ctypes.c_uint32),
         ("off_ef_alpha", ctypes.c_uint64),
+        ("tail_blocks", ctypes.c_uint32),
     ]
 
 

@@ -1080,20 +1080,41 @@ TAM_K1_FULL_KERNEL(tam_k1_main_f32, TAM_DTYPE_F32, 5)
 
 // The quarters that are not full: the last (at most four) quarters of each
 // tensor, or every quarter of a tensor whose parameter or gradient is not
-// 16-byte aligned.  One workgroup per tensor; wave w takes every fourth quarter.
-__global__ __launch_bounds__(TAM_WG) void tam_k1_tail(const TamTensor* __restrict__ T, uint32_t seed_lo,
+// 16-byte aligned.  An aligned tensor has one workgroup; an unaligned one has
+// one per TAM_TAIL_TILES tiles (tam_prepare: tail0, tail_wgs), so a large
+// unaligned tensor spreads over the GPU.  Wave w takes every fourth quarter of
+// the workgroup's range.
+__device__ __forceinline__ int tam_tail_tensor(const TamTensor* __restrict__ T, int nT, uint32_t wg) {
+  int lo = 0, hi = nT - 1;  // the last tensor whose first tail workgroup is at or before wg
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (T[mid].tail0 <= wg) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
+__global__ __launch_bounds__(TAM_WG) void tam_k1_tail(const TamTensor* __restrict__ T, int nT, uint32_t seed_lo,
                                                       uint32_t seed_hi, double2* __restrict__ partials) {
   if (tam_step_skipped(T)) return;
-  if (T[blockIdx.x].flags & TAM_FLAG_EF) return;  // the whole workgroup: tam_k1_ef covers the tensor
+  const int ti = tam_tail_tensor(T, nT, blockIdx.x);
+  const TamTensor& d = T[ti];
+  if (d.flags & TAM_FLAG_EF) return;  // the whole workgroup: tam_k1_ef covers the tensor
   __shared__ float lut[TAM_WG / 64][4 * 64];
   __shared__ TamLdsTabs tabs;
   tam_lds_tabs_fill(&tabs);
   const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
-  const TamTensor& d = T[blockIdx.x];
   const bool aligned = (((uintptr_t)d.param | (uintptr_t)d.grad) & 15u) == 0;
   const uint32_t nq = d.ntiles * 4u;
-  const uint32_t first = aligned ? (uint32_t)(d.n / (4u * TAM_BLOCK_SIZE)) : 0u;  // full quarters precede
-  for (uint32_t wq = first + wave; wq < nq; wq += 4u) {
+  uint32_t first, last;
+  if (aligned) {  // full quarters precede: tam_k1_main_<dtype> takes them
+    first = (uint32_t)(d.n / (4u * TAM_BLOCK_SIZE));
+    last = nq;
+  } else {
+    const uint32_t local = blockIdx.x - d.tail0;
+    first = local * (4u * TAM_TAIL_TILES);
+    last = first + 4u * TAM_TAIL_TILES < nq ? first + 4u * TAM_TAIL_TILES : nq;
+  }
+  for (uint32_t wq = first + wave; wq < last; wq += 4u) {
     double2* part = partials + (uint64_t)d.tile0 * 4u + wq;
     switch (d.dtype) {
       case TAM_DTYPE_BF16:
@@ -2194,7 +2215,7 @@ const char* tam_last_error(void) { return tam_err_buf; }
 int tam_prepare(TamTensor* tensors, int n_tensors, TamStepInfo* info) {
   tam_err_buf[0] = 0;
   if (!info || n_tensors < 0 || (n_tensors > 0 && !tensors)) return tam_fail(TAM_E_INVALID, "%snull argument", "");
-  uint64_t tiles = 0, ratio_blocks = 0, chunks = 0, slices = 0, ef_bytes = 0;
+  uint64_t tiles = 0, ratio_blocks = 0, chunks = 0, slices = 0, ef_bytes = 0, tail_blocks = 0;
   uint32_t dtype_mask = 0;
   uint32_t ncs = 0, nef = 0, ndev = 0;
   for (int i = 0; i < n_tensors; ++i) {
@@ -2247,6 +2268,10 @@ int tam_prepare(TamTensor* tensors, int n_tensors, TamStepInfo* info) {
     t.nb = (uint32_t)nb;
     t.ntiles = (uint32_t)nt;
     t.tile0 = (uint32_t)tiles;
+    const bool aligned = (((uintptr_t)t.param | (uintptr_t)t.grad) & 15u) == 0;
+    t.tail0 = (uint32_t)tail_blocks;
+    t.tail_wgs = (aligned || (t.flags & TAM_FLAG_EF)) ? 1u : (uint32_t)((nt + TAM_TAIL_TILES - 1) / TAM_TAIL_TILES);
+    tail_blocks += t.tail_wgs;
     if (!(t.flags & TAM_FLAG_EF)) dtype_mask |= 1u << t.dtype;  // pass 0's per-dtype kernels skip EF tensors
     t.chunk0 = (uint32_t)chunks;
     t.slice0 = (uint32_t)slices;
@@ -2260,6 +2285,7 @@ int tam_prepare(TamTensor* tensors, int n_tensors, TamStepInfo* info) {
   }
   memset(info, 0, sizeof(*info));
   info->n_tensors = n_tensors;
+  info->tail_blocks = (uint32_t)tail_blocks;
   info->total_tiles = (uint32_t)tiles;
   info->n_costate = ncs;
   info->total_chunks = (uint32_t)chunks;
@@ -2335,7 +2361,8 @@ static int tam_launch_pass(int pass, const TamTensor* d_tensors, const TamStepIn
                            d_tensors, info->n_tensors, info->total_tiles, (uint32_t)seed, (uint32_t)(seed >> 32),
                            partials);
       TAM_HIP_CHECK(hipGetLastError());
-      hipLaunchKernelGGL(tam_k1_tail, dim3(info->n_tensors), dim3(TAM_WG), 0, s, d_tensors, (uint32_t)seed,
+      hipLaunchKernelGGL(tam_k1_tail, dim3(info->tail_blocks), dim3(TAM_WG), 0, s, d_tensors, info->n_tensors,
+                         (uint32_t)seed,
                          (uint32_t)(seed >> 32), partials);
       break;
     case 1:
