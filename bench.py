@@ -205,14 +205,67 @@ def copy_reference(args):
                       "GBps": nbytes / (ms * 1e-3) / 1e9}), flush=True)
 
 
+# ---------------------------------------------------------------- streaming ceiling
+STREAM_KINDS = {"read": (0, 1), "write": (1, 1), "copy": (2, 2), "2r1w": (3, 3), "inplace": (4, 3)}
+
+
+def stream_reference(args):
+    """Bandwidth of plain streaming kernels (turboadam_amd/csrc/tam_stream.hip):
+    read, write, copy, two reads + one write to a third array, and an in-place
+    read-modify-write of one array with a read of a second (the access shape of
+    the step's parameter update), each with ordinary and with nontemporal loads
+    and stores, over 4 GiB per array.  Prints one JSON line per kernel."""
+    import ctypes
+
+    from turboadam_amd.build import STREAM_LIB_PATH
+
+    lib = ctypes.CDLL(STREAM_LIB_PATH)
+    lib.tam_stream_run.restype = ctypes.c_long
+    lib.tam_stream_run.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                   ctypes.c_uint64, ctypes.c_int, ctypes.c_void_p]
+    dev = torch.device("cuda:0")
+    n16 = 1 << 28  # 16-byte words per array: 4 GiB
+    bufs = [torch.ones(n16 * 4, dtype=torch.int32, device=dev) for _ in range(3)]
+    stream = torch.cuda.current_stream(dev)
+    results = {}
+    for name, (kind, arrays) in STREAM_KINDS.items():
+        for nt in (0, 1):
+            def launch():
+                g = lib.tam_stream_run(kind, nt, bufs[0].data_ptr(), bufs[1].data_ptr(), bufs[2].data_ptr(), n16,
+                                       args.stream_rounds, stream.cuda_stream)
+                if g < 0:
+                    raise RuntimeError(f"tam_stream_run failed ({g})")
+                return g
+            for _ in range(max(1, args.warmup)):
+                grid = launch()
+            torch.cuda.synchronize()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            for _ in range(args.steps):
+                launch()
+            b.record(stream)
+            torch.cuda.synchronize()
+            ms = a.elapsed_time(b) / args.steps
+            nbytes = arrays * n16 * 16
+            gbps = nbytes / (ms * 1e-3) / 1e9
+            results[f"{name}{'_nt' if nt else ''}"] = gbps
+            print(json.dumps({"workload": "stream", "kernel": name, "nontemporal": bool(nt), "grid": grid,
+                              "ms_per_launch": ms, "bytes_per_launch": nbytes, "GBps": gbps,
+                              "frac_of_8TBps": gbps / HBM_PEAK_GBPS}), flush=True)
+    print(json.dumps({"workload": "stream", "summary_GBps": results}), flush=True)
+
+
 # ---------------------------------------------------------------- main
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="c3", choices=sorted(WORKLOADS) + ["copy"])
+    ap.add_argument("--workload", default="c3", choices=sorted(WORKLOADS) + ["copy", "stream"])
     ap.add_argument("--grad-sets", type=int, default=2)
+    ap.add_argument("--pass-steps", type=int, default=5,
+                    help="extra steps after the timed region, issued pass by pass, that time pass 0")
+    ap.add_argument("--stream-rounds", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -225,6 +278,9 @@ def main():
     _lib.load()
     if args.workload == "copy":
         copy_reference(args)
+        return
+    if args.workload == "stream":
+        stream_reference(args)
         return
     shapes_fn, dtype, kw, log_sigma, desc = WORKLOADS[args.workload]
     shapes = shapes_fn()
@@ -260,16 +316,7 @@ def main():
         opt.step()
     torch.cuda.synchronize()
 
-    # timed region: K steps; pass 0 bracketed by events on the launch stream
-    ev = []
-
-    def hook(k, when):
-        if k == 0:
-            e = torch.cuda.Event(enable_timing=True)
-            e.record(torch.cuda.current_stream(dev))
-            ev.append(e)
-
-    opt._pass_hook = hook
+    # timed region: K steps of the production call (one tam_multi_tensor_step per step)
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     # a full collection of the warmup's garbage (tens of ms) would otherwise
     # fire inside the first timed steps, while the GPU waits on an empty queue
@@ -281,9 +328,25 @@ def main():
         opt.step()
     stop.record()
     torch.cuda.synchronize()
-    opt._pass_hook = None
     total_ms = start.elapsed_time(stop)
     ms_step = total_ms / args.steps
+
+    # pass 0 alone: further steps issued pass by pass, pass 0 bracketed by HIP
+    # events recorded on the launch stream (outside the timed region above)
+    ev = []
+
+    def hook(k, when):
+        if k == 0:
+            e = torch.cuda.Event(enable_timing=True)
+            e.record(torch.cuda.current_stream(dev))
+            ev.append(e)
+
+    opt._pass_hook = hook
+    for s in range(max(1, args.pass_steps)):
+        set_grads(args.warmup + args.steps + s)
+        opt.step()
+    torch.cuda.synchronize()
+    opt._pass_hook = None
     k1_ms = [ev[2 * i].elapsed_time(ev[2 * i + 1]) for i in range(len(ev) // 2)]
     k1_avg = float(np.mean(k1_ms))
 
@@ -332,6 +395,7 @@ def main():
             "traffic": measured_traffic(args.workload),
             "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE x2.0 + WRITE_SIZE x1.0)",
             "ms_per_launch": k1_avg,
+            "launches_timed": len(k1_ms),
             "bytes_alg_per_launch": k1_bytes,
         },
     }

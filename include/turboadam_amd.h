@@ -10,11 +10,14 @@
  * Arithmetic contract: results equal, bit for bit, the reference CPU path
  * (davidkny22/turboadam, src/turboadam/{optimizer,costate,quantize}.py) with
  * its library-defined operations fixed as follows: exp/log correctly rounded;
- * dot products and block L2 norms accumulated in fp64 over a balanced pairwise
- * tree (128-element blocks, then blocks zero-padded to a power of two) and
- * rounded to fp32 once; sqrt correctly rounded.  Stochastic-rounding draws come
- * from Philox4x32-10 (counter = (element/4, tensor_id, step, element/2^34),
- * key = seed), word element%4, uniform = (word >> 8) * 2^-24.
+ * dot products and block L2 norms: per 8 consecutive elements an fp32 pairwise
+ * tree of the products with a fused first level (fma(x0, y0, fl(x1*y1))),
+ * widened to fp64, then a balanced fp64 pairwise tree over the 16 partials of
+ * a 128-element block and over the blocks zero-padded to a power of two,
+ * rounded to fp32 once (norms: fp64 sqrt first); sqrt correctly rounded.
+ * Stochastic-rounding draws come from Philox4x32-10 (counter = (element/4,
+ * tensor_id, step, element/2^34), key = seed), word element%4, uniform =
+ * (word >> 8) * 2^-24.
  */
 #ifndef TURBOADAM_AMD_H
 #define TURBOADAM_AMD_H
@@ -210,7 +213,7 @@ int tam_costate_decode(const uint8_t* labels, const uint8_t* signs, const float*
                        float beta1, float one_minus_beta1, float* m_out, void* stream);
 
 /* decompose (reference costate.py:22-43): *alpha (device float) = fl(mg)/fl(gg)
- * with the step's fp64 pairwise dot products (0 when gg == 0), delta =
+ * with the step's dot products (the contract above; 0 when gg == 0), delta =
  * fl(m - fl(alpha*g)).  m, g fp32[n].  Workspace: tam_decompose_workspace(n)
  * bytes of device memory. */
 size_t tam_decompose_workspace(uint64_t n);
@@ -218,7 +221,7 @@ int tam_decompose(const float* m, const float* g, uint64_t n, float* alpha, floa
                   size_t ws_bytes, void* stream);
 
 /* compute_block_ratios (reference costate.py:51-86): ratios[b] =
- * ||delta_b|| / ||m_b|| (fp64 pairwise block norms), 0 where ||m_b|| == 0. */
+ * ||delta_b|| / ||m_b|| (the contract's block norms), 0 where ||m_b|| == 0. */
 int tam_block_ratios(const float* delta, const float* m, uint64_t n, float* ratios, void* stream);
 
 /* compute_thresholds (reference costate.py:94-118): taus[0], taus[1] (device

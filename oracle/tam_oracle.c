@@ -7,9 +7,11 @@
  * "exact mode": the reference's library-defined operations are fixed to
  *   - exp / log: correctly rounded fp32 (evaluated as (float)expl / (float)logl,
  *     64-bit-significand x87 arithmetic),
- *   - dot products and block L2 norms: fp64 accumulation over a balanced
- *     pairwise tree (per 128-element block, then over the blocks zero-padded
- *     to a power of two), rounded to fp32 once,
+ *   - dot products and block L2 norms: per 8 consecutive elements an fp32
+ *     pairwise tree of the products (first level fused, fma(x0, y0,
+ *     fl(x1*y1))), widened to fp64; a balanced fp64 pairwise tree over the 16
+ *     partials of a 128-element block, then over the blocks zero-padded to a
+ *     power of two; rounded to fp32 once (norms: fp64 sqrt, then rounded),
  *   - sqrt: correctly rounded,
  * and every other operation is the fp32 operation torch performs, in the
  * reference's order (fma exactly where torch fuses: Tensor.add_(alpha=) and
@@ -171,23 +173,38 @@ void or_decode_blocks(const uint8_t* labels, const uint8_t* signs, const float* 
   }
 }
 
+/* fp32 partial of the 8 products x[i]*y[i], i in [i0, i0 + 8) (0 past n):
+ * p_k = fma(x_2k, y_2k, fl(x_2k+1 * y_2k+1)), then fl(fl(p0 + p1) + fl(p2 + p3)). */
+static float lane8(const float* x, const float* y, uint64_t n, uint64_t i0) {
+  float a[8], b[8], p[4];
+  for (int k = 0; k < 8; ++k) {
+    uint64_t i = i0 + (uint64_t)k;
+    a[k] = i < n ? x[i] : 0.0f;
+    b[k] = i < n ? y[i] : 0.0f;
+  }
+  for (int k = 0; k < 4; ++k) {
+    float t = a[2 * k + 1] * b[2 * k + 1];
+    p[k] = fmaf(a[2 * k], b[2 * k], t);
+  }
+  float s01 = p[0] + p[1], s23 = p[2] + p[3];
+  return s01 + s23;
+}
+
+/* Sum over block b of x*y: fp64 pairwise over its 16 lane partials. */
+static double block_dot(const float* x, const float* y, uint64_t n, uint64_t b) {
+  double l[OR_BS / 8];
+  for (int j = 0; j < OR_BS / 8; ++j) l[j] = (double)lane8(x, y, n, b * OR_BS + 8u * (uint64_t)j);
+  return pairwise(l, OR_BS / 8);
+}
+
 /* decompose, reference costate.py:22-43. */
 float or_decompose(const float* m, const float* g, uint64_t n, float* delta) {
   uint64_t nb = (n + OR_BS - 1) / OR_BS;
   double* bgg = (double*)malloc(nb * sizeof(double));
   double* bmg = (double*)malloc(nb * sizeof(double));
-  double blk[OR_BS];
   for (uint64_t b = 0; b < nb; ++b) {
-    for (int j = 0; j < OR_BS; ++j) {
-      uint64_t i = b * OR_BS + j;
-      blk[j] = i < n ? (double)g[i] * (double)g[i] : 0.0;
-    }
-    bgg[b] = pairwise(blk, OR_BS);
-    for (int j = 0; j < OR_BS; ++j) {
-      uint64_t i = b * OR_BS + j;
-      blk[j] = i < n ? (double)m[i] * (double)g[i] : 0.0;
-    }
-    bmg[b] = pairwise(blk, OR_BS);
+    bgg[b] = block_dot(g, g, n, b);
+    bmg[b] = block_dot(m, g, n, b);
   }
   float gg = (float)(or_pairwise_sum(bgg, nb) + 0.0);
   float mg = (float)(or_pairwise_sum(bmg, nb) + 0.0);
@@ -201,15 +218,10 @@ float or_decompose(const float* m, const float* g, uint64_t n, float* delta) {
   return alpha;
 }
 
-/* L2 norm of block b of x (zero padded), fp64 pairwise, rounded once. */
+/* L2 norm of block b of x (zero padded): the block's sum of squares as in
+ * block_dot, fp64 sqrt, rounded once. */
 static float block_norm(const float* x, uint64_t n, uint64_t b) {
-  double blk[OR_BS];
-  for (int j = 0; j < OR_BS; ++j) {
-    uint64_t i = b * OR_BS + j;
-    double v = i < n ? (double)x[i] : 0.0;
-    blk[j] = v * v;
-  }
-  return (float)sqrt(pairwise(blk, OR_BS));
+  return (float)sqrt(block_dot(x, x, n, b));
 }
 
 /* compute_block_ratios, reference costate.py:51-86. */

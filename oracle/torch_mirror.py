@@ -10,9 +10,12 @@ counterparts -- the definition the C oracle and the GPU implement:
 
     exp, log         correctly rounded (64-bit-significand evaluation, one rounding)
     sqrt             correctly rounded (IEEE fp32)
-    dot (alpha)      fp64 products, balanced pairwise tree per 128-element block,
-                     then over the blocks zero-padded to a power of two, rounded once
-    block L2 norms   fp64 squares, balanced pairwise tree per block, fp64 sqrt, rounded once
+    dot (alpha)      per 8 consecutive elements an fp32 pairwise tree of the
+                     products (first level fused: fma(x0, y0, fl(x1*y1))),
+                     widened to fp64; balanced fp64 pairwise tree over the 16
+                     of a 128-element block, then over the blocks zero-padded
+                     to a power of two, rounded once
+    block L2 norms   the same per-block sums of squares, fp64 sqrt, rounded once
 
 It also serves as the timed CPU baseline (faithful mode = the reference's
 own CPU cost) and drives the per-step tie analysis of tests/test_golden.py.
@@ -70,6 +73,40 @@ def _pairwise_pad(x: np.ndarray) -> float:
     return float(_pairwise_rows(buf.reshape(1, P))[0])
 
 
+def _fma32(a: np.ndarray, b: np.ndarray, c: np.ndarray) -> np.ndarray:
+    """fl32(a*b + c) of fp32 arrays with a single rounding (an fp32 fma).
+
+    a*b is exact in fp64; TwoSum gives p + c = s + e exactly; s rounds to fp32
+    once, except where s is an fp32 midpoint and e != 0, where e decides."""
+    p = a.astype(np.float64) * b.astype(np.float64)
+    c64 = c.astype(np.float64)
+    s = p + c64
+    bb = s - p
+    e = (p - (s - bb)) + (c64 - bb)
+    r = s.astype(np.float32)
+    up = np.nextafter(r, np.float32(np.inf))
+    dn = np.nextafter(r, np.float32(-np.inf))
+    nxt = np.where(e > 0, up, dn)
+    mid = (r.astype(np.float64) + nxt.astype(np.float64)) * 0.5
+    fix = (e != 0) & (s == mid)
+    return np.where(fix, nxt, r)
+
+
+def _lane_partials(x: np.ndarray, y: np.ndarray) -> np.ndarray:
+    """fp32 partials of 8 consecutive products (x, y: fp32 (rows, 8)):
+    p_k = fma(x_2k, y_2k, fl(x_2k+1 * y_2k+1)), then (p0 + p1) + (p2 + p3)."""
+    p = [_fma32(x[:, 2 * k], y[:, 2 * k], x[:, 2 * k + 1] * y[:, 2 * k + 1]) for k in range(4)]
+    return (p[0] + p[1]) + (p[2] + p[3])
+
+
+def _block_sums(x: np.ndarray, y: np.ndarray) -> np.ndarray:
+    """Per 128-element block of fp32 (nb, 128) arrays: fp64 pairwise sum of the
+    16 lane partials."""
+    nb = x.shape[0]
+    lanes = _lane_partials(x.reshape(nb * 16, 8), y.reshape(nb * 16, 8)).astype(np.float64)
+    return _pairwise_rows(lanes.reshape(nb, 16))
+
+
 class ExactOps:
     name = "exact"
 
@@ -92,15 +129,17 @@ class ExactOps:
     def dot(a, b):
         n = a.numel()
         nb = (n + BS - 1) // BS
-        prod = np.zeros(nb * BS)
-        prod[:n] = a.numpy().astype(np.float64) * b.numpy().astype(np.float64)
-        blocks = _pairwise_rows(prod.reshape(nb, BS))
+        x = np.zeros(nb * BS, np.float32)
+        y = np.zeros(nb * BS, np.float32)
+        x[:n] = a.numpy()
+        y[:n] = b.numpy()
+        blocks = _block_sums(x.reshape(nb, BS), y.reshape(nb, BS))
         return torch.tensor(np.float32(_pairwise_pad(blocks) + 0.0))
 
     @staticmethod
     def row_norms(x2d):
-        sq = x2d.numpy().astype(np.float64) ** 2
-        return torch.from_numpy(np.sqrt(_pairwise_rows(sq)).astype(np.float32))
+        x = np.ascontiguousarray(x2d.numpy(), dtype=np.float32)
+        return torch.from_numpy(np.sqrt(_block_sums(x, x)).astype(np.float32))
 
 
 # ---------------------------------------------------------------- helpers

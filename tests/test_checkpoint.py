@@ -86,3 +86,27 @@ def test_state_dict_carries_the_philox_seed():
     opt = TurboAdam(ps)
     opt.load_state_dict(sd)
     assert opt.philox_seed == 12345
+
+
+def test_load_state_dict_keeps_fp32_moments_of_16bit_parameters():
+    """torch's loader casts state tensors to the parameter dtype; the fp32
+    exp_avg / exp_avg_sq of a bf16 parameter must come back unrounded."""
+    from turboadam_amd import TurboAdam
+
+    ps = [torch.nn.Parameter(torch.zeros(300, dtype=torch.bfloat16)),
+          torch.nn.Parameter(torch.zeros(20, 10, dtype=torch.float16))]
+    fine = torch.full((300,), 1.0 + 2.0 ** -20, dtype=torch.float32)
+    sd = {"state": {0: {"step": 3, "_compress_m": False, "exp_avg": fine.clone(), "exp_avg_sq": fine * 2.0},
+                    1: {"step": 3, "_compress_m": False, "exp_avg": fine[:200].reshape(20, 10) * 3.0,
+                        "exp_avg_sq": fine[:200].reshape(20, 10) * 4.0}},
+          "param_groups": [{**TurboAdam(ps).param_groups[0], "params": [0, 1], "compress_v": False}]}
+    opt = TurboAdam([{"params": ps, "compress_v": False}])
+    opt.load_state_dict(sd)
+    for p, scale in zip(ps, (1.0, 3.0)):
+        st = opt.state[p]
+        for key, k in (("exp_avg", scale), ("exp_avg_sq", 2.0 if scale == 1.0 else 4.0)):
+            t = st[key]
+            assert t.dtype == torch.float32 and t.shape == p.shape
+            want = (fine[: p.numel()] * k).reshape(p.shape)
+            assert torch.equal(t, want), key
+        assert st["step"] == 3

@@ -174,6 +174,8 @@ def test_exact_and_faithful_differ_only_by_ties(name):
             total[k] = max(total.get(k, 0), v) if isinstance(v, float) else total.get(k, 0) + v
         opt.step(_step_grads(case, sig, s, shapes))
     print(name, json.dumps(total))
+    # alpha within 1e-6 relative of the reference's (MKL sdot) every step
+    assert total["alpha_rel"] <= 1e-6
     # parameters move by at most a few ulps per step (sqrt and division inputs agree to the last bit or two)
     assert total["param_rel"] <= 1e-6
 

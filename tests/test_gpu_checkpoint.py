@@ -75,8 +75,11 @@ def test_state_dict_round_trip_resumes_bit_identically():
     from turboadam_amd import TurboAdam
     from turboadam_amd.costate import CoStateManager
 
-    sizes, dts = [70_000, 5000, 300], [BF16, BF16, F32]
-    shapes = [(70_000,), (50, 100), (300,)]
+    # a bf16 tensor below min_m_compress_elements (fp32 exp_avg) and a
+    # compress_v=False group (fp32 exp_avg_sq of a bf16 tensor): torch's loader
+    # would round those fp32 moments to bf16
+    sizes, dts = [70_000, 5000, 300, 300, 6000], [BF16, BF16, F32, BF16, BF16]
+    shapes = [(70_000,), (50, 100), (300,), (300,), (60, 100)]
     rng = np.random.default_rng(22)
     init = [to_bits((rng.standard_normal(n) * 0.02).astype(np.float32), dt) for n, dt in zip(sizes, dts)]
     grads = _grads(rng, sizes, dts, 5)
@@ -92,17 +95,20 @@ def test_state_dict_round_trip_resumes_bit_identically():
             opt.step()
         torch.cuda.synchronize()
 
+    def groups(params):
+        return [{"params": params[:4]}, {"params": params[4:], "compress_v": False}]
+
     pa = make()
-    oa = TurboAdam(pa, philox_seed=31337, **KW)
+    oa = TurboAdam(groups(pa), philox_seed=31337, **KW)
     run(oa, pa, range(5))
     pb = make()
-    ob = TurboAdam(pb, philox_seed=31337, **KW)
+    ob = TurboAdam(groups(pb), philox_seed=31337, **KW)
     run(ob, pb, range(3))
     buf = io.BytesIO()
     torch.save(ob.state_dict(), buf)
     buf.seek(0)
     log("resume after 3 steps from torch.save(state_dict())")
-    oc = TurboAdam(pb, **KW)  # default seed: the checkpoint restores 31337
+    oc = TurboAdam(groups(pb), **KW)  # default seed: the checkpoint restores 31337
     with torch.serialization.safe_globals([CoStateManager]):
         oc.load_state_dict(torch.load(buf, weights_only=True))
     assert oc.philox_seed == 31337

@@ -139,6 +139,92 @@ def _f32(a):
     return np.ascontiguousarray(a, dtype=np.float32)
 
 
+def _round_f32_q(q: Fraction) -> float:
+    """The fp32 value nearest the rational q (ties to even), by integer arithmetic."""
+    if q == 0:
+        return 0.0
+    a = abs(q)
+    e = a.numerator.bit_length() - a.denominator.bit_length()  # 2^e <= a < 2^(e+2)
+    if Fraction(2) ** (e + 1) <= a:
+        e += 1
+    quantum = Fraction(2) ** (max(e, -126) - 23)
+    n, r = divmod(a, quantum)
+    n = int(n)
+    if r > quantum / 2 or (r == quantum / 2 and n % 2 == 1):
+        n += 1
+    v = float(n * quantum)
+    return -v if q < 0 else v
+
+
+def _contract_lane(xs, ys) -> float:
+    """The reduction contract's fp32 partial of 8 products, in exact rational
+    arithmetic rounded to fp32 after each operation: p_k = fma(x_2k, y_2k,
+    fl(x_2k+1 y_2k+1)), then (p0 + p1) + (p2 + p3)."""
+    F = Fraction
+    p = []
+    for k in range(4):
+        t = _round_f32_q(F(float(xs[2 * k + 1])) * F(float(ys[2 * k + 1])))
+        p.append(_round_f32_q(F(float(xs[2 * k])) * F(float(ys[2 * k])) + F(t)))
+    return _round_f32_q(F(_round_f32_q(F(p[0]) + F(p[1]))) + F(_round_f32_q(F(p[2]) + F(p[3]))))
+
+
+def _pair(v):
+    return v[0] if len(v) == 1 else _pair(v[: len(v) // 2]) + _pair(v[len(v) // 2:])
+
+
+def _contract_blocks(x, y):
+    """Per 128-element block (zero padded): fp64 pairwise sum of the 16 lane partials."""
+    n = x.size
+    nb = (n + 127) // 128
+    xp = np.zeros(nb * 128, np.float32); xp[:n] = x
+    yp = np.zeros(nb * 128, np.float32); yp[:n] = y
+    return [_pair([_contract_lane(xp[i:i + 8], yp[i:i + 8]) for i in range(b * 128, b * 128 + 128, 8)])
+            for b in range(nb)]
+
+
+def test_dot_and_norm_contract_against_a_rational_restatement():
+    """alpha and block norms of the C oracle equal, bit for bit, the reduction
+    contract evaluated in exact rational arithmetic with explicit fp32 rounding
+    (an implementation that shares nothing with the oracle's fmaf / double
+    code), including products that land exactly on an fp32 rounding midpoint
+    where only the fused first level gives the right result."""
+    rng = np.random.default_rng(41)
+    # (1 + 2^-12)^2 = 1 + 2^-11 + 2^-24: an fp32 midpoint; the tiny second
+    # product decides its rounding inside the fma
+    mid = np.float32(1 + 2.0 ** -12)
+    cases = []
+    for n in (8, 128, 300, 1000):
+        m = _f32(rng.standard_normal(n) * 10.0 ** rng.integers(-3, 3, n))
+        g = _f32(rng.standard_normal(n) * 10.0 ** rng.integers(-3, 3, n))
+        cases.append((m, g))
+    m = _f32(np.tile([mid, 1e-20, mid, -1e-20, mid, 0.0, -mid, 1e-30], 32))
+    g = _f32(np.tile([mid, 1e-20, mid, 1e-20, mid, 0.0, mid, 1e-30], 32))
+    cases.append((m, g))
+    tie = _f32(np.tile([mid, 1e-20, 0, 0, 0, 0, 0, 0], 16))
+    cases.append((tie, tie))
+    for m, g in cases:
+        n = m.size
+        gg = _pair(_contract_blocks(g, g) + [0.0] * ((1 << max(0, ((n + 127) // 128 - 1).bit_length())) - (n + 127) // 128))
+        mg = _pair(_contract_blocks(m, g) + [0.0] * ((1 << max(0, ((n + 127) // 128 - 1).bit_length())) - (n + 127) // 128))
+        gg32, mg32 = np.float32(gg + 0.0), np.float32(mg + 0.0)
+        want = mg32 / gg32 if gg32 > 0 else np.float32(0.0)
+        d = np.empty_like(m)
+        got = np.float32(L.or_decompose(P(m), P(g), n, P(d)))
+        assert got.view(np.uint32) == np.float32(want).view(np.uint32), (n, got, want)
+        # block norms: fp64 sqrt of the block sum of squares, rounded once
+        nrm = np.zeros((n + 127) // 128, np.float32)
+        signs = np.zeros((n + 7) // 8, np.uint8)
+        amp = np.zeros(nrm.size, np.uint16)
+        L.or_encode(P(m), n, ctypes.c_float(np.float32(math.sqrt(128))), P(signs), P(nrm), P(amp))
+        want_n = _f32([math.sqrt(b) for b in _contract_blocks(m, m)])
+        assert np.array_equal(nrm.view(np.uint32), want_n.view(np.uint32))
+    # the last case exercises the fused first level: fl(mid^2) alone rounds
+    # the midpoint to even (down), the fma with the tiny second product rounds up
+    assert _contract_lane(tie[:8], tie[:8]) == 1 + 2.0 ** -11 + 2.0 ** -23
+    assert float(np.float32(np.float32(mid * mid) + np.float32(np.float32(1e-20) * np.float32(1e-20)))) == \
+        1 + 2.0 ** -11
+
+
 def test_decompose_closed_forms():
     rng = np.random.default_rng(5)
     g = _f32(rng.standard_normal(256))

@@ -17,6 +17,9 @@ REPO_DIR = os.path.dirname(PKG_DIR)
 BUILD_DIR = os.path.join(PKG_DIR, "_build")
 LIB_PATH = os.path.join(BUILD_DIR, "libturboadam_amd.so")
 SOURCES = [os.path.join(PKG_DIR, "csrc", "tam_step.hip")]
+# streaming kernels that bench.py times as the bandwidth ceiling (not part of the library's ABI)
+STREAM_LIB_PATH = os.path.join(BUILD_DIR, "libtam_stream.so")
+STREAM_SOURCES = [os.path.join(PKG_DIR, "csrc", "tam_stream.hip")]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
@@ -32,17 +35,23 @@ HIP_FLAGS = [
 ]
 
 
-def build_library(verbose: bool = False) -> str:
+def _hipcc(sources, out: str, verbose: bool) -> str:
     os.makedirs(BUILD_DIR, exist_ok=True)
-    tmp = LIB_PATH + ".tmp"
-    cmd = [HIPCC, *HIP_FLAGS, "-o", tmp, *SOURCES]
+    tmp = out + ".tmp"
+    cmd = [HIPCC, *HIP_FLAGS, "-o", tmp, *sources]
     if verbose:
         print(" ".join(cmd))
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stderr}")
-    os.replace(tmp, LIB_PATH)
-    return LIB_PATH
+    os.replace(tmp, out)
+    return out
+
+
+def build_library(verbose: bool = False) -> str:
+    """The optimizer library and the streaming-kernel library bench.py uses."""
+    _hipcc(STREAM_SOURCES, STREAM_LIB_PATH, verbose)
+    return _hipcc(SOURCES, LIB_PATH, verbose)
 
 
 if __name__ == "__main__":

@@ -7,8 +7,9 @@ norm (fp32), an fp16 amplitude scale and one sign bit per element (MSB first).
 TurboAdam.step runs the whole update fused in its multi-tensor launches.
 The reference's public functions are also available one tensor at a time,
 with the same names and argument meaning, on the gfx950 kernels (the
-step's arithmetic: fp64 pairwise dot products and block norms, exact
-radix selection).  Inputs must be on an MI355X (HIP) device.
+step's arithmetic: fp32 lane partials and fp64 pairwise sums for the dot
+products and block norms, exact radix selection).  Inputs must be on an
+MI355X (HIP) device.
 """
 
 import torch
@@ -132,10 +133,16 @@ def _decode(encoded: dict, alpha, g: torch.Tensor, n: int, has_state: bool, ema:
     if gf.dtype not in _lib.DTYPES:
         gf = gf.float()
     gf = gf.contiguous()
+    if n != gf.numel():
+        raise ValueError(f"decode_blocks: original_numel {n} does not match the gradient's {gf.numel()} elements")
     out = torch.empty(n, dtype=torch.float32, device=dev)
     ptrs = [0, 0, 0, 0, 0]
     keep = []
     if has_state:
+        nb = num_blocks(n)
+        if (encoded["labels"].numel() != nb or encoded["block_norms"].numel() != nb
+                or encoded["scales"].numel() != nb or encoded["sign_packed"].numel() < (n + 7) // 8):
+            raise ValueError(f"decode_blocks: the encoding does not cover {n} elements ({nb} blocks)")
         labels = encoded["labels"].to(device=dev, dtype=torch.uint8).contiguous()
         signs = encoded["sign_packed"].to(device=dev, dtype=torch.uint8).contiguous()
         norms = encoded["block_norms"].to(device=dev, dtype=torch.float32).contiguous()

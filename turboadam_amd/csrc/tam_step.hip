@@ -17,8 +17,8 @@
 //           present) and tam_k1_tail (the other quarters): CoState decode + EMA
 //           (or fp32 exp_avg EMA), 1Q decode + EMA + stochastic
 //           re-quantisation (or fp32 exp_avg_sq), denominator, decoupled
-//           weight decay, parameter update; per-quarter-tile fp64 partials of
-//           g.g and m.g.
+//           weight decay, parameter update; per-quarter-tile partials of
+//           g.g and m.g (fp32 per lane, fp64 across lanes and blocks).
 //   pass 1  tam_k_alpha_chunks, tam_k_alpha: alpha = m.g / g.g per CoState
 //           tensor (pairwise trees over the partials).
 //   pass 2  tam_k2_encode: CoState tiles: recompute m, delta = m - alpha*g,
@@ -226,12 +226,17 @@ __device__ __forceinline__ double tam_readlane_d(double v, int l) {
 __device__ __forceinline__ double tam_pair8(const double* x) {
   return ((x[0] + x[1]) + (x[2] + x[3])) + ((x[4] + x[5]) + (x[6] + x[7]));
 }
-// The same sum of the products a[i]*b[i] of fp32 values: each product is exact
-// in fp64, so the first level fl(a0*b0 + a1*b1) is one fma (zero signs
-// included, as fma and the sum follow the same rule for an exact zero).
-__device__ __forceinline__ double tam_pair8_dot(const double* a, const double* b) {
-  return (__builtin_fma(a[0], b[0], a[1] * b[1]) + __builtin_fma(a[2], b[2], a[3] * b[3])) +
-         (__builtin_fma(a[4], b[4], a[5] * b[5]) + __builtin_fma(a[6], b[6], a[7] * b[7]));
+// A lane's partial of a dot product or sum of squares (the reduction contract
+// of the alpha dots and the block norms): the 8 products a[i]*b[i] of fp32
+// values in an fp32 pairwise tree whose first level is fused,
+// p_k = fma(a_2k, b_2k, fl(a_2k+1 * b_2k+1)), then fl(fl(p0 + p1) + fl(p2 + p3)).
+// The callers widen it to fp64 for the sums across lanes and blocks.
+__device__ __forceinline__ float tam_lane_dot(const float* a, const float* b) {
+  const float p0 = __builtin_fmaf(a[0], b[0], a[1] * b[1]);
+  const float p1 = __builtin_fmaf(a[2], b[2], a[3] * b[3]);
+  const float p2 = __builtin_fmaf(a[4], b[4], a[5] * b[5]);
+  const float p3 = __builtin_fmaf(a[6], b[6], a[7] * b[7]);
+  return (p0 + p1) + (p2 + p3);
 }
 
 // Sum over the 16 lanes of a block with adjacent pairing.  After the two quad
@@ -987,16 +992,17 @@ __device__ __forceinline__ void tam_k1_quarter(const TamTensor& d, uint32_t wq, 
     } else if (FULL || W.bvalid) {
       tam_costate_m<FULL>(d, W, cs, alpha_prev, g, g, m);
     }
-    double gd[TAM_EPL], md[TAM_EPL];
+    float gz[TAM_EPL], mz[TAM_EPL];
 #pragma unroll
     for (int i = 0; i < TAM_EPL; ++i) {
       const bool ok = FULL || (W.bvalid && (uint32_t)i < W.nv);
-      gd[i] = ok ? (double)g[i] : 0.0;
-      md[i] = ok ? (double)m[i] : 0.0;
+      gz[i] = ok ? g[i] : 0.0f;
+      mz[i] = ok ? m[i] : 0.0f;
     }
-    // per block, then the wave's 4 blocks (block k in lanes 16k..16k+15):
-    // adjacent pairs, then the two pairs; lane 12 stores g.g, lane 13 m.g
-    const double t = tam_quarter_sum2(tam_pair8_dot(gd, gd), tam_pair8_dot(md, gd), lane);
+    // lane partials in fp32, then in fp64 per block and over the wave's 4
+    // blocks (block k in lanes 16k..16k+15): adjacent pairs, then the two
+    // pairs; lane 12 stores g.g, lane 13 m.g
+    const double t = tam_quarter_sum2((double)tam_lane_dot(gz, gz), (double)tam_lane_dot(mz, gz), lane);
     if (lane - 12u < 2u) tam_g((double*)part)[lane - 12u] = t;
   } else if (FULL || W.bvalid) {
     // fp32 exp_avg (optimizer.py:113): m = fma(1-b1, g, fl(m*b1))
@@ -1317,7 +1323,7 @@ __device__ __forceinline__ void tam_k2_quarter(const TamTensor& d, uint32_t wq, 
                                                const TamK2In* pre = nullptr) {
   const TamWave W = tam_wave(d, wq, lane, FULL);
   const bool ef = (d.flags & TAM_FLAG_EF) != 0;  // uniform
-  double dl[TAM_EPL], md[TAM_EPL];
+  float dl[TAM_EPL], md[TAM_EPL];
   uint32_t sbyte = 0;
   if (FULL || W.bvalid) {
     float g[TAM_EPL], ge[TAM_EPL], m[TAM_EPL];
@@ -1344,20 +1350,22 @@ __device__ __forceinline__ void tam_k2_quarter(const TamTensor& d, uint32_t wq, 
     for (int i = 0; i < TAM_EPL; ++i) {
       const bool ok = FULL || (uint32_t)i < W.nv;
       const float delta = ok ? m[i] - a * g[i] : 0.0f;  // costate.py:42
-      dl[i] = (double)delta;
-      md[i] = ok ? (double)m[i] : 0.0;
+      dl[i] = delta;
+      md[i] = ok ? m[i] : 0.0f;
       sbyte = 2u * sbyte + (delta < 0.0f ? 1u : 0u);  // element 8j+i is bit 7-i, costate.py:170-181
     }
   } else {
 #pragma unroll
-    for (int i = 0; i < TAM_EPL; ++i) dl[i] = md[i] = 0.0;
+    for (int i = 0; i < TAM_EPL; ++i) dl[i] = md[i] = 0.0f;
   }
-  // Block sums of squares with the tree of tam_block_sum: the sum of delta^2 in
-  // lane 12 of the block's row, of m^2 in lane 13.  Each lane of a pair evaluates one square
-  // root and one division: lane 12 the residual norm and the amplitude, lane 13
-  // the norm of m and the ratio.
+  // Block sums of squares: fp32 lane partials, then the fp64 tree of
+  // tam_block_sum: the sum of delta^2 in lane 12 of the block's row, of m^2 in
+  // lane 13.  Each lane of a pair evaluates one square root and one division:
+  // lane 12 the residual norm and the amplitude, lane 13 the norm of m and the
+  // ratio.
   const bool odd = (W.l16 & 1u) != 0;
-  const float nx = (float)__builtin_sqrt(tam_row_sum2(tam_pair8_dot(dl, dl), tam_pair8_dot(md, md), odd));
+  const float nx =
+      (float)__builtin_sqrt(tam_row_sum2((double)tam_lane_dot(dl, dl), (double)tam_lane_dot(md, md), odd));
   const float ny = tam_dppf<TAM_DPP_XOR1>(nx);
   const float nd = odd ? ny : nx;  // costate.py:241
   const float nm = odd ? nx : ny;
@@ -1900,17 +1908,10 @@ __global__ __launch_bounds__(TAM_WG) void tam_k_dot_quarters(const float* __rest
   const uint32_t wq = blockIdx.x * 4u + wave;
   const TamWave W = tam_wave(d, wq, lane, false);
   float mv[TAM_EPL], gv[TAM_EPL];
-  tam_ld8<TAM_DTYPE_F32, false>(m, W.e0, W.nv, mv);
+  tam_ld8<TAM_DTYPE_F32, false>(m, W.e0, W.nv, mv);  // elements past n read 0
   tam_ld8<TAM_DTYPE_F32, false>(g, W.e0, W.nv, gv);
-  double gg[TAM_EPL], mg[TAM_EPL];
-#pragma unroll
-  for (int i = 0; i < TAM_EPL; ++i) {
-    const bool ok = (uint32_t)i < W.nv;
-    gg[i] = ok ? (double)gv[i] * (double)gv[i] : 0.0;
-    mg[i] = ok ? (double)mv[i] * (double)gv[i] : 0.0;
-  }
-  const double sgg = tam_block_sum(tam_pair8(gg));
-  const double smg = tam_block_sum(tam_pair8(mg));
+  const double sgg = tam_block_sum((double)tam_lane_dot(gv, gv));
+  const double smg = tam_block_sum((double)tam_lane_dot(mv, gv));
   const double tgg = (tam_readlane_d(sgg, 0) + tam_readlane_d(sgg, 16)) +
                      (tam_readlane_d(sgg, 32) + tam_readlane_d(sgg, 48));
   const double tmg = (tam_readlane_d(smg, 0) + tam_readlane_d(smg, 16)) +
@@ -1937,14 +1938,12 @@ __global__ void tam_k_delta(const float* __restrict__ m, const float* __restrict
   delta[i] = m[i] - a * g[i];
 }
 
-// Per-block fp64 norm of x (zero padded) in all 16 lanes of the block.
+// Per-block sum of squares of x (zero padded; fp32 lane partials, fp64
+// across the block) in all 16 lanes of the block.
 __device__ __forceinline__ double tam_block_sq(const float* x, const TamWave& W) {
   float v[TAM_EPL];
   tam_ld8<TAM_DTYPE_F32, false>(x, W.e0, W.nv, v);
-  double q[TAM_EPL];
-#pragma unroll
-  for (int i = 0; i < TAM_EPL; ++i) q[i] = (double)v[i] * (double)v[i];
-  return tam_block_sum(tam_pair8(q));
+  return tam_block_sum((double)tam_lane_dot(v, v));
 }
 
 // compute_block_ratios (costate.py:51-86): r = ||delta_b|| / ||m_b||, 0 where ||m_b|| = 0
@@ -1967,14 +1966,11 @@ __global__ __launch_bounds__(TAM_WG) void tam_k_encode(const float* __restrict__
   const TamWave W = tam_wave(d, blockIdx.x * 4u + (threadIdx.x >> 6), threadIdx.x & 63u, false);
   float v[TAM_EPL];
   tam_ld8<TAM_DTYPE_F32, false>(delta, W.e0, W.nv, v);
-  double q[TAM_EPL];
   uint32_t sbyte = 0;
 #pragma unroll
-  for (int i = 0; i < TAM_EPL; ++i) {
-    q[i] = (double)v[i] * (double)v[i];
+  for (int i = 0; i < TAM_EPL; ++i)
     sbyte |= (((uint32_t)i < W.nv && v[i] < 0.0f) ? 1u : 0u) << (7 - i);  // costate.py:170-181
-  }
-  const double sd = tam_block_sum(tam_pair8(q));
+  const double sd = tam_block_sum((double)tam_lane_dot(v, v));
   if (!W.bvalid) return;
   if (W.nv > 0) signs[W.e0 >> 3] = (uint8_t)sbyte;
   if (W.l16 == 0) {

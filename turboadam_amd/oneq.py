@@ -9,7 +9,7 @@ State dict layout (reference src/turboadam/oneq.py:41-48):
 import torch
 
 from . import _lib
-from .quantize import DEFAULT_SEED, quantize_logscale_nbits
+from .quantize import DEFAULT_SEED, _dequantize_operands, quantize_logscale_nbits
 from .utils import BLOCK_SIZE, num_blocks, pad_to_blocks
 
 # TurboAdam starts v from full(1e-30) quantised deterministically
@@ -66,10 +66,8 @@ def decompress_v(compressed: dict) -> torch.Tensor:
         raise RuntimeError("turboadam_amd.decompress_v: state must be on an MI355X (HIP) device")
     if compressed["block_size"] != BLOCK_SIZE:
         raise NotImplementedError("turboadam_amd supports block_size=128 only")
-    n = compressed["original_length"]
     lib = _lib.load()
-    idx = idx.to(torch.uint8).contiguous()
-    scales = scales.to(torch.float16).contiguous()
+    idx, scales, n = _dequantize_operands(idx, scales, BLOCK_SIZE, compressed["original_length"])
     out = torch.empty(n, dtype=torch.float32, device=idx.device)
     with torch.cuda.device(idx.device):
         rc = lib.tam_v_dequantize(idx.data_ptr(), scales.data_ptr(), n, compressed["n_bits"], out.data_ptr(),

@@ -62,8 +62,16 @@ class _DeviceBuffers:
         self.ws = None
         self.pinned = None
         self.pinned_bytes = b""
-        self.skip = None
         self.stream = None  # the stream of the last step that used these buffers
+        self.captured = False  # a captured graph replays the descriptor upload from these buffers
+
+    def fits(self, desc_bytes: int, ws_bytes: int, raw) -> bool:
+        """Whether a step can run on these buffers without reallocating them or
+        rewriting the pinned bytes a captured graph re-uploads (raw: the
+        static descriptor bytes of a capturable step, or None)."""
+        if self.desc is None or self.desc.numel() < desc_bytes or self.ws is None or self.ws.numel() < ws_bytes:
+            return False
+        return raw is None or raw == self.pinned_bytes
 
     def order_on(self, stream) -> None:
         """The buffers are reused from step to step, not reallocated: a step on
@@ -73,14 +81,6 @@ class _DeviceBuffers:
         if self.stream is not None and self.stream != stream and not torch.cuda.is_current_stream_capturing():
             stream.wait_stream(self.stream)
         self.stream = stream
-
-    def skip_flag(self, found_inf: torch.Tensor) -> torch.Tensor:
-        """A persistent copy of GradScaler's found_inf (its tensor is new every
-        step; the descriptors of a captured step keep one address)."""
-        if self.skip is None:
-            self.skip = torch.zeros(1, dtype=torch.float32, device=self.device)
-        self.skip.copy_(found_inf.reshape(1))
-        return self.skip
 
     def upload_static(self, raw: bytes) -> torch.Tensor:
         """Pinned host copy of `raw` that a captured graph re-reads on every
@@ -166,6 +166,8 @@ class TurboAdam(Optimizer):
             raise ValueError(f"philox_seed must be a 64-bit unsigned integer, got {philox_seed}")
         self.philox_seed = int(philox_seed)
         self._buffers = {}
+        self._retired_buffers = []  # buffers a captured graph still replays
+        self._skip_flags = {}
         self._bc_values = {}
         self._bc_tables = {}
         # Optional callable(pass_index, "begin"|"end") run around each of the four
@@ -266,6 +268,7 @@ class TurboAdam(Optimizer):
     # state dict (reference optimizer.py:194-218)
     # ------------------------------------------------------------------
     _PACKED_V = {"indices": torch.uint8, "scales": torch.float16}
+    _FP32_STATE = ("exp_avg", "exp_avg_sq")
 
     def state_dict(self):
         """torch's optimizer state dict plus the Philox key ("philox_seed"), so
@@ -310,24 +313,26 @@ class TurboAdam(Optimizer):
         if "philox_seed" in state_dict:
             state_dict = dict(state_dict)
             self.philox_seed = int(state_dict.pop("philox_seed"))
-        saved_v = {}
+        saved_v, saved_fp32 = {}, {}
         for pid, st in state_dict.get("state", {}).items():
-            cv = st.get("compressed_v") if isinstance(st, dict) else None
+            if not isinstance(st, dict):
+                continue
+            cv = st.get("compressed_v")
             if isinstance(cv, dict):
                 saved_v[pid] = {k: cv[k] for k in self._PACKED_V if isinstance(cv.get(k), torch.Tensor)}
+            # fp32 moments of a 16-bit parameter: torch's loader would round them to its dtype
+            saved_fp32[pid] = {k: st[k] for k in self._FP32_STATE if isinstance(st.get(k), torch.Tensor)}
+        # saved ids pair with the parameters in order, as torch's loader pairs them
+        saved_ids = [i for g in state_dict.get("param_groups", []) for i in g["params"]]
         super().load_state_dict(state_dict)
-        id_to_param = {}
-        idx = 0
-        for group in self.param_groups:
-            for p in group["params"]:
-                id_to_param[idx] = p
-                idx += 1
+        param_to_id = {id(p): i for i, p in zip(saved_ids, (p for g in self.param_groups for p in g["params"]))}
         for group_idx, group in enumerate(self.param_groups):
             for p in group["params"]:
                 if p not in self.state:
                     continue
                 state = self.state[p]
                 device = p.device
+                pid = param_to_id.get(id(p))
                 step = state.get("step", 0)
                 if group.get("capturable"):  # torch's loader makes it f32 on the device
                     state["step"] = torch.as_tensor(step).to(device=device, dtype=torch.int32).reshape(()).clone()
@@ -336,7 +341,6 @@ class TurboAdam(Optimizer):
                 cv = state.get("compressed_v")
                 if isinstance(cv, dict):
                     cv.pop("rand_buf", None)
-                    pid = next((k for k, v in id_to_param.items() if v is p), None)
                     for k, dt in self._PACKED_V.items():
                         src = saved_v.get(pid, {}).get(k, cv.get(k))
                         if isinstance(src, torch.Tensor):
@@ -359,9 +363,11 @@ class TurboAdam(Optimizer):
                     if mgr._ef_residual is not None:
                         mgr._ef_residual = mgr._ef_residual.to(device=device, dtype=torch.float32).clone() \
                             .contiguous().reshape(p.shape)
-                for key in ("exp_avg", "exp_avg_sq"):
+                for key in self._FP32_STATE:
                     if key in state:
-                        state[key] = state[key].to(device=device, dtype=torch.float32).clone()
+                        src = saved_fp32.get(pid, {}).get(key, state[key])
+                        state[key] = src.to(device=device, dtype=torch.float32).clone() \
+                            .contiguous().reshape(p.shape)
                 self._link_bias_tensors(p, group_idx, state)
 
     # ------------------------------------------------------------------
@@ -537,21 +543,51 @@ class TurboAdam(Optimizer):
         if self._found_inf is not None:
             table["found_inf"][sel] = self._skip_ptr
 
-    def _launch(self, device, items):
-        lib = _lib.load()
+    def _skip_flag(self, device, found_inf: torch.Tensor) -> torch.Tensor:
+        """A persistent per-device copy of GradScaler's found_inf (its tensor is
+        new every step; the descriptors of a captured step keep one address)."""
+        flag = self._skip_flags.get(device)
+        if flag is None:
+            flag = self._skip_flags[device] = torch.zeros(1, dtype=torch.float32, device=device)
+        flag.copy_(found_inf.reshape(1))
+        return flag
+
+    def _device_buffers(self, device, capturing: bool) -> _DeviceBuffers:
+        """The device's reusable buffers.  Buffers that a captured graph uses
+        stay as they are for its replays: an eager step that would have to
+        grow them or rewrite their pinned descriptor bytes moves to fresh
+        buffers (_prepare_buffers), and the captured ones are kept alive."""
         bufs = self._buffers.get(device)
         if bufs is None:
             bufs = self._buffers[device] = _DeviceBuffers(device)
+        if capturing:
+            bufs.captured = True
+        return bufs
+
+    def _prepare_buffers(self, device, bufs, desc_bytes, ws_bytes, raw, capturing: bool) -> _DeviceBuffers:
+        if bufs.captured and not capturing and not bufs.fits(desc_bytes, ws_bytes, raw):
+            self._retired_buffers.append(bufs)
+            bufs = self._buffers[device] = _DeviceBuffers(device)
+            with torch.cuda.device(device):
+                bufs.order_on(torch.cuda.current_stream(device))
+        return bufs
+
+    def _launch(self, device, items):
+        lib = _lib.load()
+        capturing = torch.cuda.is_current_stream_capturing()
+        bufs = self._device_buffers(device, capturing)
         with torch.cuda.device(device):
             bufs.order_on(torch.cuda.current_stream(device))
             if self._found_inf is not None:
-                self._skip_ptr = bufs.skip_flag(self._found_inf).data_ptr()
+                self._skip_ptr = self._skip_flag(device, self._found_inf).data_ptr()
         table = self._describe(device, items)
         n = len(items)
         arr = (_lib.TamTensor * n).from_buffer(table)
         info = _lib.TamStepInfo()
         _lib.check(lib.tam_prepare(arr, n, ctypes.byref(info)), "tam_prepare")
         nbytes = ctypes.sizeof(arr)
+        bufs = self._prepare_buffers(device, bufs, nbytes, info.ws_bytes, bytes(arr) if info.n_device_step else None,
+                                     capturing)
         if info.n_device_step:
             # a captured graph replays this copy: the same pinned bytes every time
             host = bufs.upload_static(bytes(arr))
@@ -562,18 +598,7 @@ class TurboAdam(Optimizer):
         ws = bufs.workspace(info.ws_bytes)
         with torch.cuda.device(device):
             desc[:nbytes].copy_(host, non_blocking=True)
-            stream = _lib.stream_of(device)
-            if self._pass_hook is None:
-                rc = lib.tam_multi_tensor_step(desc.data_ptr(), arr, ctypes.byref(info), self.philox_seed,
-                                               ws.data_ptr(), ws.numel(), stream)
-                _lib.check(rc, "tam_multi_tensor_step")
-            else:
-                for k in range(5 if info.n_ef else 4):
-                    self._pass_hook(k, "begin")
-                    rc = lib.tam_step_pass(k, desc.data_ptr(), ctypes.byref(info), self.philox_seed,
-                                           ws.data_ptr(), ws.numel(), stream)
-                    _lib.check(rc, f"tam_step_pass({k})")
-                    self._pass_hook(k, "end")
+            self._issue(lib, desc.data_ptr(), arr, info, ws, _lib.stream_of(device))
         for p, state, group, group_idx, tid in items:
             if not group.get("capturable"):
                 state["step"] += 1  # capturable: the step's first launch counts it
@@ -581,6 +606,21 @@ class TurboAdam(Optimizer):
                 mgr = state["m_mgr"]
                 mgr._has_state = True
                 mgr._original_numel = p.numel()
+
+    def _issue(self, lib, desc_ptr: int, arr, info, ws: torch.Tensor, stream: int) -> None:
+        """The step's launches: one tam_multi_tensor_step call, or the passes one
+        by one around _pass_hook."""
+        if self._pass_hook is None:
+            rc = lib.tam_multi_tensor_step(desc_ptr, arr, ctypes.byref(info), self.philox_seed, ws.data_ptr(),
+                                           ws.numel(), stream)
+            _lib.check(rc, "tam_multi_tensor_step")
+            return
+        for k in range(5 if info.n_ef else 4):
+            self._pass_hook(k, "begin")
+            rc = lib.tam_step_pass(k, desc_ptr, ctypes.byref(info), self.philox_seed, ws.data_ptr(), ws.numel(),
+                                   stream)
+            _lib.check(rc, f"tam_step_pass({k})")
+            self._pass_hook(k, "end")
 
     # GradScaler hands this optimizer grad_scale and found_inf (attributes set
     # around step()) instead of unscaling and checking on the host.

@@ -49,15 +49,27 @@ def quantize_logscale_nbits(v_flat: torch.Tensor, n_bits: int = 3, block_size: i
     return idx, scales, n_bits
 
 
+def _dequantize_operands(indices: torch.Tensor, scales: torch.Tensor, block_size: int, original_numel: int):
+    """Contiguous u8 indices, f16 scales and the element count of a decode.
+
+    As in the reference (quantize.py:202-214): the indices form (nb, 128) with
+    nb = scales.shape[0], and the result is the first original_numel values
+    (all nb*128 when 0; a larger count yields only the nb*128 that exist)."""
+    nb = scales.shape[0] if scales.dim() > 0 else 0
+    if scales.numel() != 2 * nb or indices.numel() != nb * block_size:
+        raise RuntimeError(f"dequantize_logscale_nbits: {indices.numel()} indices and scales of shape "
+                           f"{tuple(scales.shape)} do not form (num_blocks, {block_size}) blocks")
+    n = original_numel or nb * block_size
+    n = min(int(n), nb * block_size)
+    return indices.to(torch.uint8).contiguous(), scales.to(torch.float16).contiguous(), n
+
+
 def dequantize_logscale_nbits(indices: torch.Tensor, scales: torch.Tensor, n_bits: int = 3,
                               block_size: int = BLOCK_SIZE, original_numel: int = 0) -> torch.Tensor:
     """Values of a 1Q representation (reference quantize.py:183-214); fp32[original_numel]."""
     _check(n_bits, block_size, indices, "dequantize_logscale_nbits")
     lib = _lib.load()
-    nb = scales.shape[0]
-    n = original_numel or nb * block_size
-    idx = indices.to(torch.uint8).contiguous()
-    sc = scales.to(torch.float16).contiguous()
+    idx, sc, n = _dequantize_operands(indices, scales, block_size, original_numel)
     out = torch.empty(n, dtype=torch.float32, device=idx.device)
     with torch.cuda.device(idx.device):
         _lib.check(lib.tam_v_dequantize(idx.data_ptr(), sc.data_ptr(), n, n_bits, out.data_ptr(),
