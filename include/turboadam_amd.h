@@ -179,6 +179,21 @@ int tam_multi_tensor_step(const TamTensor* d_tensors, const TamTensor* h_tensors
                           const TamStepInfo* info, uint64_t seed, void* workspace,
                           size_t ws_bytes, void* stream);
 
+/* tam_multi_tensor_step for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc): the same step with no workspace argument.  No counterpart in
+ * the reference.  Its workspace is a static device array of
+ * TAM_STATIC_SCRATCH_BYTES that the library holds on every GPU it runs on
+ * until the process ends; the call allocates nothing (no hipMalloc, no
+ * allocating library routine).  A step whose info->ws_bytes exceeds
+ * TAM_STATIC_SCRATCH_BYTES (about 1.07e9 parameters of CoState tensors)
+ * returns TAM_E_WORKSPACE without launching anything.  Every call on one GPU
+ * shares that GPU's array: calls that overlap on one GPU (streams not
+ * ordered with each other) race.  The caller still provides d_tensors. */
+#define TAM_STATIC_SCRATCH_BYTES (64ull << 20)
+int tam_multi_tensor_step_static(const TamTensor* d_tensors, const TamTensor* h_tensors,
+                                 const TamStepInfo* info, uint64_t seed, void* stream);
+
 /* One of the passes of tam_multi_tensor_step (same arguments): 0 = the fused
  * update, 1 = alpha, 2 = CoState encode, 3 = selection and labels, 4 = the
  * error-feedback residual and commit of the staged encoding (nothing to do

@@ -29,6 +29,8 @@ TAM_FLAG_HAS_EF = 0x20
 TAM_FLAG_DEVICE_STEP = 0x40
 
 ABI_VERSION = 8
+# workspace of tam_multi_tensor_step_static (include/turboadam_amd.h)
+TAM_STATIC_SCRATCH_BYTES = 64 << 20
 
 
 class TamTensor(ctypes.Structure):
@@ -117,6 +119,10 @@ SIGNATURES = {
     "tam_multi_tensor_step": (
         ctypes.c_int,
         [_VP, ctypes.POINTER(TamTensor), ctypes.POINTER(TamStepInfo), ctypes.c_uint64, _VP, ctypes.c_size_t, _VP],
+    ),
+    "tam_multi_tensor_step_static": (
+        ctypes.c_int,
+        [_VP, ctypes.POINTER(TamTensor), ctypes.POINTER(TamStepInfo), ctypes.c_uint64, _VP],
     ),
     "tam_step_pass": (
         ctypes.c_int,

@@ -2413,6 +2413,62 @@ int tam_multi_tensor_step(const TamTensor* d_tensors, const TamTensor* h_tensors
   return TAM_OK;
 }
 
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// the step without a caller workspace (tam_multi_tensor_step_static)
+// ---------------------------------------------------------------------------
+// Its workspace is this file-scope device array: every GPU that loads the
+// library holds one copy of TAM_STATIC_SCRATCH_BYTES until the process ends.
+// Host code never passes `scratch` itself (in host code the name is only a
+// stand-in for the symbol); it passes the device address that
+// hipGetSymbolAddress returns for the current device, looked up once per
+// device on that device's first call and kept in tam_scratch_dev.  Nothing in
+// the array must start at zero: pass 0 writes every partial that pass 1
+// reads, pass 2 every ratio that pass 3 reads, and pass 3 resets its own
+// selection state and histograms first.  Every call on one GPU uses that
+// GPU's one array, so calls that overlap on one GPU (on streams not ordered
+// with each other) race.
+static __device__ __align__(256) char scratch[TAM_STATIC_SCRATCH_BYTES];
+
+static std::atomic<void*> tam_scratch_dev[64];
+
+// Device address of the current device's copy of `scratch`.
+static int tam_scratch_ptr(void** out) {
+  int dev = -1;
+  TAM_HIP_CHECK(hipGetDevice(&dev));
+  if (dev < 0 || dev >= 64) return tam_fail(TAM_E_UNSUPPORTED, "%sdevice index %ld out of range", "", dev);
+  void* p = tam_scratch_dev[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {  // threads that race look up and store the same address
+    TAM_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (p == nullptr) return tam_fail(TAM_E_HIP, "%sno device address for the static scratch", "");
+    tam_scratch_dev[dev].store(p, std::memory_order_release);
+  }
+  *out = p;
+  return TAM_OK;
+}
+
+extern "C" {
+
+int tam_multi_tensor_step_static(const TamTensor* d_tensors, const TamTensor* h_tensors, const TamStepInfo* info,
+                                 uint64_t seed, void* stream) {
+  tam_err_buf[0] = 0;
+  (void)h_tensors;
+  if (!info) return tam_fail(TAM_E_INVALID, "%snull argument", "");
+  if (info->ws_bytes > TAM_STATIC_SCRATCH_BYTES)
+    return tam_fail(TAM_E_WORKSPACE, "%sstep needs %ld bytes of workspace, above the static scratch of 64 MiB "
+                    "(use tam_multi_tensor_step with a workspace)", "", (long)info->ws_bytes);
+  if (info->n_tensors == 0 || info->total_tiles == 0) return TAM_OK;
+  void* ws = nullptr;
+  const int rc0 = tam_scratch_ptr(&ws);
+  if (rc0 != TAM_OK) return rc0;
+  for (int pass = 0; pass < 5; ++pass) {
+    const int rc = tam_launch_pass(pass, d_tensors, info, seed, ws, TAM_STATIC_SCRATCH_BYTES, (hipStream_t)stream);
+    if (rc != TAM_OK) return rc;
+  }
+  return TAM_OK;
+}
+
 int tam_v_dequantize(const uint8_t* v_idx, const uint16_t* v_scales, uint64_t n, uint32_t v_bits, float* out,
                      void* stream) {
   tam_err_buf[0] = 0;
