@@ -1041,50 +1041,364 @@ __device__ __forceinline__ void tam_k1_quarter(const TamTensor& d, uint32_t wq, 
   if (compress_v) tam_vpath_b<FULL>(d, W, vc, vx, tabs, seed_lo, seed_hi);
 }
 
-// Full quarters (inside the tensor, aligned arrays) of one parameter dtype:
-// persistent workgroups stride over the tiles; the four waves of a workgroup
-// take the four quarters of each tile and never synchronise with each other.
-// One kernel per dtype holds only that dtype's full-quarter code, so each
-// gets its own register budget (waves per SIMD below).
+// ---------------------------------------------------------------------------
+// Pass 0 over full units: 16 elements per lane
+// ---------------------------------------------------------------------------
+// A unit is 8 consecutive blocks (1024 elements: quarters 2u and 2u + 1) of
+// one tensor, processed by one wave: lane l owns elements [16(l%8), 16(l%8)+16)
+// of block 8u + l/8, so the 8 lanes of each DPP half-row hold one block.  The
+// arithmetic is the quarter path's, element for element; what is done once per
+// block and lane -- the correctly rounded logs of the block extremes, the
+// rounding bounds, the cross-lane reductions, the addressing -- is shared by 16
+// elements of a lane instead of 8, and loads and stores move 32 bytes per lane
+// and array.  The unit's two quarter partials go to their quarters' slots.
+#define TAM_EPU 16   // elements per lane in a unit
+#define TAM_K1U_WG 128  // threads of a main pass-0 workgroup: two waves, one unit each per tile
+
+// Minimum / maximum / or over the 8 lanes of a half-row (one block).
+__device__ __forceinline__ uint32_t tam_half_umin(uint32_t v) {
+  v = __builtin_elementwise_min(v, tam_dpp<TAM_DPP_XOR1>(v));
+  v = __builtin_elementwise_min(v, tam_dpp<TAM_DPP_XOR2>(v));
+  return __builtin_elementwise_min(v, tam_dpp<TAM_DPP_HALF_MIRROR>(v));
+}
+__device__ __forceinline__ uint32_t tam_half_umax(uint32_t v) {
+  v = __builtin_elementwise_max(v, tam_dpp<TAM_DPP_XOR1>(v));
+  v = __builtin_elementwise_max(v, tam_dpp<TAM_DPP_XOR2>(v));
+  return __builtin_elementwise_max(v, tam_dpp<TAM_DPP_HALF_MIRROR>(v));
+}
+__device__ __forceinline__ uint32_t tam_half_or(uint32_t v) {
+  v |= tam_dpp<TAM_DPP_XOR1>(v);
+  v |= tam_dpp<TAM_DPP_XOR2>(v);
+  return v | tam_dpp<TAM_DPP_HALF_MIRROR>(v);
+}
+
+// Sums of a and b over each block (8 lanes, each holding the fp64 sum of its
+// two 8-element partials), then over the unit's two quarters, (b0 + b1) +
+// (b2 + b3) and (b4 + b5) + (b6 + b7): the pairwise tree of the quarter path.
+// After the first step even lanes carry partial sums of a and odd lanes of b
+// (every later step pairs lanes an even distance apart); row_ror:4 completes
+// each block in lanes 4..7 of its half-row, row_ror:8 pairs the two blocks of
+// a row in lanes 4..7 and 12..15, and the swap pairs rows 0/1 and 2/3.  The
+// sums of a are valid in lanes 12 (quarter 0) and 44 (quarter 1), of b in
+// lanes 13 and 45.  Requires every lane active.
+__device__ __forceinline__ double tam_unit_sum2(double a, double b, uint32_t lane) {
+  const bool odd = (lane & 1u) != 0;
+  double x = (odd ? b : a) + tam_dppd<TAM_DPP_XOR1>(odd ? a : b);
+  x = x + tam_dppd<TAM_DPP_XOR2>(x);
+  x = x + tam_dppd<TAM_DPP_ROR4>(x);
+  x = x + tam_dppd<TAM_DPP_ROR8>(x);
+  return tam_swap_add<1>(x);
+}
+
+// Whether unit u lies inside the tensor with aligned arrays.
+__device__ __forceinline__ bool tam_unit_full(const TamTensor& d, uint32_t u) {
+  const bool aligned = (((uintptr_t)d.param | (uintptr_t)d.grad) & 15u) == 0;
+  return aligned && (uint64_t)(u + 1u) * (8u * TAM_BLOCK_SIZE) <= d.n;
+}
+
+// 1Q decode (quantize.py:252-256), EMA (:259-270) and block extremes of a
+// lane's 16 elements; as tam_vpath_a for a full quarter.  The 2^bits decode
+// levels of a block are evaluated once: for at most 8 levels lane k of the
+// block evaluates level k and elements fetch theirs with ds_bpermute; for 16
+// and 64 levels the block's 8 lanes fill its row of a per-wave LDS table; 8-bit
+// indices evaluate per element.
+__device__ __forceinline__ TamVExt tam_vunit_a(const TamTensor& d, uint32_t lane, uint32_t sc, TamW4 iw,
+                                               const float* g, float* v, float* lutw, const TamLdsTabs* tabs) {
+  const uint32_t nbk = 1u << d.v_bits;
+  const float inv_nbk = 1.0f / (float)nbk;  // exact power of two
+  const float lmin0 = tam_f16_to_f32((uint16_t)(sc & 0xffffu));
+  const float span0 = tam_f16_to_f32((uint16_t)(sc >> 16)) - lmin0;  // quantize.py:253-255
+  const uint32_t ws[4] = {iw.x, iw.y, iw.z, iw.w};
+  uint32_t idx[TAM_EPU];
+#pragma unroll
+  for (int i = 0; i < TAM_EPU; ++i) idx[i] = (ws[i >> 2] >> (8 * (i & 3))) & 0xffu;
+  const uint32_t l8 = lane & 7u;
+  float vo[TAM_EPU];
+  if (nbk <= 8u) {
+    // every lane of the wave takes part in the permutes
+    const uint32_t k = l8 & (nbk - 1u);
+    const float val = tam_expf_lds(lmin0 + ((float)k + 0.5f) * inv_nbk * span0, tabs);
+    const uint32_t row = lane & ~7u;
+#pragma unroll
+    for (int i = 0; i < TAM_EPU; ++i) {
+      const int src = (int)((row + (idx[i] & (nbk - 1u))) << 2);
+      vo[i] = tam_u2f((uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)tam_f2u(val)));
+    }
+  } else if (nbk <= 64u) {
+    float* tab = lutw + (lane >> 3) * 64u;
+    for (uint32_t k = l8; k < nbk; k += 8u) tab[k] = tam_expf_lds(lmin0 + ((float)k + 0.5f) * inv_nbk * span0, tabs);
+    tam_wave_lds_sync();
+#pragma unroll
+    for (int i = 0; i < TAM_EPU; ++i) vo[i] = tab[idx[i] & (nbk - 1u)];
+    tam_wave_lds_sync();  // the next unit rewrites the table
+  } else {
+#pragma unroll
+    for (int i = 0; i < TAM_EPU; ++i) vo[i] = tam_expf_lds(lmin0 + ((float)idx[i] + 0.5f) * inv_nbk * span0, tabs);
+  }
+  TamVExt x;
+  if (d.beta2 >= 0.0f && d.one_minus_beta2 >= 0.0f) {  // uniform: v >= +0 or NaN (see tam_vpath_a)
+    uint32_t xmn = 0xffffffffu, xmx = 0u;
+#pragma unroll
+    for (int i = 0; i < TAM_EPU; ++i) {
+      v[i] = __builtin_fmaf(d.one_minus_beta2, g[i] * g[i], vo[i] * d.beta2);
+      const uint32_t k2 = tam_f2u(v[i]) << 1;
+      xmn = __builtin_elementwise_min(xmn, k2);
+      xmx = __builtin_elementwise_max(xmx, k2);
+    }
+    x.kmn = tam_half_umin(xmn) >> 1;
+    x.kmx = tam_half_umax(xmx) >> 1;
+    x.nan_seen = x.kmx > 0x7f800000u ? TAM_VEXT_NAN : 0u;
+  } else {
+    // v may be negative: extremes of the clamped v, NaN tested per element
+    uint32_t kmn = 0x7f800000u, kmx = 0u, nan_seen = 0u;
+#pragma unroll
+    for (int i = 0; i < TAM_EPU; ++i) {
+      v[i] = __builtin_fmaf(d.one_minus_beta2, g[i] * g[i], vo[i] * d.beta2);
+      const float vc = v[i] < 1e-38f ? 1e-38f : v[i];
+      nan_seen |= tam_isnan(vc) ? 1u : 0u;
+      kmn = __builtin_elementwise_min(kmn, tam_f2u(vc));
+      kmx = __builtin_elementwise_max(kmx, tam_f2u(vc));
+    }
+    x.kmn = tam_half_umin(kmn);
+    x.kmx = tam_half_umax(kmx);
+    x.nan_seen = (tam_half_or(nan_seen) ? TAM_VEXT_NAN : 0u) | TAM_VEXT_CLAMPED;
+  }
+  return x;
+}
+
+// Logs of the block extremes, scales, certified stochastic re-quantisation of
+// a lane's 16 elements; as tam_vpath_b for a full quarter (same bound, same
+// fast path, same exact fallback).  Every v of a block that passes the block
+// test lies in [vmin, vmax] with vmin >= 2^-126, where the clamp to 1e-38
+// (quantize.py:275) leaves it unchanged, so the fast path reads v itself; the
+// exact path clamps.
+__device__ __forceinline__ void tam_vunit_b(const TamTensor& d, uint32_t lane, uint32_t b, uint64_t e0,
+                                            const float* v, TamVExt x, const TamLdsTabs* tabs, uint32_t seed_lo,
+                                            uint32_t seed_hi) {
+  const float fnb = (float)(1u << d.v_bits);
+  const uint32_t l8 = lane & 7u;
+  const uint32_t kmn = __builtin_elementwise_max(x.kmn, TAM_BITS_1EM38);
+  const uint32_t kmx = __builtin_elementwise_max(x.kmx, TAM_BITS_1EM38);
+  const bool nan_seen = (x.nan_seen & TAM_VEXT_NAN) != 0u;
+  // correctly rounded logs of the extremes: even lanes log(vmin), odd lanes log(vmax)
+  const float lx = tam_logf_lds(tam_u2f((l8 & 1u) ? kmx : kmn), tabs);
+  const float ly = tam_dppf<TAM_DPP_XOR1>(lx);
+  float lmn = (l8 & 1u) ? ly : lx;
+  float lmx = (l8 & 1u) ? lx : ly;
+  if (nan_seen) lmn = lmx = tam_qnan();  // torch.min / torch.max propagate NaN
+  float sp = lmx - lmn;  // quantize.py:283
+  sp = sp < 1e-10f ? 1e-10f : sp;
+  if (l8 == 0u)
+    tam_g((uint32_t*)d.v_scales)[b] = (uint32_t)tam_f32_to_f16(lmn) | ((uint32_t)tam_f32_to_f16(lmx) << 16);
+  const float rsp = __builtin_amdgcn_rcpf(sp);
+  const float K = (0x1.62e430p-1f * fnb) * rsp;
+  // the block bound of tam_vpath_b (full blocks)
+  const float rmin = __builtin_amdgcn_rcpf(tam_u2f(kmn));
+  const float Lm = __builtin_fmaxf(__builtin_fabsf(lmn), __builtin_fabsf(lmx));
+  const float per_sp = __builtin_fmaf(Lm + __builtin_fabsf(lmn), 0x1p-24f, 0x1p-22f);
+  const float flat = __builtin_fmaf(fnb, 0x1p-21f + 0x1p-20f, (fnb + 2.0f) * 0x1p-21f);
+  const float Bb = __builtin_fmaf(fnb * rsp, per_sp, flat) * (1.0f + 0x1p-16f);
+  const bool blk_ok = (tam_u2f(kmn) >= 0x1p-126f) && (tam_u2f(kmx) < 0x1p100f) && !nan_seen && (sp <= 64.0f) &&
+                      (Bb < 0.25f);
+  const float H = blk_ok ? 0.5f - (Bb + 0x1p-22f) : -1.0f;
+  // the lane's two halves of 8 elements one after the other (8 draws live at a time)
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const float* vh = v + TAM_EPL * h;
+    const uint64_t quad0 = (e0 >> 2) + 2u * (uint64_t)h;
+    const TamU4 r0 = tam_philox_quad(quad0, d.tensor_id, d.step, seed_lo, seed_hi);
+    const TamU4 r1 = tam_philox_quad(quad0 + 1, d.tensor_id, d.step, seed_lo, seed_hi);
+    const uint32_t rw[TAM_EPL] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
+    uint32_t ow[2] = {0u, 0u};
+    float tmax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < TAM_EPL; ++i) {
+      const float l2 = __builtin_amdgcn_logf(vh[i] * rmin);
+      const float ct = __builtin_fmaf(l2, K, 0.5f);
+      const float dd = __builtin_fmaf(-(float)(rw[i] >> 8), 0x1p-24f, ct);  // fl(ct - u), u exact
+      const float q = __builtin_rintf(dd);
+      tmax = __builtin_fmaxf(tmax, __builtin_fabsf(dd - q));
+      // the exact path overwrites rejected elements
+      ow[i >> 2] = __builtin_amdgcn_cvt_pk_u8_f32(__builtin_amdgcn_fmed3f(q, 0.0f, fnb - 1.0f), i & 3, ow[i >> 2]);
+    }
+    if (!(tmax < H)) {  // false for a NaN bound (then H = -1)
+      // exact path: the reference's own sequence with correctly rounded log and division
+#pragma unroll
+      for (int i = 0; i < TAM_EPL; ++i) {
+        const float dd = __builtin_fmaf(-(float)(rw[i] >> 8), 0x1p-24f,
+                                        __builtin_fmaf(__builtin_amdgcn_logf(vh[i] * rmin), K, 0.5f));
+        if (!(__builtin_fabsf(dd - __builtin_rintf(dd)) < H)) {
+          const float vc = vh[i] < 1e-38f ? 1e-38f : vh[i];  // quantize.py:275
+          const float l = tam_logf_lds(vc, tabs);
+          const float c = ((l - lmn) / sp) * fnb;  // quantize.py:284-285
+          const float f = __builtin_floorf(c);
+          const float fr = c - f;
+          const float u = (float)(rw[i] >> 8) * 0x1p-24f;
+          float q = f + (u < fr ? 1.0f : 0.0f);  // quantize.py:288-294
+          q = q < 0.0f ? 0.0f : q;
+          q = q > fnb - 1.0f ? fnb - 1.0f : q;
+          const uint32_t qi = tam_isnan(q) ? 0u : (uint32_t)q;
+          const uint32_t sh = 8u * (uint32_t)(i & 3);
+          ow[i >> 2] = (ow[i >> 2] & ~(0xffu << sh)) | (qi << sh);
+        }
+      }
+    }
+    tam_g((TamW2*)(d.v_idx + e0 + TAM_EPL * h))[0] = TamW2{ow[0], ow[1]};
+  }
+}
+
+// One wave's unit: loads, first moment (CoState or fp32), second moment (1Q or
+// fp32), update, store; for CoState tensors the partial sums of g.g and m.g of
+// the unit's two quarters (part: quarter 2u's {g.g, m.g}, then 2u + 1's).
+template <uint32_t DT>
+__device__ __forceinline__ void tam_k1_unit(const TamTensor& d, uint32_t u, uint32_t lane, float* lutw,
+                                            const TamLdsTabs* tabs, uint32_t seed_lo, uint32_t seed_hi,
+                                            double* __restrict__ part) {
+  const uint32_t l8 = lane & 7u;
+  const uint32_t b = u * 8u + (lane >> 3);
+  const uint64_t e0 = (uint64_t)b * TAM_BLOCK_SIZE + l8 * TAM_EPU;
+  const bool costate = (d.flags & TAM_FLAG_COSTATE) != 0;
+  const bool compress_v = (d.flags & TAM_FLAG_COMPRESS_V) != 0;
+  const bool has_state = costate && (d.flags & TAM_FLAG_HAS_STATE);
+  float g[TAM_EPU], p[TAM_EPU], m[TAM_EPU], v[TAM_EPU];
+  // every load of the unit is issued before any result is used
+  tam_ld8<DT, true>(d.grad, e0, TAM_EPL, g);
+  tam_ld8<DT, true>(d.grad, e0 + TAM_EPL, TAM_EPL, g + TAM_EPL);
+  tam_ld8<DT, true>(d.param, e0, TAM_EPL, p);
+  tam_ld8<DT, true>(d.param, e0 + TAM_EPL, TAM_EPL, p + TAM_EPL);
+  TamCsIn cs = {0u, 0u, 0u, 0.0f};
+  uint32_t sbytes = 0u;  // sign bytes of elements e0..e0+7 (low) and e0+8..e0+15
+  if (has_state) {
+    cs.label = tam_g(d.labels)[b];
+    cs.nrm = tam_g(d.norms)[b];
+    cs.amp = tam_g(d.amp)[b];
+    sbytes = tam_g((const uint16_t*)(d.signs + (e0 >> 3)))[0];
+  }
+  uint32_t sc = 0u;
+  TamW4 iw = {0u, 0u, 0u, 0u};
+  if (compress_v) {
+    sc = tam_g((const uint32_t*)d.v_scales)[b];
+    iw = tam_g((const TamW4*)(d.v_idx + e0))[0];
+  }
+  const float alpha_prev = has_state ? tam_g(d.alpha)[0] : 0.0f;
+  tam_compiler_fence();
+
+  // ---- first moment ---------------------------------------------------
+  if (costate) {
+    TamWave W;  // only its bvalid is read (full unit)
+    W.bvalid = true;
+    TamCsIn c0 = cs, c1 = cs;
+    c0.byte = sbytes & 0xffu;
+    c1.byte = sbytes >> 8;
+    tam_costate_m<true>(d, W, c0, alpha_prev, g, g, m);
+    tam_costate_m<true>(d, W, c1, alpha_prev, g + TAM_EPL, g + TAM_EPL, m + TAM_EPL);
+    // lane partials in fp32, their fp64 sum, then per block and quarter in fp64
+    const double t = tam_unit_sum2((double)tam_lane_dot(g, g) + (double)tam_lane_dot(g + TAM_EPL, g + TAM_EPL),
+                                   (double)tam_lane_dot(m, g) + (double)tam_lane_dot(m + TAM_EPL, g + TAM_EPL),
+                                   lane);
+    if ((lane & 31u) - 12u < 2u) tam_g(part)[(lane >> 5) * 2u + (lane & 1u)] = t;
+  } else {
+    // fp32 exp_avg (optimizer.py:113): m = fma(1-b1, g, fl(m*b1))
+    float ea[TAM_EPU];
+    tam_ld8_f32<true>(d.exp_avg, e0, TAM_EPL, ea);
+    tam_ld8_f32<true>(d.exp_avg, e0 + TAM_EPL, TAM_EPL, ea + TAM_EPL);
+#pragma unroll
+    for (int i = 0; i < TAM_EPU; ++i) m[i] = __builtin_fmaf(d.one_minus_beta1, g[i], ea[i] * d.beta1);
+    tam_st8_f32<true>(d.exp_avg, e0, TAM_EPL, m);
+    tam_st8_f32<true>(d.exp_avg, e0 + TAM_EPL, TAM_EPL, m + TAM_EPL);
+  }
+
+  // ---- second moment --------------------------------------------------
+  TamVExt vx = {0u, 0u, 0u};
+  if (compress_v) {
+    vx = tam_vunit_a(d, lane, sc, iw, g, v, lutw, tabs);
+  } else {
+    // fp32 exp_avg_sq (optimizer.py:166): v = fma(fl((1-b2)*g), g, fl(v*b2))
+    float es[TAM_EPU];
+    tam_ld8_f32<true>(d.exp_avg_sq, e0, TAM_EPL, es);
+    tam_ld8_f32<true>(d.exp_avg_sq, e0 + TAM_EPL, TAM_EPL, es + TAM_EPL);
+#pragma unroll
+    for (int i = 0; i < TAM_EPU; ++i) v[i] = __builtin_fmaf(d.one_minus_beta2 * g[i], g[i], es[i] * d.beta2);
+    tam_st8_f32<true>(d.exp_avg_sq, e0, TAM_EPL, v);
+    tam_st8_f32<true>(d.exp_avg_sq, e0 + TAM_EPL, TAM_EPL, v + TAM_EPL);
+  }
+
+  // ---- parameter update -----------------------------------------------
+  {
+    uint16_t pb[TAM_EPU];
+    bool q_ok = false;
+    if (DT != TAM_DTYPE_F32) {
+      TamVExt e = vx;
+      if (!compress_v) {
+        const TamVExt e1 = tam_lane_extremes<true>(v, TAM_EPL), e2 = tam_lane_extremes<true>(v + TAM_EPL, TAM_EPL);
+        e.kmn = __builtin_elementwise_min(e1.kmn, e2.kmn);
+        e.kmx = __builtin_elementwise_max(e1.kmx, e2.kmx);
+        e.nan_seen = e1.nan_seen | e2.nan_seen;
+      }
+      q_ok = tam_q_in_range(d, e);
+    }
+    tam_update<DT>(d, p, m, v, pb, q_ok);
+    tam_update<DT>(d, p + TAM_EPL, m + TAM_EPL, v + TAM_EPL, pb + TAM_EPL, q_ok);
+    if (DT == TAM_DTYPE_F32) {
+      tam_st8_f32<true>((float*)d.param, e0, TAM_EPL, p);
+      tam_st8_f32<true>((float*)d.param, e0 + TAM_EPL, TAM_EPL, p + TAM_EPL);
+    } else {
+      tam_st8_bits<true>(d.param, e0, TAM_EPL, pb);
+      tam_st8_bits<true>(d.param, e0 + TAM_EPL, TAM_EPL, pb + TAM_EPL);
+    }
+  }
+
+  // ---- re-quantisation of v -------------------------------------------
+  if (compress_v) tam_vunit_b(d, lane, b, e0, v, vx, tabs, seed_lo, seed_hi);
+}
+
+// Full units (inside the tensor, aligned arrays) of one parameter dtype:
+// persistent workgroups of two waves stride over the tiles; wave w takes unit
+// 2(tile - tile0) + w of the tile's tensor (quarters 4(tile - tile0) + 2w and
+// + 2w + 1), and the waves never synchronise with each other.  One kernel per
+// dtype holds only that dtype's code, so each gets its own register budget.
 template <uint32_t DT>
 __device__ __forceinline__ void tam_k1_full_body(const TamTensor* __restrict__ T, int nT, uint32_t total_tiles,
                                                  uint32_t seed_lo, uint32_t seed_hi,
                                                  double2* __restrict__ partials) {
   if (tam_step_skipped(T)) return;
-  __shared__ float lut[TAM_WG / 64][4 * 64];
+  __shared__ float lut[TAM_K1U_WG / 64][8 * 64];
   __shared__ TamLdsTabs tabs;
   tam_lds_tabs_fill(&tabs);
-  const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63u;
   float* lutw = lut[wave];
   int ti = tam_find_tensor(T, nT, blockIdx.x);
   for (uint32_t tile = blockIdx.x; tile < total_tiles; tile += gridDim.x) {
     ti = tam_advance_tensor(T, nT, ti, tile);
     const TamTensor& d = T[ti];
     if (d.dtype != DT || (d.flags & TAM_FLAG_EF)) continue;  // uniform; EF: tam_k1_ef
-    const uint32_t wq = (tile - d.tile0) * 4u + wave;        // quarter tile within the tensor
-    if (!tam_quarter_full(d, wq)) continue;                 // left to tam_k1_tail
-    // a wave-uniform partials address: a per-lane one is spilled in the 16-bit
-    // kernels, and its reload waits for every load in flight (the fp32 kernel
-    // spills more with the scalar form, so it keeps the per-lane one)
-    double2* part = partials + (uint64_t)tile * 4u + (DT == TAM_DTYPE_F32 ? wave : __builtin_amdgcn_readfirstlane(wave));
-    tam_k1_quarter<DT, true>(d, wq, lane, lutw, &tabs, seed_lo, seed_hi, part);
+    const uint32_t u = (tile - d.tile0) * 2u + wave;         // unit within the tensor
+    if (!tam_unit_full(d, u)) continue;                     // left to tam_k1_tail
+    double* part = (double*)(partials + (uint64_t)tile * 4u + 2u * wave);
+    tam_k1_unit<DT>(d, u, lane, lutw, &tabs, seed_lo, seed_hi, part);
   }
 }
 
-#define TAM_K1_FULL_KERNEL(NAME, DT, WAVES)                                                                  \
-  __global__ __launch_bounds__(TAM_WG) __attribute__((amdgpu_waves_per_eu(WAVES, WAVES))) void NAME(       \
-      const TamTensor* __restrict__ T, int nT, uint32_t total_tiles, uint32_t seed_lo, uint32_t seed_hi,   \
-      double2* __restrict__ partials) {                                                                    \
-    tam_k1_full_body<DT>(T, nT, total_tiles, seed_lo, seed_hi, partials);                                  \
+#define TAM_K1_FULL_KERNEL(NAME, DT, WAVES)                                                                     \
+  __global__ __launch_bounds__(TAM_K1U_WG) __attribute__((amdgpu_waves_per_eu(WAVES, WAVES))) void NAME(      \
+      const TamTensor* __restrict__ T, int nT, uint32_t total_tiles, uint32_t seed_lo, uint32_t seed_hi,      \
+      double2* __restrict__ partials) {                                                                       \
+    tam_k1_full_body<DT>(T, nT, total_tiles, seed_lo, seed_hi, partials);                                     \
   }
-// Waves per SIMD, measured best per dtype: bf16 5 (96 VGPRs), fp16 4 (its
-// fp16 conversions spill at 96 VGPRs; 11% faster unspilled), fp32 5 (4%
-// faster than 4 despite three spilled registers).
-TAM_K1_FULL_KERNEL(tam_k1_main_bf16, TAM_DTYPE_BF16, 5)
-TAM_K1_FULL_KERNEL(tam_k1_main_f16, TAM_DTYPE_F16, 4)
-TAM_K1_FULL_KERNEL(tam_k1_main_f32, TAM_DTYPE_F32, 5)
+#ifndef TAM_K1_WAVES_BF16
+#define TAM_K1_WAVES_BF16 4
+#endif
+#ifndef TAM_K1_WAVES_F16
+#define TAM_K1_WAVES_F16 4
+#endif
+#ifndef TAM_K1_WAVES_F32
+#define TAM_K1_WAVES_F32 4
+#endif
+TAM_K1_FULL_KERNEL(tam_k1_main_bf16, TAM_DTYPE_BF16, TAM_K1_WAVES_BF16)
+TAM_K1_FULL_KERNEL(tam_k1_main_f16, TAM_DTYPE_F16, TAM_K1_WAVES_F16)
+TAM_K1_FULL_KERNEL(tam_k1_main_f32, TAM_DTYPE_F32, TAM_K1_WAVES_F32)
 
-// The quarters that are not full: the last (at most four) quarters of each
+// The quarters outside full units: the last (at most five) quarters of each
 // tensor, or every quarter of a tensor whose parameter or gradient is not
 // 16-byte aligned.  An aligned tensor has one workgroup; an unaligned one has
 // one per TAM_TAIL_TILES tiles (tam_prepare: tail0, tail_wgs), so a large
@@ -1112,8 +1426,8 @@ __global__ __launch_bounds__(TAM_WG) void tam_k1_tail(const TamTensor* __restric
   const bool aligned = (((uintptr_t)d.param | (uintptr_t)d.grad) & 15u) == 0;
   const uint32_t nq = d.ntiles * 4u;
   uint32_t first, last;
-  if (aligned) {  // full quarters precede: tam_k1_main_<dtype> takes them
-    first = (uint32_t)(d.n / (4u * TAM_BLOCK_SIZE));
+  if (aligned) {  // full units precede: tam_k1_main_<dtype> takes them
+    first = 2u * (uint32_t)(d.n / (8u * TAM_BLOCK_SIZE));
     last = nq;
   } else {
     const uint32_t local = blockIdx.x - d.tail0;
@@ -2181,14 +2495,14 @@ enum { TAM_KS_K1_BF16, TAM_KS_K1_F16, TAM_KS_K1_F32, TAM_KS_K2, TAM_KS_K1_EF, TA
 #ifndef TAM_GRID_ROUNDS
 #define TAM_GRID_ROUNDS 32
 #endif
-static uint32_t tam_resident_grid(int which, const void* kernel) {
+static uint32_t tam_resident_grid(int which, const void* kernel, int block) {
   static std::atomic<uint32_t> cache[64][TAM_KS_COUNT];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
   uint32_t g = cache[dev][which].load(std::memory_order_relaxed);
   if (g == 0) {
     int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, TAM_WG, 0) != hipSuccess || per_cu <= 0)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block, 0) != hipSuccess || per_cu <= 0)
       per_cu = 4;
     g = (uint32_t)(per_cu * tam_device_cus());
     cache[dev][which].store(g, std::memory_order_relaxed);
@@ -2329,9 +2643,9 @@ static int tam_launch_pass(int pass, const TamTensor* d_tensors, const TamStepIn
   TamSel* sel = (TamSel*)(ws + info->off_sel);
   uint32_t* hist = (uint32_t*)(ws + info->off_hist);
   float* alpha_old = (float*)(ws + info->off_ef_alpha);
-  auto grid_of = [&](int which, const void* kernel) {
+  auto grid_of = [&](int which, const void* kernel, int block = TAM_WG) {
     const uint32_t rounds = which == TAM_KS_K2 ? TAM_K2_GRID_ROUNDS : TAM_GRID_ROUNDS;
-    const uint32_t g = tam_resident_grid(which, kernel) * rounds;
+    const uint32_t g = tam_resident_grid(which, kernel, block) * rounds;
     return info->total_tiles < g ? info->total_tiles : g;
   };
   switch (pass) {
@@ -2341,16 +2655,16 @@ static int tam_launch_pass(int pass, const TamTensor* d_tensors, const TamStepIn
         TAM_HIP_CHECK(hipGetLastError());
       }
       if (info->dtype_mask & (1u << TAM_DTYPE_BF16))
-        hipLaunchKernelGGL(tam_k1_main_bf16, dim3(grid_of(TAM_KS_K1_BF16, (const void*)tam_k1_main_bf16)),
-                           dim3(TAM_WG), 0, s, d_tensors, info->n_tensors, info->total_tiles, (uint32_t)seed,
+        hipLaunchKernelGGL(tam_k1_main_bf16, dim3(grid_of(TAM_KS_K1_BF16, (const void*)tam_k1_main_bf16, TAM_K1U_WG)),
+                           dim3(TAM_K1U_WG), 0, s, d_tensors, info->n_tensors, info->total_tiles, (uint32_t)seed,
                            (uint32_t)(seed >> 32), partials);
       if (info->dtype_mask & (1u << TAM_DTYPE_F16))
-        hipLaunchKernelGGL(tam_k1_main_f16, dim3(grid_of(TAM_KS_K1_F16, (const void*)tam_k1_main_f16)),
-                           dim3(TAM_WG), 0, s, d_tensors, info->n_tensors, info->total_tiles, (uint32_t)seed,
+        hipLaunchKernelGGL(tam_k1_main_f16, dim3(grid_of(TAM_KS_K1_F16, (const void*)tam_k1_main_f16, TAM_K1U_WG)),
+                           dim3(TAM_K1U_WG), 0, s, d_tensors, info->n_tensors, info->total_tiles, (uint32_t)seed,
                            (uint32_t)(seed >> 32), partials);
       if (info->dtype_mask & (1u << TAM_DTYPE_F32))
-        hipLaunchKernelGGL(tam_k1_main_f32, dim3(grid_of(TAM_KS_K1_F32, (const void*)tam_k1_main_f32)),
-                           dim3(TAM_WG), 0, s, d_tensors, info->n_tensors, info->total_tiles, (uint32_t)seed,
+        hipLaunchKernelGGL(tam_k1_main_f32, dim3(grid_of(TAM_KS_K1_F32, (const void*)tam_k1_main_f32, TAM_K1U_WG)),
+                           dim3(TAM_K1U_WG), 0, s, d_tensors, info->n_tensors, info->total_tiles, (uint32_t)seed,
                            (uint32_t)(seed >> 32), partials);
       if (info->n_ef)
         hipLaunchKernelGGL(tam_k1_ef, dim3(grid_of(TAM_KS_K1_EF, (const void*)tam_k1_ef)), dim3(TAM_WG), 0, s,
