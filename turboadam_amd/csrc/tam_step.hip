@@ -1612,43 +1612,19 @@ __global__ __launch_bounds__(TAM_WG) void tam_k_alpha(const TamTensor* __restric
 // ---------------------------------------------------------------------------
 // With error feedback the EMA takes g + residual and the encoding goes to the
 // tensor's staging area (pass 4 still needs the previous one).
-// Inputs of a full pass-2 quarter of a 16-bit tensor without error feedback
-// (the common case), loaded one quarter ahead of their use.
-struct TamK2In {
-  TamW4 gw;  // the lane's 8 gradient elements
-  TamCsIn cs;
-};
-__device__ __forceinline__ bool tam_k2_prefetchable(const TamTensor& d, uint32_t wq) {
-  return d.dtype != TAM_DTYPE_F32 && !(d.flags & TAM_FLAG_EF) && tam_quarter_full(d, wq);
-}
-__device__ __forceinline__ TamK2In tam_k2_load(const TamTensor& d, uint32_t wq, uint32_t lane) {
-  const TamWave W = tam_wave(d, wq, lane, true);
-  TamK2In r;
-  r.gw = tam_g((const TamW4*)((const uint16_t*)d.grad + W.e0))[0];
-  r.cs = tam_cs_load<true>(d, W);
-  return r;
-}
-
-// pre: the quarter's inputs when they were loaded ahead (FULL, 16-bit, no EF).
+// A pass-2 quarter (16 lanes per block, 8 elements per lane), its inputs loaded in place.
 #define TAM_CONST __attribute__((address_space(4)))
 template <uint32_t DT, bool FULL>
 __device__ __forceinline__ void tam_k2_quarter(const TamTensor& d, uint32_t wq, uint32_t lane, float a,
-                                               float* __restrict__ ratios, char* __restrict__ ws,
-                                               const TamK2In* pre = nullptr) {
+                                               float* __restrict__ ratios, char* __restrict__ ws) {
   const TamWave W = tam_wave(d, wq, lane, FULL);
   const bool ef = (d.flags & TAM_FLAG_EF) != 0;  // uniform
   float dl[TAM_EPL], md[TAM_EPL];
   uint32_t sbyte = 0;
   if (FULL || W.bvalid) {
     float g[TAM_EPL], ge[TAM_EPL], m[TAM_EPL];
-    TamCsIn cs;
-    if (pre) {
-      tam_unpack8<DT>(pre->gw, g);
-      cs = pre->cs;
-    } else {
-      tam_ld8<DT, FULL>(d.grad, W.e0, W.nv, g);
-      cs = tam_cs_load<FULL>(d, W);
-    }
+    tam_ld8<DT, FULL>(d.grad, W.e0, W.nv, g);
+    const TamCsIn cs = tam_cs_load<FULL>(d, W);
     // a scalar load (alpha is not written in this pass): no vector-memory
     // wait covers the next quarter's loads
     const float alpha_prev = (d.flags & TAM_FLAG_HAS_STATE) ? *(const TAM_CONST float*)d.alpha : 0.0f;
@@ -1724,19 +1700,102 @@ __device__ __forceinline__ void tam_k2_any(const TamTensor& d, uint32_t wq, uint
   }
 }
 
+// Pass 2 over full units of 16-bit tensors without error feedback (the common
+// case): 16 elements per lane, 8 lanes per block, as pass 0's main kernels.
+// The unit's inputs are loaded one unit ahead of their use: the lane's 16
+// gradient elements, its block's CoState state and its two sign bytes.
+struct TamK2U {
+  TamW4 g0, g1;
+  TamCsIn cs;  // byte: the sign bytes of elements e0..e0+7 (low) and e0+8..e0+15
+};
+__device__ __forceinline__ bool tam_k2u_prefetchable(const TamTensor& d, uint32_t u) {
+  return d.dtype != TAM_DTYPE_F32 && !(d.flags & TAM_FLAG_EF) && tam_unit_full(d, u);
+}
+__device__ __forceinline__ TamK2U tam_k2u_load(const TamTensor& d, uint32_t u, uint32_t lane) {
+  const uint32_t b = u * 8u + (lane >> 3);
+  const uint64_t e0 = (uint64_t)b * TAM_BLOCK_SIZE + (lane & 7u) * TAM_EPU;
+  const TAM_GLOBAL TamW4* gp = tam_g((const TamW4*)((const uint16_t*)d.grad + e0));
+  TamK2U r;
+  r.g0 = gp[0];
+  r.g1 = gp[1];
+  r.cs = TamCsIn{0u, 0u, 0u, 0.0f};
+  if (d.flags & TAM_FLAG_HAS_STATE) {
+    r.cs.label = tam_g(d.labels)[b];
+    r.cs.nrm = tam_g(d.norms)[b];
+    r.cs.amp = tam_g(d.amp)[b];
+    r.cs.byte = tam_g((const uint16_t*)(d.signs + (e0 >> 3)))[0];
+  }
+  return r;
+}
+
+// The CoState encode of a unit (as tam_k2_quarter for full quarters): m
+// recomputed bit-identically, delta = m - alpha*g, sign bits, block norms of
+// delta and m from fp32 lane partials and an fp64 tree over the block's 8
+// lanes (the parity split of tam_unit_sum2: after row_ror:4 the sum of
+// delta^2 is in lanes 4 and 6 of the half-row, of m^2 in lanes 5 and 7), the
+// fp16 amplitude (lane 4) and the ratio (lane 5).
+template <uint32_t DT>
+__device__ __forceinline__ void tam_k2_unit(const TamTensor& d, uint32_t u, uint32_t lane, float a,
+                                            float* __restrict__ ratios, const TamK2U& in) {
+  const uint32_t l8 = lane & 7u;
+  const uint32_t b = u * 8u + (lane >> 3);
+  const uint64_t e0 = (uint64_t)b * TAM_BLOCK_SIZE + l8 * TAM_EPU;
+  float g[TAM_EPU], m[TAM_EPU], dl[TAM_EPU];
+  tam_unpack8<DT>(in.g0, g);
+  tam_unpack8<DT>(in.g1, g + TAM_EPL);
+  // a scalar load (alpha is not written in this pass): no vector-memory wait
+  // covers the next unit's loads
+  const float alpha_prev = (d.flags & TAM_FLAG_HAS_STATE) ? *(const TAM_CONST float*)d.alpha : 0.0f;
+  TamWave W;  // only its bvalid is read (full unit)
+  W.bvalid = true;
+  TamCsIn c0 = in.cs, c1 = in.cs;
+  c0.byte = in.cs.byte & 0xffu;
+  c1.byte = in.cs.byte >> 8;
+  tam_costate_m<true>(d, W, c0, alpha_prev, g, g, m);
+  tam_costate_m<true>(d, W, c1, alpha_prev, g + TAM_EPL, g + TAM_EPL, m + TAM_EPL);
+  uint32_t sb0 = 0u, sb1 = 0u;
+#pragma unroll
+  for (int i = 0; i < TAM_EPU; ++i) {
+    dl[i] = m[i] - a * g[i];  // costate.py:42
+    // element 8j+k is bit 7-k of byte j (costate.py:170-181)
+    if (i < TAM_EPL) sb0 = 2u * sb0 + (dl[i] < 0.0f ? 1u : 0u);
+    else sb1 = 2u * sb1 + (dl[i] < 0.0f ? 1u : 0u);
+  }
+  const bool odd = (l8 & 1u) != 0;
+  const double sd = (double)tam_lane_dot(dl, dl) + (double)tam_lane_dot(dl + TAM_EPL, dl + TAM_EPL);
+  const double sm = (double)tam_lane_dot(m, m) + (double)tam_lane_dot(m + TAM_EPL, m + TAM_EPL);
+  double x = (odd ? sm : sd) + tam_dppd<TAM_DPP_XOR1>(odd ? sd : sm);
+  x = x + tam_dppd<TAM_DPP_XOR2>(x);
+  x = x + tam_dppd<TAM_DPP_ROR4>(x);
+  const float nx = (float)__builtin_sqrt(x);
+  const float ny = tam_dppf<TAM_DPP_XOR1>(nx);
+  const float nd = odd ? ny : nx;  // costate.py:241
+  const float nm = odd ? nx : ny;
+  const float qv = nd / (odd ? nm : d.sqrt_block);  // costate.py:248 / :81-84
+  tam_g((uint16_t*)(d.signs + (e0 >> 3)))[0] = (uint16_t)(sb0 | (sb1 << 8));
+  if (l8 == 4u) {
+    tam_g(d.norms)[b] = nd;
+    tam_g(d.amp)[b] = tam_f32_to_f16(qv);
+  } else if (l8 == 5u) {
+    tam_g(ratios)[d.ratio_off + b] = nm == 0.0f ? 0.0f : qv;
+  }
+}
+
 // Pass 2 is bound by memory latency rather than by its arithmetic or
-// bandwidth, so each wave loads the gradient and CoState bytes of its next
-// quarter before it computes the current one.  Descriptors and the alphas come
-// through scalar loads (their indices are wave-uniform): no vector-memory
-// wait then covers the loads in flight.  7 waves per SIMD (72 VGPRs, no
-// spills): measured 13% faster than 8 waves without the lookahead; at 6 waves
-// the lookahead loses.
-__global__ __launch_bounds__(TAM_WG) __attribute__((amdgpu_waves_per_eu(7, 7))) void tam_k2_encode(const TamTensor* __restrict__ T, int nT,
-                                                        uint32_t total_tiles,
-                                                        const float* __restrict__ alpha_new,
-                                                        float* __restrict__ ratios, char* __restrict__ ws) {
+// bandwidth, so each wave loads the inputs of its next unit before it computes
+// the current one.  Descriptors and the alphas come through scalar loads
+// (their indices are wave-uniform): no vector-memory wait then covers the
+// loads in flight.  Workgroups of two waves stride over the tiles; wave w takes
+// unit 2(tile - tile0) + w.  Units of fp32 or error-feedback tensors, and units
+// that are not full, take the quarter path (tam_k2_any) for their two quarters.
+#ifndef TAM_K2_WAVES
+#define TAM_K2_WAVES 7
+#endif
+__global__ __launch_bounds__(TAM_K1U_WG) __attribute__((amdgpu_waves_per_eu(TAM_K2_WAVES, TAM_K2_WAVES))) void
+tam_k2_encode(const TamTensor* __restrict__ T, int nT, uint32_t total_tiles, const float* __restrict__ alpha_new,
+              float* __restrict__ ratios, char* __restrict__ ws) {
   if (tam_step_skipped(T)) return;
-  const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63u;
   const auto desc = [&](int i) -> const TamTensor& { return T[__builtin_amdgcn_readfirstlane(i)]; };
   // the next tile at or after `tile` of a CoState tensor (uniform)
   const auto next = [&](uint32_t& tile, int& ti) -> bool {
@@ -1749,22 +1808,27 @@ __global__ __launch_bounds__(TAM_WG) __attribute__((amdgpu_waves_per_eu(7, 7))) 
   uint32_t tile = blockIdx.x;
   int ti = tam_find_tensor(T, nT, blockIdx.x);
   bool have = next(tile, ti);
-  TamK2In pre = {};
-  bool pre_ok = have && tam_k2_prefetchable(desc(ti), (tile - desc(ti).tile0) * 4u + wave);
-  if (pre_ok) pre = tam_k2_load(desc(ti), (tile - desc(ti).tile0) * 4u + wave, lane);
+  TamK2U pre = {};
+  bool pre_ok = have && tam_k2u_prefetchable(desc(ti), (tile - desc(ti).tile0) * 2u + wave);
+  if (pre_ok) pre = tam_k2u_load(desc(ti), (tile - desc(ti).tile0) * 2u + wave, lane);
   while (have) {
     uint32_t ntile = tile + gridDim.x;
     int nti = ti;
     const bool nhave = next(ntile, nti);
     const TamTensor& d = desc(ti);
-    const uint32_t wq = (tile - d.tile0) * 4u + wave;
+    const uint32_t u = (tile - d.tile0) * 2u + wave;
     const float a = *(const TAM_CONST float*)(alpha_new + __builtin_amdgcn_readfirstlane(ti));
-    TamK2In npre = {};
-    const bool npre_ok = nhave && tam_k2_prefetchable(desc(nti), (ntile - desc(nti).tile0) * 4u + wave);
-    if (npre_ok) npre = tam_k2_load(desc(nti), (ntile - desc(nti).tile0) * 4u + wave, lane);
-    if (pre_ok && d.dtype == TAM_DTYPE_BF16) tam_k2_quarter<TAM_DTYPE_BF16, true>(d, wq, lane, a, ratios, ws, &pre);
-    else if (pre_ok) tam_k2_quarter<TAM_DTYPE_F16, true>(d, wq, lane, a, ratios, ws, &pre);
-    else tam_k2_any(d, wq, lane, a, ratios, ws);
+    TamK2U npre = {};
+    const bool npre_ok = nhave && tam_k2u_prefetchable(desc(nti), (ntile - desc(nti).tile0) * 2u + wave);
+    if (npre_ok) npre = tam_k2u_load(desc(nti), (ntile - desc(nti).tile0) * 2u + wave, lane);
+    if (pre_ok && d.dtype == TAM_DTYPE_BF16) {
+      tam_k2_unit<TAM_DTYPE_BF16>(d, u, lane, a, ratios, pre);
+    } else if (pre_ok) {
+      tam_k2_unit<TAM_DTYPE_F16>(d, u, lane, a, ratios, pre);
+    } else {
+      tam_k2_any(d, 2u * u, lane, a, ratios, ws);
+      tam_k2_any(d, 2u * u + 1u, lane, a, ratios, ws);
+    }
     tile = ntile;
     ti = nti;
     have = nhave;
@@ -2682,7 +2746,8 @@ static int tam_launch_pass(int pass, const TamTensor* d_tensors, const TamStepIn
       hipLaunchKernelGGL(tam_k_alpha, dim3(info->n_tensors), dim3(TAM_WG), 0, s, d_tensors, chunk_sums, alpha_new);
       break;
     case 2:
-      hipLaunchKernelGGL(tam_k2_encode, dim3(grid_of(TAM_KS_K2, (const void*)tam_k2_encode)), dim3(TAM_WG), 0, s,
+      hipLaunchKernelGGL(tam_k2_encode, dim3(grid_of(TAM_KS_K2, (const void*)tam_k2_encode, TAM_K1U_WG)),
+                         dim3(TAM_K1U_WG), 0, s,
                          d_tensors, info->n_tensors, info->total_tiles, alpha_new, ratios, ws);
       break;
     default:
