@@ -74,6 +74,7 @@ def lib():
         L.or_decode_blocks.argtypes = [_VP, _VP, _VP, _VP, ctypes.c_float, _VP, ctypes.c_uint64, ctypes.c_float, _VP]
         L.or_fused_v_update.argtypes = [_VP, _VP, _VP, ctypes.c_uint64, ctypes.c_int, ctypes.c_float,
                                         ctypes.c_float, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint64, _VP]
+        L.or_dequantize.argtypes = [_VP, _VP, ctypes.c_uint64, ctypes.c_int, _VP]
         L.or_quantize_logscale.argtypes = [_VP, ctypes.c_uint64, ctypes.c_int, ctypes.c_int, ctypes.c_uint32,
                                            ctypes.c_uint32, ctypes.c_uint64, _VP, _VP]
         L.or_costate_update.argtypes = [_VP, ctypes.c_uint64, ctypes.c_float, ctypes.c_float, ctypes.c_float,
@@ -103,6 +104,17 @@ def philox_uniforms(tensor_id: int, step: int, seed: int, count: int) -> np.ndar
     return out
 
 
+def dequantize(indices: np.ndarray, scales_bits: np.ndarray, n: int, bits: int) -> np.ndarray:
+    """or_dequantize: the first n decoded 1Q values (scales as f16 bit patterns, 2 per block)."""
+    idx = np.ascontiguousarray(indices, dtype=np.uint8)
+    sc = np.ascontiguousarray(scales_bits, dtype=np.uint16).reshape(-1)
+    if n > idx.size or (n + BS - 1) // BS > sc.size // 2:
+        raise ValueError("dequantize: state does not cover n values")
+    out = np.empty(n, np.float32)
+    lib().or_dequantize(ptr(idx), ptr(sc), n, bits, ptr(out))
+    return out
+
+
 def ranks(nb: int, null_pct: float, amp_pct: float):
     return max(0, int(null_pct * nb) - 1), min(nb - 1, int(amp_pct * nb))
 
@@ -129,11 +141,12 @@ class OracleTurboAdam:
             groups = params
         else:
             groups = [{"params": list(params)}]
+        self.defaults = dict(DEFAULTS)
+        self.defaults.update(kw)
         self.param_groups = []
         flat = []
         for g in groups:
-            grp = dict(DEFAULTS)
-            grp.update(kw)
+            grp = dict(self.defaults)
             grp.update({k: v for k, v in g.items() if k != "params"})
             grp["params"] = list(g["params"])
             flat.extend(grp["params"])
@@ -143,6 +156,19 @@ class OracleTurboAdam:
         self.block0 = list(block0) if block0 is not None else [0] * len(flat)
         self.seed = seed
         self.state = {}
+
+    def add_param_group(self, group, dtypes=None):
+        """torch.optim.Optimizer.add_param_group: a new group whose unset
+        hyperparameters are the optimizer's defaults; its parameters follow all
+        earlier ones (their Philox tensor ids continue the numbering)."""
+        grp = dict(self.defaults)
+        grp.update({k: v for k, v in group.items() if k != "params"})
+        grp["params"] = list(group["params"])
+        n0 = len(self.dtypes)
+        self.param_groups.append(grp)
+        self.dtypes += list(dtypes) if dtypes is not None else [DT_F32] * len(grp["params"])
+        self.tensor_ids += list(range(n0, n0 + len(grp["params"])))
+        self.block0 += [0] * len(grp["params"])
 
     def _init(self, pid, p, grp):
         n = p.size

@@ -394,6 +394,23 @@ void or_fused_v_update(uint8_t* idx, uint16_t* scales, const float* g, uint64_t 
   or_fused_v_update_at(idx, scales, g, n, bits, beta2, one_minus_beta2, tid, step, seed, 0, v_out);
 }
 
+/* dequantize_logscale_nbits, reference quantize.py:183-214 (and decompress_v,
+ * oneq.py:51-67): out[i] = exp(lmin + ((idx + 0.5) / 2^bits) * span) for the
+ * first n values, each operation rounded to fp32 in the reference's order
+ * (the division by 2^bits is exact), exp correctly rounded. */
+void or_dequantize(const uint8_t* idx, const uint16_t* scales, uint64_t n, int bits, float* out) {
+  float nbk = (float)(1u << bits);
+  for (uint64_t i = 0; i < n; ++i) {
+    uint64_t b = i / OR_BS;
+    float lmin = or_f16_to_f32(scales[2 * b]);
+    float lmax = or_f16_to_f32(scales[2 * b + 1]);
+    float span = lmax - lmin;
+    float t = ((float)idx[i] + 0.5f) / nbk;
+    float lv = lmin + t * span;
+    out[i] = or_expf(lv);
+  }
+}
+
 /* quantize_logscale_nbits, reference quantize.py:126-180, on v already padded
  * to whole blocks (npad a multiple of 128).  Min / max run over every value
  * of the block (NaN propagates); stochastic != 0 draws u as the step does. */

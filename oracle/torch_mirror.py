@@ -277,18 +277,38 @@ DEFAULTS = O.DEFAULTS
 
 
 class MirrorTurboAdam:
-    """Host logic of the reference optimizer over torch CPU parameters."""
+    """Host logic of the reference optimizer over torch CPU parameters.
+
+    params: a list of tensors, or a list of groups {"params": [...], **hyperparameters}
+    (optimizer.py:224-292 over torch.optim's param_groups); add_param_group adds one."""
 
     def __init__(self, params, ops=FaithfulOps, seed=0, **kw):
-        self.group = dict(DEFAULTS)
-        self.group.update(kw)
-        self.params = list(params)
+        self.defaults = dict(DEFAULTS)
+        self.defaults.update(kw)
+        self.params = []
+        self.param_groups = []
         self.ops = ops
         self.seed = seed
         self.state = {}
+        groups = params if params and isinstance(params[0], dict) else [{"params": list(params)}]
+        for g in groups:
+            self.add_param_group(g)
 
-    def init_state(self, i, p):
-        grp = self.group
+    @property
+    def group(self):
+        return self.param_groups[0]
+
+    def add_param_group(self, group):
+        """torch.optim.Optimizer.add_param_group: unset hyperparameters are the
+        defaults; the group's parameters follow all earlier ones."""
+        grp = dict(self.defaults)
+        grp.update({k: v for k, v in group.items() if k != "params"})
+        start = len(self.params)
+        self.params.extend(group["params"])
+        grp["idx"] = list(range(start, len(self.params)))
+        self.param_groups.append(grp)
+
+    def init_state(self, i, p, grp):
         st = {"step": 0, "_compress_m": bool(grp["compress_m"] and p.numel() >= grp["min_m_compress_elements"])}
         if st["_compress_m"]:
             st["cs"] = {"has_state": False, "alpha": torch.tensor(0.0)}
@@ -301,45 +321,51 @@ class MirrorTurboAdam:
         self.state[i] = st
 
     def step(self, grads, ops=None, traces=None):
+        """grads: aligned with the flat parameter list (None = no gradient)."""
         ops = ops or self.ops
-        grp = self.group
-        lr, (b1, b2), eps, wd = grp["lr"], grp["betas"], grp["eps"], grp["weight_decay"]
-        for i, p in enumerate(self.params):
-            if grads[i] is not None and i not in self.state:
-                self.init_state(i, p)
-        # bias corrections from the last parameter with state (optimizer.py:172-188)
-        last = [self.state[i]["step"] for i in range(len(self.params)) if i in self.state][-1] + 1
-        bc1 = torch.tensor([1.0 - b1**last], dtype=torch.float32)
-        bc2 = torch.tensor([1.0 - b2**last], dtype=torch.float32)
-        for i, p in enumerate(self.params):
-            g = grads[i]
-            if g is None:
+        for grp in self.param_groups:  # lazy state (optimizer.py:238-286)
+            for i in grp["idx"]:
+                if grads[i] is not None and i not in self.state:
+                    self.init_state(i, self.params[i], grp)
+        for grp in self.param_groups:
+            with_state = [i for i in grp["idx"] if i in self.state]
+            if not with_state:
                 continue
-            st = self.state[i]
-            st["step"] += 1
-            tr = {} if traces is not None else None
-            if wd != 0.0:
-                p.mul_(1.0 - lr * wd)
-            if st["_compress_m"]:
-                m = costate_update(st["cs"], g, b1, grp["null_pct"], grp["amp_pct"], ops, tr,
-                                   ef=grp["error_feedback"]).reshape(p.shape)
-            else:
-                st["exp_avg"].mul_(b1).add_(g.reshape(-1), alpha=1.0 - b1)
-                m = st["exp_avg"].reshape(p.shape)
-            if grp["compress_v"]:
-                cv = st["compressed_v"]
-                nb = cv["scales"].shape[0]
-                u = torch.from_numpy(O.philox_uniforms(i, st["step"], self.seed, nb * BS))
-                v = v_update(cv, g, b2, u, ops, tr).reshape(p.shape)
-            else:
-                v = st["exp_avg_sq"]
-                v.mul_(b2).addcmul_(g.reshape(-1), g.reshape(-1), value=1.0 - b2)
-                v = v.reshape(p.shape)
-            denom = ops.sqrt(v / bc2).add_(eps)
-            p.addcdiv_(m, denom * bc1, value=-lr)
-            if traces is not None:
-                tr["denom"] = denom
-                traces[i] = tr
+            lr, (b1, b2), eps, wd = grp["lr"], grp["betas"], grp["eps"], grp["weight_decay"]
+            # bias corrections from the group's last parameter with state (optimizer.py:172-188)
+            last = self.state[with_state[-1]]["step"] + 1
+            bc1 = torch.tensor([1.0 - b1**last], dtype=torch.float32)
+            bc2 = torch.tensor([1.0 - b2**last], dtype=torch.float32)
+            for i in grp["idx"]:
+                g = grads[i]
+                if g is None:
+                    continue
+                p = self.params[i]
+                st = self.state[i]
+                st["step"] += 1
+                tr = {} if traces is not None else None
+                if wd != 0.0:
+                    p.mul_(1.0 - lr * wd)
+                if st["_compress_m"]:
+                    m = costate_update(st["cs"], g, b1, grp["null_pct"], grp["amp_pct"], ops, tr,
+                                       ef=grp["error_feedback"]).reshape(p.shape)
+                else:
+                    st["exp_avg"].mul_(b1).add_(g.reshape(-1), alpha=1.0 - b1)
+                    m = st["exp_avg"].reshape(p.shape)
+                if grp["compress_v"]:
+                    cv = st["compressed_v"]
+                    nb = cv["scales"].shape[0]
+                    u = torch.from_numpy(O.philox_uniforms(i, st["step"], self.seed, nb * BS))
+                    v = v_update(cv, g, b2, u, ops, tr).reshape(p.shape)
+                else:
+                    v = st["exp_avg_sq"]
+                    v.mul_(b2).addcmul_(g.reshape(-1), g.reshape(-1), value=1.0 - b2)
+                    v = v.reshape(p.shape)
+                denom = ops.sqrt(v / bc2).add_(eps)
+                p.addcdiv_(m, denom * bc1, value=-lr)
+                if traces is not None:
+                    tr["denom"] = denom
+                    traces[i] = tr
 
     def arrays(self, i) -> dict:
         """State of parameter i in the oracle's naming (numpy)."""

@@ -232,6 +232,108 @@ def run_reference_quantize(ref_mod, name, case):
     return out, meta
 
 
+# The 1Q decode (quantize.py:183-214, oneq.py:51-67) of the reference's own
+# quantizer outputs above: all values, and a trimmed count.
+DEQ_TRIM = 37
+
+
+def run_reference_dequantize(ref_mod):
+    import importlib
+
+    quant = importlib.import_module(ref_mod.__name__ + ".quantize")
+    oneq = importlib.import_module(ref_mod.__name__ + ".oneq")
+    out, cases = {}, {}
+    for name, case in Q_CASES.items():
+        z = np.load(os.path.join(HERE, f"golden_{name}.npz"))
+        idx = torch.from_numpy(z["indices"].copy())
+        scales = torch.from_numpy(z["scales"].view(np.int16).copy()).view(torch.float16).reshape(-1, 2)
+        nb = scales.shape[0]
+        full = quant.dequantize_logscale_nbits(idx, scales, n_bits=case["bits"], block_size=128, original_numel=0)
+        trim = quant.dequantize_logscale_nbits(idx, scales, n_bits=case["bits"], block_size=128,
+                                               original_numel=nb * 128 - DEQ_TRIM)
+        out[f"{name}_full"] = np_of(full)
+        out[f"{name}_trim"] = np_of(trim)
+        if case["fn"] == "compress":
+            st = {"indices": idx, "scales": scales, "n_bits": case["bits"], "original_shape": torch.Size([case["n"]]),
+                  "original_length": case["n"], "block_size": 128}
+            out[f"{name}_decompress"] = np_of(oneq.decompress_v(st))
+        cases[name] = {"bits": case["bits"], "nb": nb}
+    meta = {"cases": cases, "trim": DEQ_TRIM, "torch": torch.__version__, "threads": torch.get_num_threads()}
+    return out, meta
+
+
+# Host logic the other cases leave out (optimizer.py:224-292, :172-188, and
+# torch.optim's add_param_group): two groups with their own hyperparameters,
+# gradients that are None for some steps (a parameter first stepped late,
+# which as its group's last parameter with state sets the group's shared bias
+# corrections; a stepped parameter then skipped), and a third group added
+# before step 5.
+GROUPS_CASE = dict(
+    sizes=[5000, 300, 4608, 9000, 2000], dt=O.DT_F32, steps=8,
+    groups=[dict(idx=[0, 1], kw=dict(lr=1e-3, weight_decay=0.01)),
+            dict(idx=[2, 3], kw=dict(lr=5e-4, betas=(0.8, 0.99), v_bits=3, null_pct=0.05, amp_pct=0.95))],
+    added=dict(before_step=4, idx=[4], kw=dict(lr=2e-3, weight_decay=0.1, compress_m=False)),
+    kw=dict(lr=1e-3),
+    # step (0-based) -> parameters without a gradient
+    none={0: [3], 1: [1, 3], 2: [1, 3]},
+)
+
+
+def groups_grads(case, sig, s):
+    """Gradients of step s (None where the schedule gives none, or before a
+    parameter's group exists)."""
+    gs = step_grads(case, sig, s)
+    added = case["added"]
+    return [None if (i in case["none"].get(s, []) or (i in added["idx"] and s < added["before_step"])) else g
+            for i, g in enumerate(gs)]
+
+
+def run_reference_groups(ref_mod, case=GROUPS_CASE):
+    torch.manual_seed(0)
+    init, sig = case_inputs(case)
+    params = [torch.nn.Parameter(from_bits(a, case["dt"])) for a in init]
+    opt = ref_mod.TurboAdam([{"params": [params[i] for i in g["idx"]], **g["kw"]} for g in case["groups"]],
+                            **case["kw"])
+    order = [i for g in case["groups"] for i in g["idx"]]
+    rl = PhiloxRandLike(SR_SEED)
+    orig = torch.rand_like
+    digests = []
+    try:
+        torch.rand_like = rl
+        for s in range(case["steps"]):
+            if s == case["added"]["before_step"]:
+                opt.add_param_group({"params": [params[i] for i in case["added"]["idx"]], **case["added"]["kw"]})
+                order += case["added"]["idx"]
+            grads = groups_grads(case, sig, s)
+            for i, p in enumerate(params):
+                p.grad = None if grads[i] is None else from_bits(grads[i], case["dt"])
+            # tensor ids are positions in param_groups order (here equal to the indices)
+            # (opt.state is a defaultdict: a parameter without state must not be looked up,
+            # or the reference's next _prepare_step_scalars finds an empty state)
+            rl.queue = [(order.index(i), (opt.state[params[i]]["step"] if params[i] in opt.state else 0) + 1)
+                        for i in order if grads[i] is not None]
+            opt.step()
+            if rl.queue:
+                raise RuntimeError("reference did not draw the expected uniforms")
+            step_d = []
+            for i, p in enumerate(params):
+                arrs = state_arrays(opt, p) if p in opt.state else {}
+                arrs["param"] = np_of(p.data)
+                step_d.append(digest(arrs))
+            digests.append(step_d)
+    finally:
+        torch.rand_like = orig
+    out = {}
+    for i, p in enumerate(params):
+        for k, v in state_arrays(opt, p).items():
+            out[f"{k}_{i}"] = v
+        out[f"param_{i}"] = np_of(p.data)
+        out[f"step_{i}"] = np.array(opt.state[p]["step"])
+    meta = {"name": "groups", "digests": digests, "sr_seed": SR_SEED, "torch": torch.__version__,
+            "threads": torch.get_num_threads()}
+    return out, meta
+
+
 def main():
     ref_root = sys.argv[1] if len(sys.argv) > 1 else "/root/reference"
     only = sys.argv[2:]  # optional case names
@@ -250,6 +352,13 @@ def main():
         if only and name not in only:
             continue
         out, meta = run_reference_quantize(ref_mod, name, case)
+        path = os.path.join(HERE, f"golden_{name}.npz")
+        np.savez_compressed(path, meta=np.array(json.dumps(meta)), **out)
+        print(f"{name}: {os.path.getsize(path)} bytes", flush=True)
+    for name, fn in (("dequantize", run_reference_dequantize), ("groups", run_reference_groups)):
+        if only and name not in only:
+            continue
+        out, meta = fn(ref_mod)
         path = os.path.join(HERE, f"golden_{name}.npz")
         np.savez_compressed(path, meta=np.array(json.dumps(meta)), **out)
         print(f"{name}: {os.path.getsize(path)} bytes", flush=True)

@@ -221,3 +221,101 @@ def test_error_feedback_end_to_end_ties(name):
     for i, (a, b) in enumerate(zip(out["exact"], out["faithful"])):
         rel = float((a - b).norm() / b.norm())
         assert rel <= 1e-4, f"{name} tensor {i}: {rel:.3g}"
+
+
+def test_oracle_dequantize_matches_reference_and_exact_exp():
+    """or_dequantize (the 1Q decode of dequantize_logscale_nbits / decompress_v,
+    quantize.py:183-214, oneq.py:51-67) on the reference's own quantized
+    states: equal to the reference's outputs except where its exp (MKL) is
+    not correctly rounded -- one ulp, on a small fraction -- and equal, bit for
+    bit, to exp evaluated in 50-digit decimal and rounded once, of the
+    reference's fp32 argument lmin + ((idx + 0.5) / 2^bits) * span."""
+    import decimal
+
+    decimal.getcontext().prec = 50
+    z = np.load(os.path.join(HERE, "golden", "golden_dequantize.npz"))
+    meta = json.loads(str(z["meta"]))
+    rng = np.random.default_rng(9)
+    for name, c in meta["cases"].items():
+        q = np.load(os.path.join(HERE, "golden", f"golden_{name}.npz"))
+        idx, sc, bits, nb = q["indices"], q["scales"].reshape(-1), c["bits"], c["nb"]
+        full = O.dequantize(idx, sc, nb * 128, bits)
+        ref = z[f"{name}_full"]
+        diff = full.view(np.int32) != ref.view(np.int32)
+        assert diff.mean() <= 0.05, (name, diff.mean())  # MKL exp: within 1 ulp, not always correctly rounded
+        assert (np.abs(full.view(np.int32) - ref.view(np.int32))[diff] <= 1).all()
+        n = nb * 128 - meta["trim"]
+        assert np.array_equal(O.dequantize(idx, sc, n, bits), full[:n])
+        assert z[f"{name}_trim"].size == n
+        if f"{name}_decompress" in z.files:
+            assert np.array_equal(O.dequantize(idx, sc, 5000, bits).view(np.int32),
+                                  full[:5000].view(np.int32))
+            assert (np.abs(full[:5000].view(np.int32) - z[f"{name}_decompress"].view(np.int32)) <= 1).all()
+        # the oracle against exact decimal exp of the same fp32 argument
+        lmin = sc[0::2].view(np.float16).astype(np.float32)
+        span = (sc[1::2].view(np.float16).astype(np.float32) - lmin).astype(np.float32)
+        for i in rng.integers(0, nb * 128, 300):
+            b = i // 128
+            t = np.float32(np.float32(idx[i]) + np.float32(0.5)) / np.float32(2 ** bits)
+            lv = np.float32(lmin[b] + np.float32(t * span[b]))
+            y = decimal.Decimal(float(lv)).exp()
+            f = np.float32(float(y))
+            cands = [np.nextafter(f, np.float32(-np.inf)), f, np.nextafter(f, np.float32(np.inf))]
+            want = min(cands, key=lambda v: (abs(decimal.Decimal(float(v)) - y), int(np.float32(v).view(np.uint32)) & 1))
+            assert full[i].view(np.uint32) == np.float32(want).view(np.uint32), (name, int(i))
+
+
+# ---------------------------------------------------------------- host logic: groups, None gradients, add_param_group
+def _groups_mirror(ops):
+    case = MG.GROUPS_CASE
+    init, sig = MG.case_inputs(case)
+    params = [MG.from_bits(a, case["dt"]) for a in init]
+    opt = TM.MirrorTurboAdam([{"params": [params[i] for i in g["idx"]], **g["kw"]} for g in case["groups"]],
+                             ops=ops, seed=MG.SR_SEED, **case["kw"])
+    return case, sig, params, opt
+
+
+def _groups_torch_grads(case, sig, s):
+    return [None if g is None else MG.from_bits(g, case["dt"]) for g in MG.groups_grads(case, sig, s)]
+
+
+def test_faithful_mirror_reproduces_reference_groups():
+    """Two groups with their own hyperparameters, None gradients (a late
+    parameter that, as its group's last parameter with state, sets the group's
+    shared bias corrections; a parameter skipped after its first step) and a
+    group added before step 5: the faithful mirror equals the reference's
+    per-step digests."""
+    z, meta = _load("groups")
+    case, sig, params, opt = _groups_mirror(TM.FaithfulOps)
+    for s in range(case["steps"]):
+        if s == case["added"]["before_step"]:
+            opt.add_param_group({"params": [params[i] for i in case["added"]["idx"]], **case["added"]["kw"]})
+        opt.step(_groups_torch_grads(case, sig, s))
+        got = []
+        for i, p in enumerate(params):
+            arrs = opt.arrays(i) if i in opt.state else {}
+            arrs["param"] = MG.np_of(p)
+            got.append(MG.digest(arrs))
+        assert got == meta["digests"][s], f"groups: step {s + 1} differs from the reference"
+    for i in range(len(params)):
+        assert opt.state[i]["step"] == int(z[f"step_{i}"])
+
+
+def test_exact_mirror_equals_c_oracle_groups():
+    case, sig, params, opt = _groups_mirror(TM.ExactOps)
+    init, _ = MG.case_inputs(case)
+    oparams = [a.copy() for a in init]
+    orc = O.OracleTurboAdam([{"params": [oparams[i] for i in g["idx"]], **g["kw"]} for g in case["groups"]],
+                            dtypes=[case["dt"]] * 4, seed=MG.SR_SEED, **case["kw"])
+    for s in range(case["steps"]):
+        if s == case["added"]["before_step"]:
+            opt.add_param_group({"params": [params[i] for i in case["added"]["idx"]], **case["added"]["kw"]})
+            orc.add_param_group({"params": [oparams[i] for i in case["added"]["idx"]], **case["added"]["kw"]},
+                                dtypes=[case["dt"]])
+        opt.step(_groups_torch_grads(case, sig, s))
+        orc.step(MG.groups_grads(case, sig, s))
+        for i, p in enumerate(params):
+            assert np.array_equal(MG.np_of(p), oparams[i]), f"step {s + 1} param {i}"
+            if i in opt.state:
+                for k, v in opt.arrays(i).items():
+                    assert np.array_equal(v, orc.state[i][k]), f"step {s + 1} tensor {i} {k}"

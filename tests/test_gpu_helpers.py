@@ -219,11 +219,48 @@ def test_quantize_logscale(stochastic, bits):
     assert nbits == bits
     assert _same(_np(idx), idx_o)
     assert _same(_np(sc).reshape(-1), sc_o)
-    # round trip through dequantize / decompress
+    # round trip through dequantize / decompress, against the oracle's decode
     dq = Q.dequantize_logscale_nbits(idx, sc, bits, original_numel=n)
+    assert _same(_np(dq), O.dequantize(idx_o, sc_o, n, bits))
     comp = {"indices": idx, "scales": sc, "n_bits": bits, "original_shape": torch.Size([n]),
             "original_length": n, "block_size": 128}
-    assert _same(_np(oneq.decompress_v(comp)), _np(dq))
+    assert _same(_np(oneq.decompress_v(comp)), O.dequantize(idx_o, sc_o, n, bits))
+
+
+def test_dequantize_and_decompress_against_oracle_and_reference():
+    """dequantize_logscale_nbits / decompress_v (tam_v_dequantize) on the
+    reference's own quantized states (tests/golden): bit-exact against the
+    oracle's or_dequantize, and against the reference's outputs except where
+    its exp (MKL) is not correctly rounded, by one ulp there."""
+    import json
+    import os
+
+    from turboadam_amd import oneq, quantize as Q
+
+    here = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+    z = np.load(os.path.join(here, "golden_dequantize.npz"))
+    meta = json.loads(str(z["meta"]))
+    for name, c in meta["cases"].items():
+        q = np.load(os.path.join(here, f"golden_{name}.npz"))
+        idx, sc, bits, nb = q["indices"], q["scales"].reshape(-1), c["bits"], c["nb"]
+        log(f"dequantize {name}: {nb} blocks, {bits} bits")
+        idx_t, sc_t = _t(idx), _t(sc.view(np.float16)).reshape(nb, 2)
+        for n, key in ((nb * 128, "full"), (nb * 128 - meta["trim"], "trim")):
+            got = _np(Q.dequantize_logscale_nbits(idx_t, sc_t, bits, original_numel=n))
+            assert _same(got, O.dequantize(idx, sc, n, bits)), (name, key)
+            ref = z[f"{name}_{key}"]
+            diff = got.view(np.int32) != ref.view(np.int32)
+            assert diff.mean() <= 0.05 and (np.abs(got.view(np.int32) - ref.view(np.int32))[diff] <= 1).all()
+        # the reference returns the first nb*128 values for a larger count (quantize.py:214)
+        assert _np(Q.dequantize_logscale_nbits(idx_t, sc_t, bits, original_numel=nb * 128 + 5)).size == nb * 128
+        if f"{name}_decompress" in z.files:
+            n = 5000
+            comp = {"indices": idx_t, "scales": sc_t, "n_bits": bits, "original_shape": torch.Size([n]),
+                    "original_length": n, "block_size": 128}
+            got = _np(oneq.decompress_v(comp))
+            assert _same(got, O.dequantize(idx, sc, n, bits))
+            ref = z[f"{name}_decompress"]
+            assert (np.abs(got.view(np.int32) - ref.view(np.int32)) <= 1).all()
 
 
 def test_compress_v_logscale_init_closed_form():

@@ -520,3 +520,28 @@ def test_requantisation_of_narrow_log_spans(bits, lmin, lmax):
             bad += compare_states(gpu_state(opt, p), orc.state[i], f"step {s + 2} tensor {i}")
         log(f"narrow spans bits={bits} [{lmin}, {lmax}]: step {s + 2}, {len(bad)} mismatches")
         assert not bad, "\n".join(bad[:20])
+
+
+def test_update_bf16_results_near_rounding_midpoints():
+    # parameters in [1, 2) (bf16 spacing 2^-7) and lr = 2^-8: at step 1 the
+    # update is -lr*sign(g)/(1 + eps/|g|), so p + u lands within a few fp32
+    # units of a bf16 rounding midpoint, spread by eps/|g| across the certified
+    # update's error bound: accepted and rejected elements side by side, every
+    # one bit-exact
+    log("edge: bf16 updates near rounding midpoints")
+    rng = np.random.default_rng(76)
+    sizes = [4096 * 3 + 77, 5000]
+    init = [(1.0 + rng.integers(0, 128, n) / 128.0).astype(np.float32) for n in sizes]
+    grads = _edge_grads(rng, sizes, 3, 1e-5)
+    _check(_edge_run(BF16, init, grads, lr=2.0 ** -8, eps=1e-8))
+
+
+def test_update_beta1_near_one():
+    # bc1 = 1 - beta1^t near 2^-22 t: k_abs = fl(2^-147/bc1) and the
+    # certificate's absolute error term k_abs*r are at their largest
+    log("edge: beta1 = 1 - 2^-22, bf16")
+    rng = np.random.default_rng(77)
+    sizes = [4096 + 77, 3000]
+    init = [(rng.standard_normal(n) * 0.02).astype(np.float32) for n in sizes]
+    grads = _edge_grads(rng, sizes, 3, 1e-3)
+    _check(_edge_run(BF16, init, grads, lr=1e-3, betas=(1.0 - 2.0 ** -22, 0.999)))

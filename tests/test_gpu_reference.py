@@ -104,3 +104,48 @@ def test_gpu_200_step_trajectory_matches_reference():
 
     _run("traj_f32", check)
     assert worst and max(worst.values()) <= 1e-4, worst
+
+
+def test_gpu_groups_none_gradients_and_add_param_group():
+    """Two groups with their own hyperparameters, None gradients (a late
+    parameter that sets its group's shared bias corrections, a parameter
+    skipped after its first step) and a group added before step 5: the GPU
+    equals the oracle bit for bit every step, and ends within 1e-6 of the
+    reference's parameters (tests/golden/golden_groups.npz) with its step counts."""
+    from oracle import oracle as O
+    from tests.helpers import compare_states
+    from turboadam_amd import TurboAdam
+
+    log("GPU vs oracle and reference: param groups, None gradients, add_param_group")
+    z = np.load(os.path.join(HERE, "golden", "golden_groups.npz"))
+    case = MG.GROUPS_CASE
+    dev = torch.device("cuda:0")
+    init, sig = MG.case_inputs(case)
+    params = [torch.nn.Parameter(MG.from_bits(a, case["dt"]).to(dev)) for a in init]
+    opt = TurboAdam([{"params": [params[i] for i in g["idx"]], **g["kw"]} for g in case["groups"]],
+                    philox_seed=MG.SR_SEED, **case["kw"])
+    oparams = [a.copy() for a in init]
+    orc = O.OracleTurboAdam([{"params": [oparams[i] for i in g["idx"]], **g["kw"]} for g in case["groups"]],
+                            dtypes=[case["dt"]] * 4, seed=MG.SR_SEED, **case["kw"])
+    bad = []
+    for s in range(case["steps"]):
+        if s == case["added"]["before_step"]:
+            added = case["added"]
+            opt.add_param_group({"params": [params[i] for i in added["idx"]], **added["kw"]})
+            orc.add_param_group({"params": [oparams[i] for i in added["idx"]], **added["kw"]}, dtypes=[case["dt"]])
+        grads = MG.groups_grads(case, sig, s)
+        for p, g in zip(params, grads):
+            p.grad = None if g is None else MG.from_bits(g, case["dt"]).to(dev)
+        opt.step()
+        orc.step(grads)
+        torch.cuda.synchronize()
+        for i, p in enumerate(params):
+            if not np.array_equal(from_torch(p.data).view(np.uint32), oparams[i].view(np.uint32)):
+                bad.append(f"step {s + 1} tensor {i}: params differ")
+            if i in orc.state:
+                bad += compare_states(gpu_state(opt, p), orc.state[i], f"step {s + 1} tensor {i}")
+    assert not bad, "\n".join(bad[:20])
+    for i, p in enumerate(params):
+        pr = _rel(from_torch(p.data).astype(np.float64), z[f"param_{i}"].astype(np.float64))
+        assert pr <= 1e-6, f"tensor {i}: param rel {pr:.3g}"
+        assert opt.state[p]["step"] == int(z[f"step_{i}"])
