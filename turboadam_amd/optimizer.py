@@ -109,6 +109,55 @@ class _DeviceBuffers:
         return self.ws
 
 
+class _StepPlan:
+    """The descriptor table of one device's step, kept from step to step while
+    the same parameters have gradients and no state has been created,
+    replaced or loaded since (TurboAdam._layout_version).  A later step
+    rewrites only what changes between steps: gradient pointers, step numbers,
+    the has-state flags and the group scalars (lr, betas, eps, weight decay,
+    bias corrections)."""
+
+    def __init__(self, key, table, gsel, groups, static_flags, costate, ef, capturable):
+        self.key = key
+        self.table = table
+        self.gsel = gsel              # group row of each descriptor row
+        self.groups = groups          # (group, group_idx) of each group row
+        self.static_flags = static_flags  # flags without HAS_STATE / HAS_EF / WD
+        self.costate = costate        # rows with CoState m
+        self.ef = ef                  # rows with error feedback
+        self.capturable = capturable  # rows whose step fields the device fills
+        self.any_capturable = bool(capturable.any())
+        self.cost_rows = np.flatnonzero(costate)
+        self.ef_rows = np.flatnonzero(ef)
+        self.step_rows = np.flatnonzero(~capturable)
+
+
+class _PinnedUpload:
+    """Two pinned host buffers used in turn for the descriptor upload of eager
+    steps; a buffer is rewritten only after the copy from it has completed."""
+
+    def __init__(self):
+        self.bufs = [None, None]
+        self.events = [None, None]
+        self.k = 0
+
+    def stage(self, arr, nbytes: int) -> torch.Tensor:
+        k = self.k = 1 - self.k
+        if self.events[k] is not None:
+            self.events[k].synchronize()
+        if self.bufs[k] is None or self.bufs[k].numel() < nbytes:
+            self.bufs[k] = torch.empty(max(nbytes, 4096), dtype=torch.uint8, pin_memory=True)
+        ctypes.memmove(self.bufs[k].data_ptr(), ctypes.addressof(arr), nbytes)
+        return self.bufs[k][:nbytes]
+
+    def copied(self, stream) -> None:
+        """Record that the copy from the buffer just staged is enqueued on stream."""
+        ev = self.events[self.k]
+        if ev is None:
+            ev = self.events[self.k] = torch.cuda.Event()
+        ev.record(stream)
+
+
 class TurboAdam(Optimizer):
     """Adam optimizer with compressed first and second moment storage.
 
@@ -166,6 +215,11 @@ class TurboAdam(Optimizer):
             raise ValueError(f"philox_seed must be a 64-bit unsigned integer, got {philox_seed}")
         self.philox_seed = int(philox_seed)
         self._buffers = {}
+        self._plans = {}
+        self._uploads = {}
+        # bumped whenever a state is created, replaced or loaded: a descriptor
+        # table built before is then rebuilt (_StepPlan)
+        self._layout_version = 0
         self._retired_buffers = []  # buffers a captured graph still replays
         self._skip_flags = {}
         self._bc_values = {}
@@ -173,6 +227,12 @@ class TurboAdam(Optimizer):
         # Optional callable(pass_index, "begin"|"end") run around each of the four
         # launches (the step is then issued pass by pass); used to time kernels.
         self._pass_hook = None
+
+    def add_param_group(self, param_group):
+        """torch.optim.Optimizer.add_param_group; later parameters' tensor ids
+        (their positions in param_groups order) follow the new group's."""
+        super().add_param_group(param_group)
+        self._layout_version = getattr(self, "_layout_version", 0) + 1
 
     # ------------------------------------------------------------------
     # lazy state initialisation (reference optimizer.py:238-286)
@@ -203,6 +263,7 @@ class TurboAdam(Optimizer):
         if not group["compress_v"]:
             state["exp_avg_sq"] = torch.zeros_like(p, dtype=torch.float32, memory_format=torch.contiguous_format)
         self._link_bias_tensors(p, group_idx, state)
+        self._layout_version += 1
 
     def _link_bias_tensors(self, p, group_idx, state):
         device_key = (group_idx, p.device.type, p.device.index)
@@ -248,15 +309,19 @@ class TurboAdam(Optimizer):
                         self._init_state(p, group, group_idx, state)
                     if group["compress_v"] and "compressed_v" not in state:
                         state["compressed_v"] = init_v_state(p, group["v_bits"], group["block_size"])
-                    per_device.setdefault(p.device, []).append((p, state, group, group_idx, tid))
-                if not device_step:
+                        self._layout_version += 1
                     dev = p.device
-                    last[(dev.type, dev.index)] = state["step"]
+                    items = per_device.get(dev)
+                    if items is None:
+                        items = per_device[dev] = []
+                    items.append((p, state, group, group_idx, tid))
+                if not device_step:
+                    last[p.device] = state["step"]
             if last:
                 beta1, beta2 = group["betas"]
-                for (dtype_, index), step in last.items():
+                for dev, step in last.items():
                     next_step = step + 1
-                    self._bc_values[(group_idx, dtype_, index)] = (1.0 - beta1**next_step, 1.0 - beta2**next_step)
+                    self._bc_values[(group_idx, dev.type, dev.index)] = (1.0 - beta1**next_step, 1.0 - beta2**next_step)
         for key, (bc1, bc2) in self._bc_values.items():
             t = self._group_step_tensors.get(key)
             if t is not None:
@@ -310,6 +375,7 @@ class TurboAdam(Optimizer):
         CoStateManager objects are adopted into this package's class.  A
         "philox_seed" entry (written by state_dict) restores the Philox key.
         """
+        self._layout_version += 1
         if "philox_seed" in state_dict:
             state_dict = dict(state_dict)
             self.philox_seed = int(state_dict.pop("philox_seed"))
@@ -388,7 +454,21 @@ class TurboAdam(Optimizer):
         return (_f32(1.0 - lr * wd), _f32(beta1), _f32(1.0 - beta1), _f32(beta2), _f32(1.0 - beta2), _f32(bc1),
                 bc2_f, inv_bc2, _f32(inv_bc2), _f32(group["eps"]), _f32(-lr), _SQRT_BLOCK_F32)
 
-    def _describe(self, device, items) -> np.ndarray:
+    def _grad_ptr(self, p, state) -> int:
+        """Device address of p's gradient (checked; a contiguous copy of a
+        strided one is kept alive for the step)."""
+        g = p.grad
+        if g.is_sparse:
+            raise RuntimeError("turboadam_amd.TurboAdam does not support sparse gradients")
+        if g.dtype != p.dtype or g.device != p.device:
+            raise RuntimeError("turboadam_amd: gradient dtype/device must match the parameter")
+        if not g.is_contiguous():
+            g = g.contiguous()
+            state["_grad_keepalive"] = g
+            self._keepalive.append(state)
+        return g.data_ptr()
+
+    def _describe(self, device, items) -> _StepPlan:
         """The descriptor table (TamTensor rows) of one device's step.
 
         The per-tensor fields are gathered in one pass over the items and
@@ -397,31 +477,24 @@ class TurboAdam(Optimizer):
         rows = []
         group_rows = []
         groups = {}
+        group_list = []
         device_step = []
         for p, state, group, group_idx, tid in items:
             gi = groups.get(group_idx)
             if gi is None:
                 if group["block_size"] != BLOCK_SIZE:
                     raise NotImplementedError("turboadam_amd kernels use 128-element blocks (block_size=128)")
-                gi = groups[group_idx] = (len(group_rows), group["compress_v"],
-                                          _lib.TAM_FLAG_WD if group["weight_decay"] != 0.0 else 0,
-                                          bool(group.get("capturable")))
+                gi = groups[group_idx] = (len(group_rows), group["compress_v"], bool(group.get("capturable")))
                 group_rows.append(self._group_fields(group, group_idx, device))
-            gk, compress_v, flags, capturable = gi
-            g = p.grad
-            if g.is_sparse:
-                raise RuntimeError("turboadam_amd.TurboAdam does not support sparse gradients")
+                group_list.append((group, group_idx))
+            gk, compress_v, capturable = gi
+            flags = 0
             code = _DTYPES.get(p.dtype)
             if code is None:
                 raise NotImplementedError(f"turboadam_amd: unsupported parameter dtype {p.dtype}")
-            if g.dtype != p.dtype or g.device != p.device:
-                raise RuntimeError("turboadam_amd: gradient dtype/device must match the parameter")
             if not p.is_contiguous():
                 raise RuntimeError("turboadam_amd: parameters must be contiguous")
-            if not g.is_contiguous():
-                g = g.contiguous()
-                state["_grad_keepalive"] = g
-                self._keepalive.append(state)
+            gptr = self._grad_ptr(p, state)
             n = p.numel()
             nb = num_blocks(n)
             v_idx = v_scales = v_bits = exp_avg_sq = exp_avg = 0
@@ -456,6 +529,7 @@ class TurboAdam(Optimizer):
                     flags |= _lib.TAM_FLAG_EF
                     if mgr._ef_residual is None:
                         mgr._ef_residual = torch.zeros_like(p, dtype=torch.float32)
+                        self._layout_version += 1
                     else:
                         flags |= _lib.TAM_FLAG_HAS_EF
                     ef = mgr._ef_residual.data_ptr()
@@ -466,22 +540,60 @@ class TurboAdam(Optimizer):
                 step = 0  # filled on the device
             else:
                 step = state["step"] + 1  # the counter advances once the step is launched
-            rows.append((p.data_ptr(), g.data_ptr(), v_idx, v_scales, exp_avg_sq, exp_avg, signs, labels, norms,
+            rows.append((p.data_ptr(), gptr, v_idx, v_scales, exp_avg_sq, exp_avg, signs, labels, norms,
                          amp, alpha, ef, n, code, flags, v_bits, tid & 0xFFFFFFFF, step & 0xFFFFFFFF, k_lo, k_hi,
-                         gk))
+                         gk, capturable))
         table = np.zeros(len(rows), dtype=_DESC)
-        if not rows:
-            return table
-        cols = list(zip(*rows))
+        cols = list(zip(*rows)) if rows else [()] * (len(_ROW_FIELDS) + 2)
         for name, col in zip(_ROW_FIELDS, cols):
             table[name] = col
-        gsel = np.asarray(cols[-1], dtype=np.intp)
-        gvals = np.asarray(group_rows, dtype=np.float64)
-        for j, name in enumerate(_GROUP_FIELDS):
-            table[name] = gvals[gsel, j]
+        gsel = np.asarray(cols[-2], dtype=np.intp)
+        capt = np.asarray(cols[-1], dtype=bool)
+        plan = _StepPlan(None, table, gsel, group_list, None, (table["flags"] & _lib.TAM_FLAG_COSTATE) != 0,
+                         (table["flags"] & _lib.TAM_FLAG_EF) != 0, capt)
+        self._set_group_fields(plan, device, group_rows)
         if device_step:
             self._describe_device_step(table, device, device_step)
-        return table
+        plan.static_flags = table["flags"] & np.uint32(
+            ~(_lib.TAM_FLAG_HAS_STATE | _lib.TAM_FLAG_HAS_EF | _lib.TAM_FLAG_WD) & 0xFFFFFFFF)
+        return plan
+
+    def _set_group_fields(self, plan, device, group_rows=None) -> None:
+        """The fields a group shares (lr, betas, eps, weight decay and its flag,
+        bias corrections), for every row."""
+        if group_rows is None:
+            group_rows = [self._group_fields(g, gi, device) for g, gi in plan.groups]
+        if not group_rows:
+            return
+        t = plan.table
+        gvals = np.asarray(group_rows, dtype=np.float64)
+        for j, name in enumerate(_GROUP_FIELDS):
+            t[name] = gvals[plan.gsel, j]
+        wd = np.asarray([_lib.TAM_FLAG_WD if g["weight_decay"] != 0.0 else 0 for g, _ in plan.groups], np.uint32)
+        t["flags"] = (t["flags"] & np.uint32(~_lib.TAM_FLAG_WD & 0xFFFFFFFF)) | wd[plan.gsel]
+
+    def _refresh(self, plan, device, items) -> None:
+        """Per-step fields of a kept descriptor table: gradient pointers, step
+        numbers, has-state flags, group scalars (the rest is unchanged since
+        the plan was built: the same parameters, the same state arrays)."""
+        t = plan.table
+        t["grad"] = [self._grad_ptr(p, state) for p, state, _, _, _ in items]
+        if plan.step_rows.size:
+            t["step"][plan.step_rows] = [(items[i][1]["step"] + 1) & 0xFFFFFFFF for i in plan.step_rows]
+        flags = plan.static_flags.copy()
+        host = ~plan.capturable  # capturable rows: the device sets HAS_STATE / HAS_EF
+        if plan.cost_rows.size:
+            hs = np.zeros(len(items), bool)
+            hs[plan.cost_rows] = [items[i][1]["m_mgr"]._has_state for i in plan.cost_rows]
+            flags[hs & host] |= np.uint32(_lib.TAM_FLAG_HAS_STATE)
+        if plan.ef_rows.size:
+            he = np.zeros(len(items), bool)
+            he[plan.ef_rows] = True  # the residual exists (allocated when the plan was built) and has been written
+            flags[he & host] |= np.uint32(_lib.TAM_FLAG_HAS_EF)
+        t["flags"] = flags
+        self._set_group_fields(plan, device)
+        if plan.any_capturable:
+            t["found_inf"][plan.capturable] = self._skip_ptr if self._found_inf is not None else 0
 
     # ------------------------------------------------------------------
     # capturable steps (the step counter and bias corrections on the device)
@@ -540,8 +652,7 @@ class TurboAdam(Optimizer):
         table["bc_step"][sel] = src_ptr
         table["bc_table"][sel] = tab_ptr
         table["bc_len"][sel] = tab_len
-        if self._found_inf is not None:
-            table["found_inf"][sel] = self._skip_ptr
+        table["found_inf"][sel] = self._skip_ptr if self._found_inf is not None else 0
 
     def _skip_flag(self, device, found_inf: torch.Tensor) -> torch.Tensor:
         """A persistent per-device copy of GradScaler's found_inf (its tensor is
@@ -580,7 +691,15 @@ class TurboAdam(Optimizer):
             bufs.order_on(torch.cuda.current_stream(device))
             if self._found_inf is not None:
                 self._skip_ptr = self._skip_flag(device, self._found_inf).data_ptr()
-        table = self._describe(device, items)
+        key = tuple(it[4] for it in items)
+        plan = self._plans.get(device)
+        if plan is None or plan.key != (key, self._layout_version):
+            plan = self._describe(device, items)
+            plan.key = (key, self._layout_version)  # after _describe, which may create an EF residual
+            self._plans[device] = plan
+        else:
+            self._refresh(plan, device, items)
+        table = plan.table
         n = len(items)
         arr = (_lib.TamTensor * n).from_buffer(table)
         info = _lib.TamStepInfo()
@@ -588,24 +707,31 @@ class TurboAdam(Optimizer):
         nbytes = ctypes.sizeof(arr)
         bufs = self._prepare_buffers(device, bufs, nbytes, info.ws_bytes, bytes(arr) if info.n_device_step else None,
                                      capturing)
+        upload = None
         if info.n_device_step:
             # a captured graph replays this copy: the same pinned bytes every time
             host = bufs.upload_static(bytes(arr))
         else:
-            host = torch.empty(nbytes, dtype=torch.uint8, pin_memory=True)
-            ctypes.memmove(host.data_ptr(), ctypes.addressof(arr), nbytes)
+            upload = self._uploads.get(device)
+            if upload is None:
+                upload = self._uploads[device] = _PinnedUpload()
+            host = upload.stage(arr, nbytes)
         desc = bufs.desc_buffer(nbytes)
         ws = bufs.workspace(info.ws_bytes)
         with torch.cuda.device(device):
+            stream = torch.cuda.current_stream(device)
             desc[:nbytes].copy_(host, non_blocking=True)
-            self._issue(lib, desc.data_ptr(), arr, info, ws, _lib.stream_of(device))
+            if upload is not None:
+                upload.copied(stream)
+            self._issue(lib, desc.data_ptr(), arr, info, ws, stream.cuda_stream)
         for p, state, group, group_idx, tid in items:
             if not group.get("capturable"):
                 state["step"] += 1  # capturable: the step's first launch counts it
             if state["_compress_m"]:
                 mgr = state["m_mgr"]
-                mgr._has_state = True
-                mgr._original_numel = p.numel()
+                if not mgr._has_state:
+                    mgr._has_state = True
+                    mgr._original_numel = p.numel()
 
     def _issue(self, lib, desc_ptr: int, arr, info, ws: torch.Tensor, stream: int) -> None:
         """The step's launches: one tam_multi_tensor_step call, or the passes one
