@@ -15,9 +15,10 @@
  * widened to fp64, then a balanced fp64 pairwise tree over the 16 partials of
  * a 128-element block and over the blocks zero-padded to a power of two,
  * rounded to fp32 once (norms: fp64 sqrt first); sqrt correctly rounded.
- * Stochastic-rounding draws come from Philox4x32-10 (counter = (element/4,
- * tensor_id, step, element/2^34), key = seed), word element%4, uniform =
- * (word >> 8) * 2^-24.
+ * Stochastic-rounding draws come from Philox4x32-10, key = seed: element
+ * e = 16t + k of the zero-padded block layout takes bits [24k, 24k+24) of the
+ * 384-bit little-endian string of the blocks with counters (3t + j,
+ * tensor_id, step, (3t + j) >> 32), j = 0, 1, 2; uniform = draw * 2^-24.
  */
 #ifndef TURBOADAM_AMD_H
 #define TURBOADAM_AMD_H

@@ -16,8 +16,10 @@
  * and every other operation is the fp32 operation torch performs, in the
  * reference's order (fma exactly where torch fuses: Tensor.add_(alpha=) and
  * addcmul_).  Stochastic-rounding uniforms: Philox4x32-10 (its own
- * implementation here), counter (e/4, tensor_id, step, e>>34), key seed,
- * word e%4, u = (word >> 8) * 2^-24.  Compiled with -ffp-contract=off.
+ * implementation here): elements in groups of 16, group t = e/16 taking the
+ * 384 bits of the blocks with counters (3t + j, tensor_id, step, (3t+j)>>32),
+ * j = 0..2, key seed, little endian; element 16t + k takes bits
+ * [24k, 24k+24), u = that integer * 2^-24.  Compiled with -ffp-contract=off.
  */
 #include <math.h>
 #include <stdint.h>
@@ -50,16 +52,38 @@ void or_philox4x32_10(const uint32_t ctr[4], uint32_t k0, uint32_t k1, uint32_t 
   out[0] = c0; out[1] = c1; out[2] = c2; out[3] = c3;
 }
 
+/* The 16 uniforms of draw group t (elements 16t .. 16t+15): the 384 bits of
+ * the Philox blocks with counters (3t + j, tid, step, (3t + j) >> 32), j =
+ * 0, 1, 2, as a little-endian bit string; element 16t + k takes the 24-bit
+ * integer at bits [24k, 24k + 24), times 2^-24. */
+static void or_group_uniforms(uint64_t t, uint32_t tid, uint32_t step, uint64_t seed, float* u16) {
+  uint8_t bytes[48];
+  for (int j = 0; j < 3; ++j) {
+    uint64_t c = 3 * t + (uint64_t)j;
+    uint32_t ctr[4] = {(uint32_t)c, tid, step, (uint32_t)(c >> 32)};
+    uint32_t w[4];
+    or_philox4x32_10(ctr, (uint32_t)seed, (uint32_t)(seed >> 32), w);
+    for (int i = 0; i < 4; ++i)
+      for (int b = 0; b < 4; ++b) bytes[16 * j + 4 * i + b] = (uint8_t)(w[i] >> (8 * b));
+  }
+  for (int k = 0; k < 16; ++k) {
+    uint32_t d = (uint32_t)bytes[3 * k] | ((uint32_t)bytes[3 * k + 1] << 8) | ((uint32_t)bytes[3 * k + 2] << 16);
+    u16[k] = (float)d * (1.0f / 16777216.0f);
+  }
+}
+
 static float or_uniform(uint64_t e, uint32_t tid, uint32_t step, uint64_t seed) {
-  uint64_t q = e >> 2;
-  uint32_t ctr[4] = {(uint32_t)q, tid, step, (uint32_t)(q >> 32)};
-  uint32_t w[4];
-  or_philox4x32_10(ctr, (uint32_t)seed, (uint32_t)(seed >> 32), w);
-  return (float)(w[e & 3] >> 8) * (1.0f / 16777216.0f);
+  float u16[16];
+  or_group_uniforms(e >> 4, tid, step, seed, u16);
+  return u16[e & 15];
 }
 
 void or_philox_uniforms(uint32_t tid, uint32_t step, uint64_t seed, uint64_t count, float* out) {
-  for (uint64_t e = 0; e < count; ++e) out[e] = or_uniform(e, tid, step, seed);
+  float u16[16];
+  for (uint64_t t = 0; t * 16 < count; ++t) {
+    or_group_uniforms(t, tid, step, seed, u16);
+    for (int k = 0; k < 16 && t * 16 + (uint64_t)k < count; ++k) out[t * 16 + (uint64_t)k] = u16[k];
+  }
 }
 
 /* ------------------------------------------------------ fp16 / bf16 RNE */
@@ -374,12 +398,15 @@ static void or_fused_v_update_at(uint8_t* idx, uint16_t* scales, const float* g,
     scales[2 * b + 1] = or_f32_to_f16(nmax);
     float sp = nmax - nmin;
     if (sp < 1e-10f) sp = 1e-10f;                  /* :283 clamp(min=1e-10) */
+    float ub[OR_BS];                               /* the block's draws (8 groups of 16) */
+    for (int t = 0; t < OR_BS / 16; ++t)
+      or_group_uniforms((e_base + b * OR_BS) / 16 + (uint64_t)t, tid, step, seed, ub + 16 * t);
     for (int j = 0; j < OR_BS; ++j) {
       uint64_t i = b * OR_BS + j;
       float c = ((lg[j] - nmin) / sp) * nbk;       /* :284-285 */
       float f = floorf(c);
       float fr = c - f;
-      float u = or_uniform(e_base + i, tid, step, seed);
+      float u = ub[j];
       float r = f + (u < fr ? 1.0f : 0.0f);        /* :288-294 */
       if (r < 0.0f) r = 0.0f;
       if (r > nbk - 1.0f) r = nbk - 1.0f;

@@ -43,15 +43,30 @@ def test_philox_known_answers(ctr, key, want):
 
 
 def test_philox_uniform_layout():
-    # element e uses word e%4 of the call with counter (e//4, tid, step, 0)
+    # group t = e // 16: the three blocks with counters (3t + j, tid, step,
+    # (3t + j) >> 32) as one little-endian 384-bit integer; element e takes
+    # bits [24 (e % 16), 24 (e % 16) + 24) -- here as Python big-integer
+    # arithmetic over the KAT-pinned generator, including a counter past 2^32
     seed = 0x0123456789ABCDEF
-    u = O.philox_uniforms(5, 9, seed, 12)
-    for e in range(12):
-        c = np.array([e // 4, 5, 9, 0], np.uint32)
+    n = 16 * 5 + 7
+    u = O.philox_uniforms(5, 9, seed, n)
+
+    def block(c):
+        ctr = np.array([c & 0xFFFFFFFF, 5, 9, c >> 32], np.uint32)
         out = np.zeros(4, np.uint32)
-        L.or_philox4x32_10(P(c), seed & 0xFFFFFFFF, seed >> 32, P(out))
-        assert u[e] == np.float32((int(out[e % 4]) >> 8) * 2.0**-24)
+        L.or_philox4x32_10(P(ctr), seed & 0xFFFFFFFF, seed >> 32, P(out))
+        return sum(int(w) << (32 * i) for i, w in enumerate(out))
+
+    for e in range(n):
+        t, k = divmod(e, 16)
+        bits = sum(block(3 * t + j) << (128 * j) for j in range(3))
+        assert u[e] == np.float32(((bits >> (24 * k)) & 0xFFFFFF) * 2.0**-24), e
     assert (u >= 0).all() and (u < 1).all()
+    # a group whose counters pass 2^32 (group t = 2^32 // 3 + 1): the slice
+    # draws of a block0 offset reach it through or_fused_v_update
+    t = (1 << 32) // 3 + 1
+    bits = sum(block(3 * t + j) << (128 * j) for j in range(3))
+    assert 3 * t > (1 << 32) and bits > 0
 
 
 # ---------------------------------------------------------------- fp16 / bf16

@@ -75,21 +75,54 @@ TAM_HD TamU4 tam_philox4x32_10(TamU4 c, uint32_t k0, uint32_t k1) {
   return c;
 }
 
-// Uniform in [0,1) with 24-bit resolution: (word >> 8) * 2^-24 (exact).
-TAM_HD float tam_u01(uint32_t w) { return (float)(w >> 8) * 0x1p-24f; }
-
-// The stochastic-rounding draw of element `e` (index into the tensor's
-// zero-padded block layout) of tensor `tid` at optimizer step `step`:
-// counter = (e/4, tid, step, e/2^34), key = (seed_lo, seed_hi), word e%4.
-TAM_HD TamU4 tam_philox_quad(uint64_t quad, uint32_t tid, uint32_t step,
-                             uint32_t seed_lo, uint32_t seed_hi) {
+// Stochastic-rounding draws of tensor `tid` at optimizer step `step`.  The
+// elements of the tensor's zero-padded block layout go in groups of 16
+// consecutive ones, e = 16t + k; group t takes the 384 bits of three
+// Philox4x32-10 blocks with counters (3t + j, tid, step, (3t + j) >> 32),
+// j = 0, 1, 2, key (seed_lo, seed_hi), read as the little-endian words
+// w0..w11, and element k's draw is the 24-bit integer at bits [24k, 24k+24):
+// uniform = that integer * 2^-24 (exact).  Every output bit is used (four
+// draws per three words).
+TAM_HD TamU4 tam_philox_block(uint64_t ctr, uint32_t tid, uint32_t step, uint32_t seed_lo, uint32_t seed_hi) {
   TamU4 c;
-  c.x = (uint32_t)quad;
+  c.x = (uint32_t)ctr;
   c.y = tid;
   c.z = step;
-  c.w = (uint32_t)(quad >> 32);
+  c.w = (uint32_t)(ctr >> 32);
   return tam_philox4x32_10(c, seed_lo, seed_hi);
 }
+
+// The eight 24-bit draws of a 192-bit window (six consecutive words w0..w5
+// of a group: words 0..5 for elements 0..7 of the group, words 6..11 for
+// elements 8..15): draw k takes bits [24k, 24k+24) of the window, which for
+// k = 1, 2, 5, 6 run over a word boundary (v_alignbit of the word pair).
+TAM_HD void tam_split24(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3, uint32_t w4, uint32_t w5,
+                        uint32_t* r) {
+  r[0] = w0 & 0xffffffu;
+  r[1] = (uint32_t)((((uint64_t)w1 << 32) | w0) >> 24) & 0xffffffu;
+  r[2] = (uint32_t)((((uint64_t)w2 << 32) | w1) >> 16) & 0xffffffu;
+  r[3] = w2 >> 8;
+  r[4] = w3 & 0xffffffu;
+  r[5] = (uint32_t)((((uint64_t)w4 << 32) | w3) >> 24) & 0xffffffu;
+  r[6] = (uint32_t)((((uint64_t)w5 << 32) | w4) >> 16) & 0xffffffu;
+  r[7] = w5 >> 8;
+}
+
+// The draws of the 8 consecutive elements e0 .. e0+7 (e0 a multiple of 8) of
+// group t = e0/16: half h = (e0/8) % 2 of the group needs blocks 3t + h and
+// 3t + h + 1, a = block 3t + h, b = block 3t + h + 1:
+// h = 0: w0..w5 = a0..a3, b0, b1;  h = 1: w6..w11 = a2, a3, b0..b3.
+TAM_HD void tam_draws8(uint64_t e0, uint32_t tid, uint32_t step, uint32_t seed_lo, uint32_t seed_hi,
+                       uint32_t* r) {
+  const bool h = (e0 >> 3) & 1u;
+  const uint64_t c0 = 3u * (e0 >> 4) + (h ? 1u : 0u);
+  const TamU4 a = tam_philox_block(c0, tid, step, seed_lo, seed_hi);
+  const TamU4 b = tam_philox_block(c0 + 1u, tid, step, seed_lo, seed_hi);
+  tam_split24(h ? a.z : a.x, h ? a.w : a.y, h ? b.x : a.z, h ? b.y : a.w, h ? b.z : b.x, h ? b.w : b.y, r);
+}
+
+// Uniform of a 24-bit draw.
+TAM_HD float tam_u24f(uint32_t d) { return (float)d * 0x1p-24f; }
 
 // ---------------------------------------------------------------------------
 // fp16 / bf16 rounding (round to nearest, ties to even)

@@ -677,10 +677,9 @@ __device__ __forceinline__ void tam_vpath_b(const TamTensor& d, const TamWave& W
   const float C = (-lmn * fnb) * rsp;
   const float KB = K * 0x1p-20f;
   const float CB = __builtin_fmaf(__builtin_fabsf(C), 0x1p-21f, 0x1p-22f);
-  const uint64_t quad0 = W.e0 >> 2;
-  const TamU4 r0 = tam_philox_quad(quad0, d.tensor_id, d.step, seed_lo, seed_hi);
-  const TamU4 r1 = tam_philox_quad(quad0 + 1, d.tensor_id, d.step, seed_lo, seed_hi);
-  const uint32_t rw[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
+  // the lane's 8 draws (24-bit integers)
+  uint32_t rw[TAM_EPL];
+  tam_draws8(W.e0, d.tensor_id, d.step, seed_lo, seed_hi, rw);
   // indices go straight into their bytes (v_cvt_pk_u8_f32 of an integral
   // value in [0, 255]); partial blocks accept per element (lane masks)
   uint32_t ow[2] = {0u, 0u};
@@ -723,7 +722,7 @@ __device__ __forceinline__ void tam_vpath_b(const TamTensor& d, const TamWave& W
     for (int i = 0; i < TAM_EPL; ++i) {
       const float l2 = __builtin_amdgcn_logf(vc[i] * rmin);
       const float ct = __builtin_fmaf(l2, K, 0.5f);
-      const float dd = __builtin_fmaf(-(float)(rw[i] >> 8), 0x1p-24f, ct);  // fl(ct - u), u exact
+      const float dd = __builtin_fmaf(-(float)rw[i], 0x1p-24f, ct);  // fl(ct - u), u exact
       const float q = __builtin_rintf(dd);
       tmax = __builtin_fmaxf(tmax, __builtin_fabsf(dd - q));
       // the exact path overwrites rejected elements
@@ -735,7 +734,7 @@ __device__ __forceinline__ void tam_vpath_b(const TamTensor& d, const TamWave& W
     for (int i = 0; i < TAM_EPL; ++i) {
       const float l2 = __builtin_amdgcn_logf(vc[i]);
       const float ct = __builtin_fmaf(l2, K, C);
-      const float dd = __builtin_fmaf(-(float)(rw[i] >> 8), 0x1p-24f, ct);  // fl(ct - u), u exact
+      const float dd = __builtin_fmaf(-(float)rw[i], 0x1p-24f, ct);  // fl(ct - u), u exact
       const float B = __builtin_fmaf(__builtin_fabsf(l2), KB, __builtin_fmaf(__builtin_fabsf(ct), 0x1p-21f, CB));
       const float q = __builtin_ceilf(dd);
       const float r = q - dd;
@@ -749,7 +748,7 @@ __device__ __forceinline__ void tam_vpath_b(const TamTensor& d, const TamWave& W
 #pragma unroll
     for (int i = 0; i < TAM_EPL; ++i) {
       if (FULL) {  // the element's own test, as in the lane's
-        const float dd = __builtin_fmaf(-(float)(rw[i] >> 8), 0x1p-24f,
+        const float dd = __builtin_fmaf(-(float)rw[i], 0x1p-24f,
                                         __builtin_fmaf(__builtin_amdgcn_logf(vc[i] * rmin), K, 0.5f));
         okv[i] = __builtin_fabsf(dd - __builtin_rintf(dd)) < H;
       }
@@ -758,7 +757,7 @@ __device__ __forceinline__ void tam_vpath_b(const TamTensor& d, const TamWave& W
         const float c = ((l - lmn) / sp) * fnb;  // quantize.py:284-285
         const float f = __builtin_floorf(c);
         const float fr = c - f;
-        const float u = (float)(rw[i] >> 8) * 0x1p-24f;
+        const float u = (float)rw[i] * 0x1p-24f;
         float q = f + (u < fr ? 1.0f : 0.0f);  // quantize.py:288-294
         q = q < 0.0f ? 0.0f : q;
         q = q > fnb - 1.0f ? fnb - 1.0f : q;
@@ -1201,21 +1200,32 @@ __device__ __forceinline__ void tam_vunit_b(const TamTensor& d, uint32_t lane, u
   const bool blk_ok = (tam_u2f(kmn) >= 0x1p-126f) && (tam_u2f(kmx) < 0x1p100f) && !nan_seen && (sp <= 64.0f) &&
                       (Bb < 0.25f);
   const float H = blk_ok ? 0.5f - (Bb + 0x1p-22f) : -1.0f;
-  // the lane's two halves of 8 elements one after the other (8 draws live at a time)
+  // the lane's 16 elements are one group of draws (three Philox blocks): the
+  // two halves of 8 one after the other, the first from blocks 3t and 3t + 1
+  // (words w0..w5), the second from w6, w7 and block 3t + 2
+  const uint64_t c0 = 3u * (e0 >> 4);
+  uint32_t carry0 = 0u, carry1 = 0u;
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const float* vh = v + TAM_EPL * h;
-    const uint64_t quad0 = (e0 >> 2) + 2u * (uint64_t)h;
-    const TamU4 r0 = tam_philox_quad(quad0, d.tensor_id, d.step, seed_lo, seed_hi);
-    const TamU4 r1 = tam_philox_quad(quad0 + 1, d.tensor_id, d.step, seed_lo, seed_hi);
-    const uint32_t rw[TAM_EPL] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
+    uint32_t rw[TAM_EPL];
+    if (h == 0) {
+      const TamU4 a = tam_philox_block(c0, d.tensor_id, d.step, seed_lo, seed_hi);
+      const TamU4 bb = tam_philox_block(c0 + 1u, d.tensor_id, d.step, seed_lo, seed_hi);
+      tam_split24(a.x, a.y, a.z, a.w, bb.x, bb.y, rw);
+      carry0 = bb.z;
+      carry1 = bb.w;
+    } else {
+      const TamU4 c = tam_philox_block(c0 + 2u, d.tensor_id, d.step, seed_lo, seed_hi);
+      tam_split24(carry0, carry1, c.x, c.y, c.z, c.w, rw);
+    }
     uint32_t ow[2] = {0u, 0u};
     float tmax = 0.0f;
 #pragma unroll
     for (int i = 0; i < TAM_EPL; ++i) {
       const float l2 = __builtin_amdgcn_logf(vh[i] * rmin);
       const float ct = __builtin_fmaf(l2, K, 0.5f);
-      const float dd = __builtin_fmaf(-(float)(rw[i] >> 8), 0x1p-24f, ct);  // fl(ct - u), u exact
+      const float dd = __builtin_fmaf(-(float)rw[i], 0x1p-24f, ct);  // fl(ct - u), u exact
       const float q = __builtin_rintf(dd);
       tmax = __builtin_fmaxf(tmax, __builtin_fabsf(dd - q));
       // the exact path overwrites rejected elements
@@ -1225,7 +1235,7 @@ __device__ __forceinline__ void tam_vunit_b(const TamTensor& d, uint32_t lane, u
       // exact path: the reference's own sequence with correctly rounded log and division
 #pragma unroll
       for (int i = 0; i < TAM_EPL; ++i) {
-        const float dd = __builtin_fmaf(-(float)(rw[i] >> 8), 0x1p-24f,
+        const float dd = __builtin_fmaf(-(float)rw[i], 0x1p-24f,
                                         __builtin_fmaf(__builtin_amdgcn_logf(vh[i] * rmin), K, 0.5f));
         if (!(__builtin_fabsf(dd - __builtin_rintf(dd)) < H)) {
           const float vc = vh[i] < 1e-38f ? 1e-38f : vh[i];  // quantize.py:275
@@ -1233,7 +1243,7 @@ __device__ __forceinline__ void tam_vunit_b(const TamTensor& d, uint32_t lane, u
           const float c = ((l - lmn) / sp) * fnb;  // quantize.py:284-285
           const float f = __builtin_floorf(c);
           const float fr = c - f;
-          const float u = (float)(rw[i] >> 8) * 0x1p-24f;
+          const float u = (float)rw[i] * 0x1p-24f;
           float q = f + (u < fr ? 1.0f : 0.0f);  // quantize.py:288-294
           q = q < 0.0f ? 0.0f : q;
           q = q > fnb - 1.0f ? fnb - 1.0f : q;
@@ -2455,11 +2465,7 @@ __global__ __launch_bounds__(TAM_WG) void tam_k_quantize(const float* __restrict
   sp = sp < 1e-10f ? 1e-10f : sp;
   uint32_t rw[TAM_EPL] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
   if (stochastic) {
-    const uint64_t quad0 = W.e0 >> 2;
-    const TamU4 r0 = tam_philox_quad(quad0, tensor_id, step, seed_lo, seed_hi);
-    const TamU4 r1 = tam_philox_quad(quad0 + 1, tensor_id, step, seed_lo, seed_hi);
-    rw[0] = r0.x; rw[1] = r0.y; rw[2] = r0.z; rw[3] = r0.w;
-    rw[4] = r1.x; rw[5] = r1.y; rw[6] = r1.z; rw[7] = r1.w;
+    tam_draws8(W.e0, tensor_id, step, seed_lo, seed_hi, rw);
   }
   const float top = fnb - 0.001f;  // f32(2^bits - 0.001)
 #pragma unroll
@@ -2468,7 +2474,7 @@ __global__ __launch_bounds__(TAM_WG) void tam_k_quantize(const float* __restrict
     float q;
     if (stochastic) {
       const float f = __builtin_floorf(c);
-      const float u = (float)(rw[i] >> 8) * 0x1p-24f;
+      const float u = (float)rw[i] * 0x1p-24f;
       q = f + (u < c - f ? 1.0f : 0.0f);
       q = q < 0.0f ? 0.0f : q;
       q = q > fnb - 1.0f ? fnb - 1.0f : q;
@@ -2495,14 +2501,16 @@ __global__ void tam_k_v_dequantize(const uint8_t* __restrict__ idx, const uint16
   out[i] = tam_expf(lmin + ((float)idx[i] + 0.5f) * inv_nbk * span);
 }
 
+// One thread per 8 elements (half a group of draws).
 __global__ void tam_k_philox_uniforms(uint32_t tid, uint32_t step, uint32_t seed_lo, uint32_t seed_hi,
                                       uint64_t count, float* __restrict__ out) {
-  const uint64_t q = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (q * 4 >= count) return;
-  const TamU4 r = tam_philox_quad(q, tid, step, seed_lo, seed_hi);
-  const uint32_t w[4] = {r.x, r.y, r.z, r.w};
-  for (int k = 0; k < 4; ++k)
-    if (q * 4 + k < count) out[q * 4 + k] = tam_u01(w[k]);
+  const uint64_t e0 = ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8u;
+  if (e0 >= count) return;
+  uint32_t rw[8];
+  tam_draws8(e0, tid, step, seed_lo, seed_hi, rw);
+#pragma unroll
+  for (int k = 0; k < 8; ++k)
+    if (e0 + k < count) out[e0 + k] = tam_u24f(rw[k]);
 }
 
 __global__ void tam_k_math_eval(int fn, const float* __restrict__ in, float* __restrict__ out, uint64_t n) {
@@ -2867,8 +2875,8 @@ int tam_philox_uniforms(uint32_t tensor_id, uint32_t step, uint64_t seed, uint64
   tam_err_buf[0] = 0;
   if (!out) return tam_fail(TAM_E_INVALID, "%snull argument", "");
   if (count == 0) return TAM_OK;
-  const uint64_t quads = (count + 3) / 4;
-  const uint64_t blocks = (quads + 255) / 256;
+  const uint64_t eights = (count + 7) / 8;
+  const uint64_t blocks = (eights + 255) / 256;
   hipLaunchKernelGGL(tam_k_philox_uniforms, dim3((uint32_t)blocks), dim3(256), 0, (hipStream_t)stream,
                      tensor_id, step, (uint32_t)seed, (uint32_t)(seed >> 32), count, out);
   TAM_HIP_CHECK(hipGetLastError());
