@@ -165,19 +165,35 @@ def cpu_baseline(shapes, dtype, kw, log_sigma, budget_s=20.0):
 
 
 # ---------------------------------------------------------------- HBM traffic
-TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "tam_k1_main_c3_fetch_write.md")
+KERNEL_SOURCES = ("tam_step.hip", "tam_math.h", "tam_tables.h")
+
+
+def kernel_source_sha() -> str:
+    """First 16 hex digits of the sha256 over the kernel sources, in order."""
+    import hashlib
+
+    h = hashlib.sha256()
+    for name in KERNEL_SOURCES:
+        with open(os.path.join(ROOT, "turboadam_amd", "csrc", name), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
 
 
 def measured_traffic(workload: str):
     """HBM bytes per pass-0 launch from the committed rocprofv3 FETCH_SIZE /
-    WRITE_SIZE summary (counters scaled by their plain-copy calibration), or
-    None when no summary covers this workload."""
-    if workload != "c3" or not os.path.exists(TRAFFIC_PROFILE):
+    WRITE_SIZE summary of this workload (counters scaled by their plain-copy
+    calibration), or None when no summary covers the workload or the summary
+    was taken on other kernel sources than the ones built here."""
+    path = os.path.join(ROOT, "profiles", f"tam_k1_main_{workload}_fetch_write.md")
+    if not os.path.exists(path):
         return None
-    for line in open(TRAFFIC_PROFILE):
-        if line.startswith("traffic_bytes_per_launch"):
-            return float(line.split("=")[1])
-    return None
+    sha, traffic = None, None
+    for line in open(path):
+        if line.startswith("Kernel sources") and "`" in line:
+            sha = line.split("`")[1]
+        elif line.startswith("traffic_bytes_per_launch"):
+            traffic = float(line.split("=")[1])
+    return traffic if sha == kernel_source_sha() else None
 
 
 # ---------------------------------------------------------------- copy reference
@@ -393,7 +409,8 @@ def main():
             "unit": "GB/s",
             "frac": k1_gbps / HBM_PEAK_GBPS,
             "traffic": measured_traffic(args.workload),
-            "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE x2.0 + WRITE_SIZE x1.0)",
+            "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE x2.0 + WRITE_SIZE x1.0, "
+                            "from the profile of these kernel sources; null if none)",
             "ms_per_launch": k1_avg,
             "launches_timed": len(k1_ms),
             "bytes_alg_per_launch": k1_bytes,
