@@ -20,6 +20,9 @@
  * 384 bits of the blocks with counters (3t + j, tensor_id, step, (3t+j)>>32),
  * j = 0..2, key seed, little endian; element 16t + k takes bits
  * [24k, 24k+24), u = that integer * 2^-24.  Compiled with -ffp-contract=off.
+ * Loops over independent blocks or elements run under OpenMP; each iteration
+ * writes its own outputs and every reduction runs in its fixed order after
+ * the loop, so results do not depend on the thread count.
  */
 #include <math.h>
 #include <stdint.h>
@@ -184,6 +187,7 @@ static void st(void* p, int dtype, uint64_t i, float v) {
 /* decode_blocks, reference costate.py:261-324 (m_hat = alpha*g + scale*sign). */
 void or_decode_blocks(const uint8_t* labels, const uint8_t* signs, const float* norms, const uint16_t* amp,
                       float alpha, const float* g, uint64_t n, float q, float* m_hat) {
+#pragma omp parallel for schedule(static)
   for (uint64_t i = 0; i < n; ++i) {
     uint64_t b = i / OR_BS;
     float s = 0.0f;
@@ -226,6 +230,7 @@ float or_decompose(const float* m, const float* g, uint64_t n, float* delta) {
   uint64_t nb = (n + OR_BS - 1) / OR_BS;
   double* bgg = (double*)malloc(nb * sizeof(double));
   double* bmg = (double*)malloc(nb * sizeof(double));
+#pragma omp parallel for schedule(static)
   for (uint64_t b = 0; b < nb; ++b) {
     bgg[b] = block_dot(g, g, n, b);
     bmg[b] = block_dot(m, g, n, b);
@@ -235,6 +240,7 @@ float or_decompose(const float* m, const float* g, uint64_t n, float* delta) {
   free(bgg);
   free(bmg);
   float alpha = gg > 0.0f ? mg / gg : 0.0f;        /* :39-41 */
+#pragma omp parallel for schedule(static)
   for (uint64_t i = 0; i < n; ++i) {
     float ag = alpha * g[i];
     delta[i] = m[i] - ag;                          /* :42 */
@@ -251,6 +257,7 @@ static float block_norm(const float* x, uint64_t n, uint64_t b) {
 /* compute_block_ratios, reference costate.py:51-86. */
 void or_block_ratios(const float* delta, const float* m, uint64_t n, float* ratios) {
   uint64_t nb = (n + OR_BS - 1) / OR_BS;
+#pragma omp parallel for schedule(static)
   for (uint64_t b = 0; b < nb; ++b) {
     float dn = block_norm(delta, n, b);
     float mn = block_norm(m, n, b);
@@ -287,12 +294,14 @@ void or_classify(const float* ratios, uint64_t nb, float tau0, float tau1, uint8
 /* encode_blocks, reference costate.py:213-258 (+ _pack_signs :157-182). */
 void or_encode(const float* delta, uint64_t n, float q, uint8_t* signs, float* norms, uint16_t* amp) {
   uint64_t nb = (n + OR_BS - 1) / OR_BS;
+#pragma omp parallel for schedule(static)
   for (uint64_t b = 0; b < nb; ++b) {
     float nd = block_norm(delta, n, b);
     norms[b] = nd;
     amp[b] = or_f32_to_f16(nd / q);
   }
   uint64_t nbytes = (n + 7) / 8;
+#pragma omp parallel for schedule(static)
   for (uint64_t j = 0; j < nbytes; ++j) {
     uint32_t byte = 0;
     for (int k = 0; k < 8; ++k) {
@@ -318,6 +327,7 @@ void or_costate_update_ef(const float* g, uint64_t n, float beta1, float one_min
   uint64_t nb = (n + OR_BS - 1) / OR_BS;
   float* m_hat = (float*)calloc(n, sizeof(float));
   if (has_state) or_decode_blocks(labels, signs, norms, amp, *alpha, g, n, q, m_hat);
+#pragma omp parallel for schedule(static)
   for (uint64_t i = 0; i < n; ++i) {
     float gc = (ef && has_ef) ? g[i] + ef_residual[i] : g[i];  /* :410-413 */
     float a = beta1 * m_hat[i];
@@ -335,6 +345,7 @@ void or_costate_update_ef(const float* g, uint64_t n, float beta1, float one_min
   *alpha = al;
   if (ef) {                                        /* :428-437 */
     or_decode_blocks(labels, signs, norms, amp, 0.0f, g, n, q, m_hat);
+#pragma omp parallel for schedule(static)
     for (uint64_t i = 0; i < n; ++i) {
       float e = delta[i] - m_hat[i];
       if (has_ef) {
@@ -367,8 +378,9 @@ static void or_fused_v_update_at(uint8_t* idx, uint16_t* scales, const float* g,
                                  uint64_t e_base, float* v_out) {
   uint64_t nb = (n + OR_BS - 1) / OR_BS;
   float nbk = (float)(1u << bits);
-  float vb[OR_BS], lg[OR_BS];
+#pragma omp parallel for schedule(static)
   for (uint64_t b = 0; b < nb; ++b) {
+    float vb[OR_BS], lg[OR_BS];
     float lmin = or_f16_to_f32(scales[2 * b]);
     float lmax = or_f16_to_f32(scales[2 * b + 1]);
     float span = lmax - lmin;                      /* :253-255 */
@@ -427,6 +439,7 @@ void or_fused_v_update(uint8_t* idx, uint16_t* scales, const float* g, uint64_t 
  * (the division by 2^bits is exact), exp correctly rounded. */
 void or_dequantize(const uint8_t* idx, const uint16_t* scales, uint64_t n, int bits, float* out) {
   float nbk = (float)(1u << bits);
+#pragma omp parallel for schedule(static)
   for (uint64_t i = 0; i < n; ++i) {
     uint64_t b = i / OR_BS;
     float lmin = or_f16_to_f32(scales[2 * b]);
@@ -446,8 +459,9 @@ void or_quantize_logscale(const float* v, uint64_t npad, int bits, int stochasti
   uint64_t nb = npad / OR_BS;
   float nbk = (float)(1u << bits);
   float top = (float)((double)(1u << bits) - 0.001);  /* clamp(0, n_buckets - 0.001), :179 */
-  float lg[OR_BS];
+#pragma omp parallel for schedule(static)
   for (uint64_t b = 0; b < nb; ++b) {
+    float lg[OR_BS];
     float lmin = INFINITY, lmax = -INFINITY;
     int nan_seen = 0;
     for (int j = 0; j < OR_BS; ++j) {
@@ -496,17 +510,20 @@ void or_step_tensor(OrTensor* t, uint64_t seed) {
   float* p = (float*)malloc(n * sizeof(float));
   float* m = (float*)malloc(n * sizeof(float));
   float* v = (float*)malloc(n * sizeof(float));
+#pragma omp parallel for schedule(static)
   for (uint64_t i = 0; i < n; ++i) {
     g[i] = ld(t->grad, (int)t->dtype, i);
     p[i] = ld(t->param, (int)t->dtype, i);
   }
   if (t->flags & OR_FLAG_WD)                        /* :106-107 */
+#pragma omp parallel for schedule(static)
     for (uint64_t i = 0; i < n; ++i) p[i] = round_p(p[i] * t->c_wd, (int)t->dtype);
   if (t->flags & OR_FLAG_COSTATE) {                 /* :110-111 */
     or_costate_update_ef(g, n, t->beta1, t->one_minus_beta1, t->sqrt_block, t->k_lo, t->k_hi,
                          (t->flags & OR_FLAG_HAS_STATE) != 0, t->labels, t->signs, t->norms, t->amp, t->alpha,
                          (t->flags & OR_FLAG_EF) != 0, (t->flags & OR_FLAG_HAS_EF) != 0, t->ef_residual, m);
   } else {                                          /* :113-114 */
+#pragma omp parallel for schedule(static)
     for (uint64_t i = 0; i < n; ++i) {
       float a = t->exp_avg[i] * t->beta1;
       t->exp_avg[i] = fmaf(t->one_minus_beta1, g[i], a);
@@ -517,6 +534,7 @@ void or_step_tensor(OrTensor* t, uint64_t seed) {
     or_fused_v_update_at(t->v_idx, t->v_scales, g, n, (int)t->v_bits, t->beta2, t->one_minus_beta2, t->tensor_id,
                          t->step, seed, (uint64_t)t->block0 * OR_BS, v);
   } else {                                          /* :165-167 */
+#pragma omp parallel for schedule(static)
     for (uint64_t i = 0; i < n; ++i) {
       float a = t->exp_avg_sq[i] * t->beta2;
       float b = t->one_minus_beta2 * g[i];
@@ -524,6 +542,7 @@ void or_step_tensor(OrTensor* t, uint64_t seed) {
       v[i] = t->exp_avg_sq[i];
     }
   }
+#pragma omp parallel for schedule(static)
   for (uint64_t i = 0; i < n; ++i) {
     float vq = v[i] / t->bias_correction2;          /* :163 */
     float den = sqrtf(vq) + t->eps;

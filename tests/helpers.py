@@ -151,19 +151,37 @@ def run_side_by_side(sizes, dts, steps, seed=0, check_every=1, shapes=None, grad
         orc.step(grads)
         if (s + 1) % check_every == 0 or s == steps - 1:
             torch.cuda.synchronize()
-            for i, p in enumerate(g_params):
-                if i not in orc.state:
-                    continue
-                where = f"step {s + 1} tensor {i} (n={sizes[i]})"
-                pa = from_torch(p.data)
-                pb = o_params[i]
-                if not np.array_equal(pa.view(np.uint32) if pa.dtype == np.float32 else pa,
-                                      pb.view(np.uint32) if pb.dtype == np.float32 else pb):
-                    nd = int(np.count_nonzero(pa != pb))
-                    bad.append(f"{where}: param differs in {nd}/{pa.size}")
-                bad += compare_states(gpu_state(opt, p), orc.state[i], where)
+            bad += compare_with_oracle(opt, g_params, orc, o_params, f"step {s + 1}", sizes)
             if bad:
                 return bad
+    return bad
+
+
+def _bits_of(a: np.ndarray) -> np.ndarray:
+    return a.view(np.uint32) if a.dtype == np.float32 else a
+
+
+def compare_with_oracle(opt, params, orc, o_params, where: str, sizes=None) -> list:
+    """Parameters, every state array and the step counters of a GPU TurboAdam
+    against the oracle's, bit for bit (the GPU's device-side step counters of
+    a capturable group included); returns a list of mismatch descriptions."""
+    bad = []
+    for i, p in enumerate(params):
+        w = f"{where} tensor {i}" + (f" (n={sizes[i]})" if sizes is not None else "")
+        pa, pb = from_torch(p.data), o_params[i]
+        if not np.array_equal(_bits_of(pa), _bits_of(pb)):
+            nd = int(np.count_nonzero(_bits_of(pa) != _bits_of(pb)))
+            bad.append(f"{w}: param differs in {nd}/{pa.size}")
+        if i not in orc.state:
+            if p in opt.state and int(opt.state[p]["step"]) != 0:
+                bad.append(f"{w}: stepped on the GPU, never in the oracle")
+            continue
+        if p not in opt.state:
+            bad.append(f"{w}: no GPU state")
+            continue
+        if int(opt.state[p]["step"]) != int(orc.state[i]["step"]):
+            bad.append(f"{w}: step {int(opt.state[p]['step'])} vs oracle {orc.state[i]['step']}")
+        bad += compare_states(gpu_state(opt, p), orc.state[i], w)
     return bad
 
 

@@ -8,7 +8,9 @@ For capturable groups the skip happens on the device: a captured step replays
 as a skip whenever found_inf is nonzero, counters included.  Gradients are
 fp32: GradScaler's unscale op has no bf16 kernel on this torch build (it
 raises for bf16 gradients before the optimizer is reached, with or without
-this protocol).
+this protocol).  The oracle steps on the unscaled gradients of the steps
+that are not skipped (scales are powers of two, so unscaling is exact) and
+must equal both flows bit for bit.
 """
 
 import numpy as np
@@ -16,7 +18,7 @@ import pytest
 import torch
 
 from oracle import oracle as O
-from tests.helpers import compare_states, from_torch, gpu_state, log, to_bits, to_torch
+from tests.helpers import compare_states, compare_with_oracle, from_torch, gpu_state, log, to_bits, to_torch
 
 pytestmark = pytest.mark.gpu
 
@@ -62,6 +64,8 @@ def test_grad_scaler_protocol_equals_default_flow():
     opt_a = TurboAdam(pa, **kw)
     opt_b = TurboAdam(pb, **kw)
     opt_b._step_supports_amp_scaling = False  # GradScaler: unscale_, host check, skip
+    oparams = [a.copy() for a in init]
+    orc = O.OracleTurboAdam(oparams, dtypes=dts, seed=5, lr=1e-3, weight_decay=0.05)
     sc_a = torch.amp.GradScaler("cuda", init_scale=2.0 ** 12, growth_interval=2)
     sc_b = torch.amp.GradScaler("cuda", init_scale=2.0 ** 12, growth_interval=2)
     one = torch.ones((), device=dev)
@@ -80,9 +84,12 @@ def test_grad_scaler_protocol_equals_default_flow():
         sc_a.update()
         sc_b.step(opt_b)
         sc_b.update()
+        if s not in (1, 4):
+            orc.step([to_bits(g, dt) for g, dt in zip(gs, dts)])
         torch.cuda.synchronize()
         log(f"amp step {s + 1}: scale {scale}")
         bad = _compare(opt_a, pa, opt_b, pb, f"step {s + 1}")
+        bad += compare_with_oracle(opt_a, pa, orc, oparams, f"step {s + 1} vs oracle", sizes)
         assert not bad, "\n".join(bad[:20])
 
 
@@ -97,6 +104,8 @@ def test_captured_step_skips_on_device_when_found_inf():
     cap = TurboAdam(pc, capturable=True, **kw)
     eager = TurboAdam(pe, **kw)
     eager._step_supports_amp_scaling = False
+    oparams = [a.copy() for a in init]
+    orc = O.OracleTurboAdam(oparams, dtypes=dts, seed=6, lr=1e-3, weight_decay=0.05)
     scale = torch.full((), 2.0 ** 8, dtype=torch.float32, device=dev)
     found = torch.zeros((), dtype=torch.float32, device=dev)
     static = [torch.zeros(n, dtype=p.dtype, device=dev) for n, p in zip(sizes, pc)]
@@ -116,6 +125,7 @@ def test_captured_step_skips_on_device_when_found_inf():
         torch._amp_foreach_non_finite_check_and_unscale_([p.grad for p in pe], torch.zeros(1, device=dev), inv)
         if not skips[s]:
             eager.step()
+            orc.step([to_bits(g, dt) for g, dt in zip(grads[s], dts)])
 
     cap.grad_scale, cap.found_inf = scale, found
     side = torch.cuda.Stream()
@@ -128,7 +138,7 @@ def test_captured_step_skips_on_device_when_found_inf():
     for s in range(2):
         eager_step(s)
     torch.cuda.synchronize()
-    bad = _compare(cap, pc, eager, pe, "warm-up")
+    bad = _compare(cap, pc, eager, pe, "warm-up") + compare_with_oracle(cap, pc, orc, oparams, "warm-up vs oracle")
     assert not bad, "\n".join(bad[:20])
     graph = torch.cuda.CUDAGraph()
     set_static(2)
@@ -143,5 +153,6 @@ def test_captured_step_skips_on_device_when_found_inf():
         torch.randn(1 << 20, device=dev).sum().item()  # eager work between replays
         log(f"replay {s - 1}: skip={skips[s]}")
         bad = _compare(cap, pc, eager, pe, f"replay {s - 1}")
+        bad += compare_with_oracle(cap, pc, orc, oparams, f"replay {s - 1} vs oracle", sizes)
         assert not bad, "\n".join(bad[:20])
     del cap.grad_scale, cap.found_inf

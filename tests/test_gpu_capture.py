@@ -4,8 +4,10 @@ With capturable=True the step's first launch takes the step number, the bias
 corrections and the has-state flags from device counters, so one captured
 step() replays as a real step each time.  Every replay, with new gradients
 copied into the captured gradient tensors and eager work and synchronisations
-between replays, must equal an eager optimizer's step bit for bit: parameters,
-every state array and the step counters.
+between replays, must equal an eager optimizer's step and the CPU oracle's bit for
+bit: parameters, every state array and the step counters (the device prologue's
+step numbers, shared bias corrections and has-state flags are thereby checked
+against the reference's host logic as the oracle restates it).
 """
 
 import numpy as np
@@ -13,7 +15,7 @@ import pytest
 import torch
 
 from oracle import oracle as O
-from tests.helpers import compare_states, from_torch, gpu_state, log, to_bits, to_torch
+from tests.helpers import compare_states, compare_with_oracle, from_torch, gpu_state, log, to_bits, to_torch
 
 pytestmark = pytest.mark.gpu
 
@@ -49,6 +51,11 @@ def test_captured_step_replays_equal_eager_steps():
     eager = TurboAdam(groups(pe), **kw)
     cap = TurboAdam(groups(pc), capturable=True, **kw)
     static = [torch.zeros_like(p) for p in pc]
+    oparams = [a.copy() for a in init]
+    orc = O.OracleTurboAdam(groups(oparams), dtypes=dts, seed=777, lr=1e-3, weight_decay=0.05)
+
+    def step_oracle(s):
+        orc.step([None if (i == late and s == 0) else g for i, g in enumerate(grads[s])])
 
     def set_eager(s):
         for i, (p, g, dt, n) in enumerate(zip(pe, grads[s], dts, sizes)):
@@ -68,7 +75,7 @@ def test_captured_step_replays_equal_eager_steps():
                 bad += compare_states(gpu_state(cap, b), gpu_state(eager, a), f"{where} tensor {i}")
                 if int(cap.state[b]["step"].item()) != eager.state[a]["step"]:
                     bad.append(f"{where} tensor {i}: step counter differs")
-        return bad
+        return bad + compare_with_oracle(cap, pc, orc, oparams, f"{where} vs oracle", sizes)
 
     # warm-up (eager) steps of the capturable optimizer on a side stream
     side = torch.cuda.Stream()
@@ -81,6 +88,7 @@ def test_captured_step_replays_equal_eager_steps():
     for s in range(2):
         set_eager(s)
         eager.step()
+        step_oracle(s)
     torch.cuda.synchronize()
     bad = compare("warm-up")
     assert not bad, "\n".join(bad[:20])
@@ -96,6 +104,7 @@ def test_captured_step_replays_equal_eager_steps():
         graph.replay()
         set_eager(s)
         eager.step()
+        step_oracle(s)
         torch.cuda.synchronize()
         # eager work of the program's own between replays
         torch.randn(1 << 20, device=dev).sum().item()

@@ -23,7 +23,7 @@ import torch
 
 import bench
 from oracle import oracle as O
-from tests.helpers import compare_states, f16_bits, from_torch, gpu_state, log
+from tests.helpers import compare_states, compare_with_oracle, f16_bits, from_torch, gpu_state, log
 
 pytestmark = pytest.mark.gpu
 
@@ -70,12 +70,14 @@ def _compare_spot(opt, params, orc, spot, where):
 
 def test_llama3_8b_shaped_full_steps():
     """Config C3: all 291 bf16 tensors (8.03e9 params) stepped on the GPU;
-    four of them (both norm shapes, a k and a q projection) against the oracle."""
+    five of them against the oracle: both norm shapes, a k and a q projection,
+    and the 525M-parameter embedding (4.1M blocks: the multi-chunk alpha
+    reduction and the multi-slice threshold selection at their largest)."""
     from turboadam_amd import TurboAdam
 
     shapes = bench.llama3_8b_shapes()
     names = [s[0] for s in shapes]
-    spot = [names.index(k) for k in ("l0.norm1", "l0.k", "l31.q", "norm")]
+    spot = [names.index(k) for k in ("embed", "l0.norm1", "l0.k", "l31.q", "norm")]
     log(f"C3 full size: {len(shapes)} tensors, spot checks {[names[i] for i in spot]}")
     dev = torch.device("cuda:0")
     gen = torch.Generator(device=dev)
@@ -107,6 +109,45 @@ def test_llama3_8b_shaped_full_steps():
         log(f"  step {step + 1}: GPU step done, oracle spot checks {'ok' if not bad else 'FAILED'}")
     bad += _invariants(opt, params, 4)
     assert not bad, "\n".join(bad[:20])
+
+
+def test_gpt2_block_200_steps():
+    """Config C0 as specified: one GPT-2-small block in fp32 (12 tensors,
+    7,087,872 params; LayerNorm weights 1, the rest N(0, 0.02)), gradients
+    N(0, s_t^2) with s_t ~ LogNormal(ln 1e-3, 1) per tensor plus a persistent
+    drift direction of 0.3 s_t, v_bits 4, lr 6e-4, wd 0.01: 200 steps on the
+    GPU, every tensor against the oracle bit for bit every 20 steps."""
+    from turboadam_amd import TurboAdam
+
+    shapes = bench.gpt2_block_shapes()
+    log(f"C0: {len(shapes)} tensors, 200 steps")
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(17)
+    params = []
+    for name, shp in shapes:
+        t = torch.ones(shp, device=dev) if name.startswith("ln_") and name.endswith(".w") else \
+            torch.empty(shp, device=dev).normal_(0.0, 0.02, generator=gen)
+        params.append(torch.nn.Parameter(t))
+    kw = dict(lr=6e-4, weight_decay=0.01, v_bits=4)
+    opt = TurboAdam(params, philox_seed=SEED, **kw)
+    oparams = [from_torch(p) for p in params]
+    orc = O.OracleTurboAdam(oparams, seed=SEED, **kw)
+    sig = np.exp(math.log(1e-3) + np.random.default_rng(3).standard_normal(len(shapes)))
+    drift = [torch.randn(shp, device=dev, generator=gen) for _, shp in shapes]
+    for step in range(200):
+        for i, p in enumerate(params):
+            z = torch.randn(p.shape, device=dev, generator=gen)
+            p.grad = (z + 0.3 * drift[i]) * float(sig[i])
+        grads = [from_torch(p.grad) for p in params]
+        opt.step()
+        orc.step(grads)
+        if (step + 1) % 20 == 0:
+            torch.cuda.synchronize()
+            bad = compare_with_oracle(opt, params, orc, oparams, f"step {step + 1}")
+            log(f"  step {step + 1}: {'ok' if not bad else 'FAILED'}")
+            assert not bad, "\n".join(bad[:20])
+    assert all(int(opt.state[p]["step"]) == 200 for p in params)
 
 
 def test_v_only_2_28_full_steps_sliced():

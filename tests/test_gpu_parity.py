@@ -2,9 +2,9 @@
 
 Bar: bit-exact for every packed-state byte (1Q indices, fp16 scales, sign
 bits, labels, fp16 amplitudes), for block norms, alpha and parameters, on
-identical inputs and Philox draws.  Sizes are small enough for the scalar
-oracle to finish in seconds; full-size configurations are covered by the
-size-independent checks in test_gpu_invariants.py.
+identical inputs and Philox draws.  Sizes are small enough for the CPU
+oracle to finish in seconds; the benchmark configurations at full size are in
+test_gpu_fullsize.py.
 """
 
 import math
