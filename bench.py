@@ -122,46 +122,114 @@ def bytes_per_param(dtype_bytes: int, costate: bool, compress_v: bool = True, ef
 
 
 # ---------------------------------------------------------------- CPU baseline
-def cpu_baseline(shapes, dtype, kw, log_sigma, budget_s=20.0):
-    """Time the reference's CPU step on a bounded sample of the workload.
+FULL_SAMPLE_MAX = 300_000_000  # workloads up to this many parameters run whole on the CPU
+ONE_THREAD_PARAMS = 16_000_000
+
+
+def cpu_info():
+    """CPU model, logical CPUs online, and the CPUs this process may run on."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:
+        usable = os.cpu_count() or 1
+    return model, os.cpu_count() or 1, usable
+
+
+def cpu_sample(shapes, with_embeddings=False):
+    """The tensors the CPU baseline steps: the whole workload when it has at
+    most FULL_SAMPLE_MAX parameters, otherwise its first decoder layer (the
+    32 identical layers hold 87% of the 8B-shaped set's parameters) and, with
+    with_embeddings, the embedding and the output head as well; in workload
+    order."""
+    total = sum(math.prod(shp) for _, shp in shapes)
+    if total <= FULL_SAMPLE_MAX:
+        return list(shapes), False
+    keep = [(n, shp) for n, shp in shapes if n.startswith("l0.") or (with_embeddings and n in ("embed", "lm_head"))]
+    return (keep or list(shapes[:1])), True
+
+
+def _time_mirror(TM, shapes, dtype, kw, log_sigma, threads, min_steps, budget_s, gen):
+    """Median seconds of the steady-state steps (second and later) of the
+    reference's CPU step over the given shapes; gradients are drawn outside
+    the timed region."""
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        params = [(torch.randn(shp, generator=gen) * 0.02).to(dtype) for _, shp in shapes]
+        sig = [math.exp(log_sigma + float(torch.randn((), generator=gen))) for _ in shapes]
+        opt = TM.MirrorTurboAdam(params, ops=TM.FaithfulOps, seed=1, **kw)
+        times = []
+        t_end = time.perf_counter() + budget_s
+        while len(times) < min_steps or (time.perf_counter() < t_end and len(times) < 6):
+            grads = [(torch.randn(p.shape, generator=gen) * s).to(dtype) for p, s in zip(params, sig)]
+            t0 = time.perf_counter()
+            opt.step(grads)
+            times.append(time.perf_counter() - t0)
+            del grads
+        return float(np.median(times[1:])), len(times)
+    finally:
+        torch.set_num_threads(prev)
+
+
+def cpu_baseline(shapes, dtype, kw, log_sigma, budget_s=20.0, with_embeddings=False):
+    """The reference's CPU step timed on this host (BASELINE's CPU plan).
 
     Runs oracle/torch_mirror.py in faithful mode -- the reference CPU path
     restated op for op in torch (it reproduces the reference's outputs bit for
-    bit, tests/test_golden.py) -- on the host cores, with the same parameter
-    shapes and dtype, on the workload's tensors in order (skipping any above
-    20M parameters) until about 20M parameters.
+    bit, tests/test_golden.py) -- on cpu_sample(shapes) with every CPU this
+    process may use (at most OMP_NUM_THREADS when that is set), median of the
+    steady-state steps.  The per-step cost is linear in the parameter count, so
+    a sampled workload's whole step is extrapolated as params / rate.  A
+    1-thread figure is taken on the sample's first tensors up to
+    ONE_THREAD_PARAMS parameters (a leading 1-D slice of the first tensor when
+    that alone is larger).
     """
     from oracle import torch_mirror as TM
 
-    threads = max(1, min(16, os.cpu_count() or 1))
-    prev = torch.get_num_threads()
-    torch.set_num_threads(threads)
+    model, online, usable = cpu_info()
+    threads = usable
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+        threads = max(1, min(threads, int(os.environ["OMP_NUM_THREADS"])))
     gen = torch.Generator().manual_seed(7)
-    sample, total = [], 0
-    for name, shp in shapes:
-        n = int(np.prod(shp))
-        if n > 20_000_000:
-            continue
-        sample.append((name, shp))
-        total += n
-        if total >= 20_000_000:
+    sample, sampled = cpu_sample(shapes, with_embeddings)
+    n_sample = sum(math.prod(shp) for _, shp in sample)
+    n_all = sum(math.prod(shp) for _, shp in shapes)
+    t, steps = _time_mirror(TM, sample, dtype, kw, log_sigma, threads, 2, budget_s, gen)
+
+    one, n_one = [], 0
+    for name, shp in sample:
+        n = math.prod(shp)
+        if n_one + n > 2 * ONE_THREAD_PARAMS:
+            if not one:
+                one, n_one = [(name + "[:%d]" % ONE_THREAD_PARAMS, (ONE_THREAD_PARAMS,))], ONE_THREAD_PARAMS
             break
-    params = [(torch.randn(shp, generator=gen) * 0.02).to(dtype) for _, shp in sample]
-    opt = TM.MirrorTurboAdam(params, ops=TM.FaithfulOps, seed=1, **kw)
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while len(times) < 2 or (time.perf_counter() < t_end and len(times) < 6):
-        grads = [(torch.randn(p.shape, generator=gen) * math.exp(log_sigma)).to(dtype) for p in params]
-        t0 = time.perf_counter()
-        opt.step(grads)
-        times.append(time.perf_counter() - t0)
-    torch.set_num_threads(prev)
-    t = float(np.median(times[1:]))
-    names = ", ".join(n for n, _ in sample[:4])
-    return {"value": total / t, "unit": "params/s", "cores": threads, "kind": "port",
-            "sample": f"{len(sample)} tensors of the workload ({names}; {total} params, {str(dtype)[6:]}), "
-                      f"{len(times)} steps, median of steps 2+; reference CPU step restated in torch ops "
-                      f"(faithful mirror, bit-identical to the reference), {threads} threads"}
+        one.append((name, shp))
+        n_one += n
+        if n_one >= ONE_THREAD_PARAMS:
+            break
+    t1, steps1 = _time_mirror(TM, one, dtype, kw, log_sigma, 1, 2, budget_s / 2, gen)
+
+    names = ", ".join(n for n, _ in sample[:3]) + (", ..." if len(sample) > 3 else "")
+    part = "first decoder layer + embed + lm_head" if with_embeddings else "first decoder layer"
+    how = (f"{part} ({len(sample)} tensors: {names}; {n_sample} of {n_all} params), "
+           f"whole-step time extrapolated by parameter count" if sampled else
+           f"the whole workload ({len(sample)} tensors, {n_sample} params)")
+    return {"value": n_sample / t, "unit": "params/s", "cores": threads, "kind": "port",
+            "sample": f"{how}, {str(dtype)[6:]}; {steps} steps, median of steps 2+; reference CPU step restated "
+                      f"in torch ops (faithful mirror, bit-identical to the reference), {threads} threads",
+            "ms_per_step_workload": n_all / (n_sample / t) * 1e3,
+            "one_thread": {"value": n_one / t1, "unit": "params/s", "steps": steps1,
+                           "sample": ", ".join(n for n, _ in one) + f" ({n_one} params)"},
+            "cpu_model": model, "cpus_online": online, "cpus_usable": usable}
 
 
 # ---------------------------------------------------------------- HBM traffic
@@ -283,6 +351,11 @@ def main():
                     help="extra steps after the timed region, issued pass by pass, that time pass 0")
     ap.add_argument("--stream-rounds", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-with-embeddings", action="store_true",
+                    help="include the embedding and output head in a sampled workload's CPU baseline "
+                         "(several minutes of CPU time on the 8B-shaped set)")
+    ap.add_argument("--cpu-baseline-only", action="store_true",
+                    help="time only the CPU baseline of the workload (no GPU work)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the optimizer step is single-device); "
@@ -300,6 +373,10 @@ def main():
         return
     shapes_fn, dtype, kw, log_sigma, desc = WORKLOADS[args.workload]
     shapes = shapes_fn()
+    if args.cpu_baseline_only:
+        print(json.dumps({"workload": desc, "cpu_baseline": cpu_baseline(
+            shapes, dtype, kw, log_sigma, with_embeddings=args.cpu_with_embeddings)}), flush=True)
+        return
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     gen = torch.Generator(device=dev)
@@ -417,7 +494,7 @@ def main():
         },
     }
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(shapes, dtype, kw, log_sigma)
+        out["cpu_baseline"] = cpu_baseline(shapes, dtype, kw, log_sigma, with_embeddings=args.cpu_with_embeddings)
     print(json.dumps(out), flush=True)
 
 

@@ -56,3 +56,29 @@ def test_more_than_one_gpu_is_refused():
                          text=True, timeout=300, cwd=ROOT)
     assert res.returncode == 2
     assert "one GPU" in res.stderr
+
+
+def test_cpu_baseline_sample():
+    # workloads up to 300M parameters run whole; the 8B-shaped set samples its first decoder layer
+    for name in ("c0", "c1", "c2", "c4"):
+        shapes = bench.WORKLOADS[name][0]()
+        assert bench.cpu_sample(shapes) == (list(shapes), False)
+    sample, sampled = bench.cpu_sample(bench.llama3_8b_shapes())
+    assert sampled and [n for n, _ in sample] == [f"l0.{k}" for k in
+                                                   ("q", "k", "v", "o", "gate", "up", "down", "norm1", "norm2")]
+    assert _count(sample)[1] == 218_112_000
+    sample, _ = bench.cpu_sample(bench.llama3_8b_shapes(), with_embeddings=True)
+    assert [n for n, _ in sample][0] == "embed" and [n for n, _ in sample][-1] == "lm_head"
+    assert _count(sample) == (11, 218_112_000 + 2 * 128256 * 4096)
+
+
+def test_kernel_source_sha_gates_the_traffic_figure():
+    # a profile summary names the kernel sources it measured; another build reads null
+    for name in ("c1", "c2", "c3", "c4"):
+        path = os.path.join(ROOT, "profiles", f"tam_k1_main_{name}_fetch_write.md")
+        if not os.path.exists(path):
+            continue
+        sha = [ln.split("`")[1] for ln in open(path) if ln.startswith("Kernel sources")][0]
+        t = bench.measured_traffic(name)
+        assert (t is not None) == (sha == bench.kernel_source_sha())
+    assert bench.measured_traffic("c0") is None

@@ -1,14 +1,8 @@
-"""Block helpers (reference src/turboadam/utils.py:18-53)."""
+"""Block helpers the 1Q initialisation uses (reference src/turboadam/utils.py:27-53)."""
 
 import torch
 
 BLOCK_SIZE = 128
-MATRIX_NUMEL_THRESHOLD = 10_000
-
-
-def is_matrix_param(param: torch.Tensor) -> bool:
-    """Whether the reference would route param to its matrix path (utils.py:22-24)."""
-    return param.ndim >= 2 and param.numel() > MATRIX_NUMEL_THRESHOLD
 
 
 def pad_to_blocks(tensor: torch.Tensor, block_size: int = BLOCK_SIZE, pad_value: float = 0.0):
@@ -24,11 +18,6 @@ def pad_to_blocks(tensor: torch.Tensor, block_size: int = BLOCK_SIZE, pad_value:
         return tensor, original_length
     fill = tensor.new_full((block_size - remainder,), pad_value)
     return torch.cat([tensor, fill]), original_length
-
-
-def unpad_from_blocks(padded: torch.Tensor, original_length: int) -> torch.Tensor:
-    """Strip the padding added by pad_to_blocks (utils.py:56-67)."""
-    return padded[:original_length]
 
 
 def num_blocks(n: int, block_size: int = BLOCK_SIZE) -> int:
