@@ -316,6 +316,14 @@ __device__ __forceinline__ uint32_t tam_block_or(uint32_t v) {
 // is sunk below the first use of another (each would then wait on its own).
 __device__ __forceinline__ void tam_compiler_fence() { asm volatile("" ::: "memory"); }
 
+// Value barrier: the compiler treats x as rewritten here, so no computation on
+// x moves above this point.  Pinning every loaded value after a fence keeps the
+// compiler from interleaving arithmetic on early loads with the issue of later
+// ones (each such use would wait on its load before the later loads issue).
+__device__ __forceinline__ void tam_pin(uint32_t& x) { asm volatile("" : "+v"(x)); }
+__device__ __forceinline__ void tam_pin(float& x) { asm volatile("" : "+v"(x)); }
+__device__ __forceinline__ void tam_pin(TamW4& x) { asm volatile("" : "+v"(x)); }
+
 // Orders this wave's LDS accesses before and after the call (LDS operations of
 // one wave execute in order, so no s_barrier is needed between lanes of a wave).
 __device__ __forceinline__ void tam_wave_lds_sync() {
@@ -1260,29 +1268,33 @@ __device__ __forceinline__ void tam_vunit_b(const TamTensor& d, uint32_t lane, u
 // One wave's unit: loads, first moment (CoState or fp32), second moment (1Q or
 // fp32), update, store; for CoState tensors the partial sums of g.g and m.g of
 // the unit's two quarters (part: quarter 2u's {g.g, m.g}, then 2u + 1's).
+// Every load of the unit is issued first and its value pinned, so the unit
+// waits on memory once.
 template <uint32_t DT>
 __device__ __forceinline__ void tam_k1_unit(const TamTensor& d, uint32_t u, uint32_t lane, float* lutw,
                                             const TamLdsTabs* tabs, uint32_t seed_lo, uint32_t seed_hi,
                                             double* __restrict__ part) {
+  constexpr int NW = DT == TAM_DTYPE_F32 ? 4 : 2;  // 16-byte words per lane of a parameter-dtype array
   const uint32_t l8 = lane & 7u;
   const uint32_t b = u * 8u + (lane >> 3);
   const uint64_t e0 = (uint64_t)b * TAM_BLOCK_SIZE + l8 * TAM_EPU;
   const bool costate = (d.flags & TAM_FLAG_COSTATE) != 0;
   const bool compress_v = (d.flags & TAM_FLAG_COMPRESS_V) != 0;
   const bool has_state = costate && (d.flags & TAM_FLAG_HAS_STATE);
-  float g[TAM_EPU], p[TAM_EPU], m[TAM_EPU], v[TAM_EPU];
-  // every load of the unit is issued before any result is used
-  tam_ld8<DT, true>(d.grad, e0, TAM_EPL, g);
-  tam_ld8<DT, true>(d.grad, e0 + TAM_EPL, TAM_EPL, g + TAM_EPL);
-  tam_ld8<DT, true>(d.param, e0, TAM_EPL, p);
-  tam_ld8<DT, true>(d.param, e0 + TAM_EPL, TAM_EPL, p + TAM_EPL);
-  TamCsIn cs = {0u, 0u, 0u, 0.0f};
-  uint32_t sbytes = 0u;  // sign bytes of elements e0..e0+7 (low) and e0+8..e0+15
+  const uint64_t off = e0 * (DT == TAM_DTYPE_F32 ? 4u : 2u);
+  TamW4 gw[NW], pw[NW];
+#pragma unroll
+  for (int k = 0; k < NW; ++k) gw[k] = tam_g((const TamW4*)((const char*)d.grad + off))[k];
+#pragma unroll
+  for (int k = 0; k < NW; ++k) pw[k] = tam_g((const TamW4*)((const char*)d.param + off))[k];
+  uint32_t label = 0u, amp = 0u, sbytes = 0u;  // sbytes: sign bytes of elements e0..e0+7 (low) and e0+8..e0+15
+  float nrm = 0.0f, alpha_prev = 0.0f;
   if (has_state) {
-    cs.label = tam_g(d.labels)[b];
-    cs.nrm = tam_g(d.norms)[b];
-    cs.amp = tam_g(d.amp)[b];
+    label = tam_g(d.labels)[b];
+    nrm = tam_g(d.norms)[b];
+    amp = tam_g(d.amp)[b];
     sbytes = tam_g((const uint16_t*)(d.signs + (e0 >> 3)))[0];
+    alpha_prev = tam_g(d.alpha)[0];
   }
   uint32_t sc = 0u;
   TamW4 iw = {0u, 0u, 0u, 0u};
@@ -1290,8 +1302,34 @@ __device__ __forceinline__ void tam_k1_unit(const TamTensor& d, uint32_t u, uint
     sc = tam_g((const uint32_t*)d.v_scales)[b];
     iw = tam_g((const TamW4*)(d.v_idx + e0))[0];
   }
-  const float alpha_prev = has_state ? tam_g(d.alpha)[0] : 0.0f;
   tam_compiler_fence();
+#pragma unroll
+  for (int k = 0; k < NW; ++k) {
+    tam_pin(gw[k]);
+    tam_pin(pw[k]);
+  }
+  tam_pin(label);
+  tam_pin(nrm);
+  tam_pin(amp);
+  tam_pin(sbytes);
+  tam_pin(alpha_prev);
+  tam_pin(sc);
+  tam_pin(iw);
+  float g[TAM_EPU], p[TAM_EPU], m[TAM_EPU], v[TAM_EPU];
+  if constexpr (DT == TAM_DTYPE_F32) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const TamF4 gk = __builtin_bit_cast(TamF4, gw[k]), pk = __builtin_bit_cast(TamF4, pw[k]);
+      g[4 * k] = gk.x; g[4 * k + 1] = gk.y; g[4 * k + 2] = gk.z; g[4 * k + 3] = gk.w;
+      p[4 * k] = pk.x; p[4 * k + 1] = pk.y; p[4 * k + 2] = pk.z; p[4 * k + 3] = pk.w;
+    }
+  } else {
+    tam_unpack8<DT>(gw[0], g);
+    tam_unpack8<DT>(gw[1], g + TAM_EPL);
+    tam_unpack8<DT>(pw[0], p);
+    tam_unpack8<DT>(pw[1], p + TAM_EPL);
+  }
+  const TamCsIn cs = {label, amp, 0u, nrm};
 
   // ---- first moment ---------------------------------------------------
   if (costate) {
@@ -1309,6 +1347,8 @@ __device__ __forceinline__ void tam_k1_unit(const TamTensor& d, uint32_t u, uint
     if ((lane & 31u) - 12u < 2u) tam_g(part)[(lane >> 5) * 2u + (lane & 1u)] = t;
   } else {
     // fp32 exp_avg (optimizer.py:113): m = fma(1-b1, g, fl(m*b1))
+    // (fp32 moments are loaded here, not with the unit's other loads: their
+    // registers would otherwise count against every unit of the kernel)
     float ea[TAM_EPU];
     tam_ld8_f32<true>(d.exp_avg, e0, TAM_EPL, ea);
     tam_ld8_f32<true>(d.exp_avg, e0 + TAM_EPL, TAM_EPL, ea + TAM_EPL);
@@ -1377,15 +1417,27 @@ __device__ __forceinline__ void tam_k1_full_body(const TamTensor* __restrict__ T
   tam_lds_tabs_fill(&tabs);
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63u;
   float* lutw = lut[wave];
-  int ti = tam_find_tensor(T, nT, blockIdx.x);
-  for (uint32_t tile = blockIdx.x; tile < total_tiles; tile += gridDim.x) {
+  // tensor by tensor: the descriptor is read once per tensor, then the wave
+  // takes its units of the tensor in grid strides
+  uint32_t tile = blockIdx.x;
+  int ti = tam_find_tensor(T, nT, tile);
+  while (tile < total_tiles) {
     ti = tam_advance_tensor(T, nT, ti, tile);
     const TamTensor& d = T[ti];
-    if (d.dtype != DT || (d.flags & TAM_FLAG_EF)) continue;  // uniform; EF: tam_k1_ef
-    const uint32_t u = (tile - d.tile0) * 2u + wave;         // unit within the tensor
-    if (!tam_unit_full(d, u)) continue;                     // left to tam_k1_tail
-    double* part = (double*)(partials + (uint64_t)tile * 4u + 2u * wave);
-    tam_k1_unit<DT>(d, u, lane, lutw, &tabs, seed_lo, seed_hi, part);
+    const uint32_t end = d.tile0 + d.ntiles;  // the tensor's tiles end here
+    if (d.dtype == DT && !(d.flags & TAM_FLAG_EF)) {  // uniform; EF: tam_k1_ef
+      // units u < nfull are full (inside the tensor, aligned arrays); the
+      // rest are tam_k1_tail's, and u grows with the tile
+      const bool aligned = (((uintptr_t)d.param | (uintptr_t)d.grad) & 15u) == 0;
+      const uint64_t nfull = aligned ? d.n / (8u * TAM_BLOCK_SIZE) : 0u;
+      for (; tile < end; tile += gridDim.x) {
+        const uint32_t u = (tile - d.tile0) * 2u + wave;  // unit within the tensor
+        if (u >= nfull) break;
+        double* part = (double*)(partials + (uint64_t)tile * 4u + 2u * wave);
+        tam_k1_unit<DT>(d, u, lane, lutw, &tabs, seed_lo, seed_hi, part);
+      }
+    }
+    while (tile < end) tile += gridDim.x;  // this workgroup's first tile past the tensor
   }
 }
 
