@@ -158,6 +158,30 @@ class _PinnedUpload:
         ev.record(stream)
 
 
+class _FastStep:
+    """The host side of a steady step, kept from the previous step: one device,
+    no capturable group, the same parameters with gradients and unchanged state
+    (TurboAdam._layout_version), every CoState tensor past its first update
+    and every error-feedback residual written.  Such a step skips the
+    per-parameter walk of _collect: the gradients are gathered by list
+    comprehensions, checked only when a gradient object is new (dtype, layout,
+    contiguity, device), and the step numbers and bias corrections come from
+    the kept state dicts."""
+
+    def __init__(self, version, device, params, absent, rows, states, grads, pdtypes, bc_src, plan):
+        self.version = version
+        self.device = device
+        self.dev_index = device.index if device.index is not None else torch.cuda.current_device()
+        self.params = params      # every parameter of the optimizer, in order
+        self.absent = absent      # [p.grad is None] of the step this was built from
+        self.rows = rows          # positions (in params) of the descriptor rows
+        self.states = states      # their state dicts
+        self.grads = grads        # the gradient objects last checked, per row
+        self.pdtypes = pdtypes    # parameter dtypes, per row
+        self.bc_src = bc_src      # (bc key, group betas, state dict whose step sets the group's bias corrections)
+        self.plan = plan
+
+
 class TurboAdam(Optimizer):
     """Adam optimizer with compressed first and second moment storage.
 
@@ -227,6 +251,7 @@ class TurboAdam(Optimizer):
         # Optional callable(pass_index, "begin"|"end") run around each of the four
         # launches (the step is then issued pass by pass); used to time kernels.
         self._pass_hook = None
+        self._fast = None  # _FastStep of the last steady step
 
     def add_param_group(self, param_group):
         """torch.optim.Optimizer.add_param_group; later parameters' tensor ids
@@ -699,8 +724,22 @@ class TurboAdam(Optimizer):
             self._plans[device] = plan
         else:
             self._refresh(plan, device, items)
+        self._submit(lib, device, plan, bufs, capturing)
+        for p, state, group, group_idx, tid in items:
+            if not group.get("capturable"):
+                state["step"] += 1  # capturable: the step's first launch counts it
+            if state["_compress_m"]:
+                mgr = state["m_mgr"]
+                if not mgr._has_state:
+                    mgr._has_state = True
+                    mgr._original_numel = p.numel()
+        return plan
+
+    def _submit(self, lib, device, plan, bufs, capturing: bool) -> None:
+        """Derived fields (tam_prepare), buffers, the descriptor upload and the
+        step's launches on the device's current stream."""
         table = plan.table
-        n = len(items)
+        n = len(table)
         arr = (_lib.TamTensor * n).from_buffer(table)
         info = _lib.TamStepInfo()
         _lib.check(lib.tam_prepare(arr, n, ctypes.byref(info)), "tam_prepare")
@@ -724,14 +763,90 @@ class TurboAdam(Optimizer):
             if upload is not None:
                 upload.copied(stream)
             self._issue(lib, desc.data_ptr(), arr, info, ws, stream.cuda_stream)
-        for p, state, group, group_idx, tid in items:
-            if not group.get("capturable"):
-                state["step"] += 1  # capturable: the step's first launch counts it
+
+    # ------------------------------------------------------------------
+    # steady steps (_FastStep)
+    # ------------------------------------------------------------------
+    def _keep_fast(self, per_device, plans) -> None:
+        """Keep what a following step with the same gradients needs (or drop
+        it when this step's shape does not allow a fast one)."""
+        self._fast = None
+        if len(per_device) != 1 or self._keepalive:
+            return
+        (device, items), = per_device.items()
+        if any(group.get("capturable") for group in self.param_groups):
+            return
+        for _, state, _, _, _ in items:
             if state["_compress_m"]:
                 mgr = state["m_mgr"]
-                if not mgr._has_state:
-                    mgr._has_state = True
-                    mgr._original_numel = p.numel()
+                if not mgr._has_state or (mgr._error_feedback and mgr._ef_residual is None):
+                    return
+        plan = plans[device]
+        params = [p for group in self.param_groups for p in group["params"]]
+        pos = {id(p): i for i, p in enumerate(params)}
+        rows = [pos[id(p)] for p, _, _, _, _ in items]
+        bc_src = []
+        for group_idx, group in enumerate(self.param_groups):
+            src = None  # the group's last parameter with state (optimizer.py:172-188)
+            for q in group["params"]:
+                st = self.state.get(q)
+                if st is not None and q.device == device:
+                    src = st
+            if src is not None:
+                bc_src.append(((group_idx, device.type, device.index), group, src))
+        self._fast = _FastStep(self._layout_version, device, params, [p.grad is None for p in params], rows,
+                               [it[1] for it in items], [it[0].grad for it in items], [it[0].dtype for it in items],
+                               bc_src, plan)
+
+    def _fast_step(self) -> bool:
+        """A steady step (_FastStep) if this one is; False (nothing done) otherwise."""
+        f = self._fast
+        if f is None or f.version != self._layout_version:
+            return False
+        gs = [p.grad for p in f.params]
+        if [g is None for g in gs] != f.absent:
+            return False
+        grads = [gs[i] for i in f.rows]
+        kept = f.grads
+        for j, g in enumerate(grads):
+            if g is not kept[j]:  # a new gradient object: the checks of _grad_ptr
+                if not (g.dtype is f.pdtypes[j] and g.layout is torch.strided and g.is_contiguous()
+                        and g.get_device() == f.dev_index):
+                    return False
+                kept[j] = g
+        plan = f.plan
+        if self._plans.get(f.device) is not plan:
+            return False
+        device = f.device
+        self._bc_values = {}
+        for key, group, src in f.bc_src:
+            beta1, beta2 = group["betas"]
+            next_step = src["step"] + 1
+            bc = (1.0 - beta1**next_step, 1.0 - beta2**next_step)
+            self._bc_values[key] = bc
+            t = self._group_step_tensors.get(key)
+            if t is not None:
+                t["bc1"].fill_(bc[0])
+                t["bc2"].fill_(bc[1])
+        t = plan.table
+        t["grad"] = [g.data_ptr() for g in grads]
+        states = f.states
+        t["step"] = np.asarray([st["step"] for st in states], dtype=np.int64) + 1
+        flags = plan.static_flags.copy()
+        if plan.cost_rows.size:
+            flags[plan.cost_rows] |= np.uint32(_lib.TAM_FLAG_HAS_STATE)
+        if plan.ef_rows.size:
+            flags[plan.ef_rows] |= np.uint32(_lib.TAM_FLAG_HAS_EF)
+        t["flags"] = flags
+        self._set_group_fields(plan, device)
+        lib = _lib.load()
+        bufs = self._device_buffers(device, False)
+        with torch.cuda.device(device):
+            bufs.order_on(torch.cuda.current_stream(device))
+        self._submit(lib, device, plan, bufs, False)
+        for st in states:
+            st["step"] += 1
+        return True
 
     def _issue(self, lib, desc_ptr: int, arr, info, ws: torch.Tensor, stream: int) -> None:
         """The step's launches: one tam_multi_tensor_step call, or the passes one
@@ -790,10 +905,16 @@ class TurboAdam(Optimizer):
                 return loss
         if grad_scale is not None:
             self._unscale_grads(grad_scale)
+        elif found_inf is None and not torch.cuda.is_current_stream_capturing() and self._fast_step():
+            return loss
         try:
             # one fused step of every parameter with a gradient (reference optimizer.py:88-170)
-            for device, items in self._collect().items():
-                self._launch(device, items)
+            per_device = self._collect()
+            plans = {device: self._launch(device, items) for device, items in per_device.items()}
+            if grad_scale is None and found_inf is None:
+                self._keep_fast(per_device, plans)
+            else:
+                self._fast = None
         finally:
             self._found_inf = None
             for state in self._keepalive:
