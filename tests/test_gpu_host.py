@@ -1,0 +1,81 @@
+"""Steady steps of the host code (GPU): a step whose parameters with gradients
+and whose state are those of the previous step skips the per-parameter walk.
+Every transition in and out of that path must leave the results bit-identical
+to the oracle: new gradient tensors, reused gradient tensors refilled in place,
+a gradient that goes missing and comes back, an lr change, a state dict
+loaded mid-run and a group added mid-run."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from tests.helpers import compare_with_oracle, from_torch, log, to_bits, to_torch
+
+pytestmark = pytest.mark.gpu
+
+F32, BF16 = O.DT_F32, O.DT_BF16
+
+
+def test_steady_steps_match_oracle_across_transitions():
+    from turboadam_amd import TurboAdam
+
+    dev = torch.device("cuda:0")
+    sizes = [5000, 300, 4096 + 77, 9000]
+    dts = [F32, F32, BF16, BF16]
+    rng = np.random.default_rng(51)
+    init = [to_bits((rng.standard_normal(n) * 0.02).astype(np.float32), dt) for n, dt in zip(sizes, dts)]
+    params = [torch.nn.Parameter(to_torch(a, dt, (n,), dev)) for a, dt, n in zip(init, dts, sizes)]
+    kw = dict(lr=1e-3, weight_decay=0.05)
+    opt = TurboAdam(params[:3], philox_seed=21, **kw)
+    oparams = [a.copy() for a in init]
+    orc = O.OracleTurboAdam(oparams[:3], dtypes=dts[:3], seed=21, **kw)
+    kept = [None] * len(sizes)
+    taken = []
+    fast_step = opt._fast_step
+
+    def spy():
+        r = fast_step()
+        taken.append(r)
+        return r
+
+    opt._fast_step = spy
+
+    def grads(step):
+        return [to_bits((rng.standard_normal(n) * 1e-3 * (1 + step % 3)).astype(np.float32), dt)
+                for n, dt in zip(sizes, dts)]
+
+    for step in range(12):
+        gs = grads(step)
+        n_active = 4 if step >= 9 else 3
+        if step == 9:  # a group added mid-run: its parameter gets its own group
+            opt.add_param_group({"params": [params[3]], "lr": 5e-4})
+            orc.add_param_group({"params": [oparams[3]], "lr": 5e-4}, dtypes=[dts[3]])
+        if step == 6:  # an lr schedule step
+            for grp in opt.param_groups:
+                grp["lr"] = 2e-3
+            for grp in orc.param_groups:
+                grp["lr"] = 2e-3
+        if step == 7:  # the optimizer's own state dict, loaded back mid-run
+            opt.load_state_dict(opt.state_dict())
+        og = []
+        for i in range(n_active):
+            if step == 4 and i == 1:  # a gradient that goes missing for one step
+                params[i].grad = None
+                og.append(None)
+                continue
+            t = to_torch(gs[i], dts[i], (sizes[i],), dev)
+            if step in (2, 3, 10) and kept[i] is not None:
+                kept[i].copy_(t)  # the same gradient object, refilled in place
+                params[i].grad = kept[i]
+            else:
+                params[i].grad = kept[i] = t
+            og.append(gs[i])
+        opt.step()
+        orc.step(og)
+        torch.cuda.synchronize()
+        bad = compare_with_oracle(opt, params[:n_active], orc, oparams[:n_active], f"step {step + 1}")
+        assert not bad, "\n".join(bad[:20])
+    log(f"12 steps; steady path taken at steps {[i + 1 for i, r in enumerate(taken) if r]}")
+    assert sum(taken) >= 5
+    assert taken[-1]  # the last step was steady again
