@@ -269,8 +269,10 @@ int tam_v_quantize(const float* v, uint64_t n_padded, uint32_t v_bits, int stoch
 
 /* Self-check of the device arithmetic: out[i] = f(in[i]) with f selected by
  * `fn` (0 log, 1 exp, 2 f32->f16->f32, 3 f32->bf16->f32 in software, 4 sqrt,
- * 5 f32->bf16->f32 by the hardware conversion).  No counterpart in
- * the reference: it lets a caller confirm the device math equals the host. */
+ * 5 f32->bf16->f32 by the hardware conversion; the raw hardware instructions
+ * whose error bounds the certified fast paths assume: 6 v_sqrt_f32,
+ * 7 v_rcp_f32, 8 v_log_f32 (log2)).  No counterpart in the reference: it lets
+ * a caller confirm the device math equals the host. */
 int tam_math_eval(int fn, const float* in, float* out, uint64_t n, void* stream);
 
 #ifdef __cplusplus

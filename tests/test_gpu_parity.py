@@ -103,6 +103,46 @@ def test_device_sqrt_is_correctly_rounded():
     assert np.array_equal(got.view(np.uint32), np.sqrt(x).view(np.uint32))
 
 
+def test_hardware_sqrt_rcp_log2_error_bounds_on_every_normal_input():
+    """The certified fast paths rest on three hardware instructions' error
+    bounds: v_sqrt_f32 and v_rcp_f32 (bf16/fp16 update) within 2^-23 relative,
+    v_log_f32 (1Q index) within 2^-21 relative of log2.  Checked on every
+    positive normal fp32 input (v_rcp_f32 where 1/x is normal too; log2 exact
+    at 1), against fp64 references on the device, 2^27 inputs at a time."""
+    _l, lib = _lib()
+    dev = torch.device("cuda:0")
+    lo, hi, chunk = 0x00800000, 0x7F800000, 1 << 27
+    worst = {6: 0.0, 7: 0.0, 8: 0.0}
+    out = torch.empty(chunk, dtype=torch.float32, device=dev)
+    for start in range(lo, hi, chunk):
+        n = min(chunk, hi - start)
+        bits = torch.arange(start, start + n, dtype=torch.int64, device=dev).to(torch.int32)
+        x = bits.view(torch.float32)
+        xd = x.double()
+        for fn in (6, 7, 8):
+            _l.check(lib.tam_math_eval(fn, x.data_ptr(), out.data_ptr(), n, _l.stream_of(dev)), "tam_math_eval")
+            y = out[:n].double()
+            if fn == 6:
+                ref = torch.sqrt(xd)
+                rel = ((y - ref) / ref).abs()
+            elif fn == 7:
+                ref = 1.0 / xd
+                rel = ((y - ref) * xd).abs()
+                rel = torch.where(x < 2.0 ** 126, rel, torch.zeros_like(rel))
+            else:
+                ref = torch.log2(xd)
+                exact_one = x == 1.0
+                assert bool((y[exact_one] == 0.0).all())
+                rel = torch.where(exact_one, torch.zeros_like(ref), ((y - ref) / ref).abs())
+            worst[fn] = max(worst[fn], float(rel.max()))
+        del bits, x, xd, y, ref, rel
+    log(f"max relative error over every normal input: v_sqrt_f32 2^{np.log2(worst[6]):.3f}, "
+        f"v_rcp_f32 2^{np.log2(worst[7]):.3f}, v_log_f32 2^{np.log2(worst[8]):.3f}")
+    assert worst[6] <= 2.0 ** -23
+    assert worst[7] <= 2.0 ** -23
+    assert worst[8] <= 2.0 ** -21
+
+
 def test_philox_uniforms_match_oracle():
     _l, lib = _lib()
     dev = torch.device("cuda:0")

@@ -579,8 +579,8 @@ __device__ __forceinline__ TamVExt tam_vpath_a(const TamTensor& d, const TamWave
   // EMA (quantize.py:259-270) and the clamp of :275.
   TamVExt x;
   if (d.beta2 >= 0.0f && d.one_minus_beta2 >= 0.0f) {  // uniform
-    // v >= +0 or NaN.  The extremes are taken on the bit patterns of v shifted
-    // left by one: the sign bit drops out and a NaN of either sign orders
+    // v >= +0 or NaN.  The extremes are taken on the bit patterns of v with
+    // the sign bit cleared: -0 orders as +0 and a NaN of either sign orders
     // above +inf.  The clamp commutes with min and max, so vpath_b clamps the
     // extremes; vc = max(v, 1e-38) equals the clamp except for a NaN, whose
     // block is re-quantised from its NaN extremes whatever vc holds.
@@ -591,14 +591,14 @@ __device__ __forceinline__ TamVExt tam_vpath_a(const TamTensor& d, const TamWave
       const float g2 = valid ? g[i] * g[i] : 0.0f;
       v[i] = __builtin_fmaf(d.one_minus_beta2, g2, vo[i] * d.beta2);
       vc[i] = __builtin_fmaxf(v[i], 1e-38f);
-      const uint32_t k2 = tam_f2u(v[i]) << 1;
+      const uint32_t k = tam_f2u(v[i]) & 0x7fffffffu;
       if (valid && bvalid) {
-        xmn = __builtin_elementwise_min(xmn, k2);
-        xmx = __builtin_elementwise_max(xmx, k2);
+        xmn = __builtin_elementwise_min(xmn, k);
+        xmx = __builtin_elementwise_max(xmx, k);
       }
     }
-    x.kmn = tam_block_umin(xmn) >> 1;
-    x.kmx = tam_block_umax(xmx) >> 1;
+    x.kmn = tam_block_umin(xmn);
+    x.kmx = tam_block_umax(xmx);
     x.nan_seen = x.kmx > 0x7f800000u ? TAM_VEXT_NAN : 0u;
   } else {
     // v may be negative: extremes of the clamped v, NaN tested per element
@@ -632,13 +632,13 @@ __device__ __forceinline__ TamVExt tam_lane_extremes(const float* v, uint32_t nv
 #pragma unroll
   for (int i = 0; i < TAM_EPL; ++i) {
     if (FULL || (uint32_t)i < nv) {
-      xmn = __builtin_elementwise_min(xmn, tam_f2u(v[i]) << 1);
-      xmx = __builtin_elementwise_max(xmx, tam_f2u(v[i]) << 1);
+      xmn = __builtin_elementwise_min(xmn, tam_f2u(v[i]) & 0x7fffffffu);
+      xmx = __builtin_elementwise_max(xmx, tam_f2u(v[i]) & 0x7fffffffu);
     }
   }
   TamVExt x;
-  x.kmn = xmn >> 1;
-  x.kmx = xmx >> 1;
+  x.kmn = xmn;
+  x.kmx = xmx;
   x.nan_seen = x.kmx > 0x7f800000u ? TAM_VEXT_NAN : 0u;
   return x;
 }
@@ -787,14 +787,14 @@ __device__ __forceinline__ void tam_vpath_b(const TamTensor& d, const TamWave& W
 // test proves the fp32 rounding, else from the division.
 //
 // bf16 / fp16 parameters: a fast sequence u~ = fl(fl(c*m) * r) with
-// r = rcp(fl(s~ + eps)), s~ = fl(q * rsq(q)), q = fl(v * fl(1/bc2)),
+// r = rcp(fl(s~ + eps)), s~ = sqrt(q) (v_sqrt_f32), q = fl(v * fl(1/bc2)),
 // c = fl(-lr/bc1).  In the model fl(x) = x(1 + d) + e (|d| <= 2^-24,
 // |e| <= 2^-150 and e != 0 only below 2^-126), with q a positive normal and
 // 0 <= eps < 2^124 (so 2^-63 <= den < 2^125 and r is a normal):
 //  * relative parts: the exact sequence's six roundings, the fast
-//    sequence's seven and the two hardware results (each within 2^-23 on
-//    normal inputs -- checked exhaustively on gfx950), 17 units of 2^-24,
-//    inside 2^-19;
+//    sequence's six and the two hardware results (v_sqrt_f32 within
+//    2^-23.36 and v_rcp_f32 within 2^-23 on normal inputs -- each checked
+//    exhaustively on gfx950), 16 units of 2^-24, inside 2^-19;
 //  * absolute parts: e of fl(-lr*m) divided by t2 (at most
 //    2^-150 r/bc1 (1 + 2^-21)), e of c*m times r, and e of upd and u~, below
 //    k_abs r + 2^-149 with k_abs = fl(2^-147/bc1).
@@ -854,7 +854,7 @@ __device__ __forceinline__ void tam_update(const TamTensor& d, float* p, const f
 #pragma unroll
   for (int i = 0; i < TAM_EPL; ++i) {
     const float q = v[i] * d.inv_bc2_f32;
-    const float s = q * __builtin_amdgcn_rsqf(q);
+    const float s = __builtin_amdgcn_sqrtf(q);
     const float r = __builtin_amdgcn_rcpf(s + d.eps);
     const float u = (c_lr * m[i]) * r;
     const float st = pw[i] + u;
@@ -1148,12 +1148,12 @@ __device__ __forceinline__ TamVExt tam_vunit_a(const TamTensor& d, uint32_t lane
 #pragma unroll
     for (int i = 0; i < TAM_EPU; ++i) {
       v[i] = __builtin_fmaf(d.one_minus_beta2, g[i] * g[i], vo[i] * d.beta2);
-      const uint32_t k2 = tam_f2u(v[i]) << 1;
-      xmn = __builtin_elementwise_min(xmn, k2);
-      xmx = __builtin_elementwise_max(xmx, k2);
+      const uint32_t k = tam_f2u(v[i]) & 0x7fffffffu;
+      xmn = __builtin_elementwise_min(xmn, k);
+      xmx = __builtin_elementwise_max(xmx, k);
     }
-    x.kmn = tam_half_umin(xmn) >> 1;
-    x.kmx = tam_half_umax(xmx) >> 1;
+    x.kmn = tam_half_umin(xmn);
+    x.kmx = tam_half_umax(xmx);
     x.nan_seen = x.kmx > 0x7f800000u ? TAM_VEXT_NAN : 0u;
   } else {
     // v may be negative: extremes of the clamped v, NaN tested per element
@@ -1208,6 +1208,7 @@ __device__ __forceinline__ void tam_vunit_b(const TamTensor& d, uint32_t lane, u
   const bool blk_ok = (tam_u2f(kmn) >= 0x1p-126f) && (tam_u2f(kmx) < 0x1p100f) && !nan_seen && (sp <= 64.0f) &&
                       (Bb < 0.25f);
   const float H = blk_ok ? 0.5f - (Bb + 0x1p-22f) : -1.0f;
+  const uint32_t byte_lsb = d.v_bits < 8u ? 0x01010101u : 0u;  // uniform
   // the lane's 16 elements are one group of draws (three Philox blocks): the
   // two halves of 8 one after the other, the first from blocks 3t and 3t + 1
   // (words w0..w5), the second from w6, w7 and block 3t + 2
@@ -1236,9 +1237,15 @@ __device__ __forceinline__ void tam_vunit_b(const TamTensor& d, uint32_t lane, u
       const float dd = __builtin_fmaf(-(float)rw[i], 0x1p-24f, ct);  // fl(ct - u), u exact
       const float q = __builtin_rintf(dd);
       tmax = __builtin_fmaxf(tmax, __builtin_fabsf(dd - q));
-      // the exact path overwrites rejected elements
-      ow[i >> 2] = __builtin_amdgcn_cvt_pk_u8_f32(__builtin_amdgcn_fmed3f(q, 0.0f, fnb - 1.0f), i & 3, ow[i >> 2]);
+      // v_cvt_pk_u8_f32 saturates to [0, 255]; the exact path overwrites rejected elements
+      ow[i >> 2] = __builtin_amdgcn_cvt_pk_u8_f32(q, i & 3, ow[i >> 2]);
     }
+    // An accepted q lies in [0, 2^bits] (q = -1 or 2^bits + 1 would put d half
+    // a unit from q), so the clamp to 2^bits - 1 moves only the byte 2^bits:
+    // each byte loses its bit `bits` (no borrow crosses a byte; with 8 bits the
+    // saturation has clamped)
+    ow[0] -= (ow[0] >> d.v_bits) & byte_lsb;
+    ow[1] -= (ow[1] >> d.v_bits) & byte_lsb;
     if (!(tmax < H)) {  // false for a NaN bound (then H = -1)
       // exact path: the reference's own sequence with correctly rounded log and division
 #pragma unroll
@@ -2577,6 +2584,9 @@ __global__ void tam_k_math_eval(int fn, const float* __restrict__ in, float* __r
     case 3: y = tam_bf16_to_f32(tam_f32_to_bf16(x)); break;
     case 4: y = __builtin_sqrtf(x); break;
     case 5: y = tam_bf16_to_f32(tam_f32_to_bf16_rne(x)); break;
+    case 6: y = __builtin_amdgcn_sqrtf(x); break;
+    case 7: y = __builtin_amdgcn_rcpf(x); break;
+    case 8: y = __builtin_amdgcn_logf(x); break;
     default: y = x; break;
   }
   out[i] = y;
@@ -2938,7 +2948,7 @@ int tam_philox_uniforms(uint32_t tensor_id, uint32_t step, uint64_t seed, uint64
 int tam_math_eval(int fn, const float* in, float* out, uint64_t n, void* stream) {
   tam_err_buf[0] = 0;
   if (!in || !out) return tam_fail(TAM_E_INVALID, "%snull argument", "");
-  if (fn < 0 || fn > 5) return tam_fail(TAM_E_INVALID, "%sunknown function %ld", "", fn);
+  if (fn < 0 || fn > 8) return tam_fail(TAM_E_INVALID, "%sunknown function %ld", "", fn);
   if (n == 0) return TAM_OK;
   const uint64_t blocks = (n + 255) / 256;
   hipLaunchKernelGGL(tam_k_math_eval, dim3((uint32_t)blocks), dim3(256), 0, (hipStream_t)stream, fn, in, out, n);
