@@ -97,6 +97,12 @@ WORKLOADS = {
     "c3-rank0of8": (llama3_8b_rank0_of8_shapes, torch.bfloat16, dict(lr=3e-4, weight_decay=0.1, v_bits=4),
                     math.log(1e-4), "llama3-8b-shaped bf16 m+v v_bits=4, rank 0 of 8 (tensor sharding)"),
 }
+# the ragged set's sweep: v_bits in {2, 3, 6, 8} x (null_pct, amp_pct) in {(0.10, 0.90), (0.05, 0.95)}
+for _bits in (2, 3, 6, 8):
+    for _null, _amp in ((0.10, 0.90), (0.05, 0.95)):
+        WORKLOADS[f"c4-b{_bits}-n{round(_null * 100):02d}"] = (
+            ragged_shapes, torch.float32, dict(lr=1e-3, v_bits=_bits, null_pct=_null, amp_pct=_amp), math.log(1e-3),
+            f"ragged 1000 tensors fp32 m+v v_bits={_bits} null/amp pct {_null:.2f}/{_amp:.2f}")
 
 
 def bytes_per_param(dtype_bytes: int, costate: bool, compress_v: bool = True, ef: bool = False):

@@ -58,6 +58,16 @@ def test_more_than_one_gpu_is_refused():
     assert "one GPU" in res.stderr
 
 
+def test_ragged_sweep_workloads():
+    # the ragged set's sweep: every v_bits x (null_pct, amp_pct) pair on the same 1000 tensors
+    names = sorted(n for n in bench.WORKLOADS if n.startswith("c4-b"))
+    assert len(names) == 8
+    pairs = {(bench.WORKLOADS[n][2]["v_bits"], bench.WORKLOADS[n][2]["null_pct"], bench.WORKLOADS[n][2]["amp_pct"])
+             for n in names}
+    assert pairs == {(b, nl, am) for b in (2, 3, 6, 8) for nl, am in ((0.10, 0.90), (0.05, 0.95))}
+    assert all(bench.WORKLOADS[n][0] is bench.ragged_shapes for n in names)
+
+
 def test_cpu_baseline_sample():
     # workloads up to 300M parameters run whole; the 8B-shaped set samples its first decoder layer
     for name in ("c0", "c1", "c2", "c4"):
