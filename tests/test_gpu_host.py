@@ -79,3 +79,45 @@ def test_steady_steps_match_oracle_across_transitions():
     log(f"12 steps; steady path taken at steps {[i + 1 for i, r in enumerate(taken) if r]}")
     assert sum(taken) >= 5
     assert taken[-1]  # the last step was steady again
+
+
+def test_replaced_parameter_storage_is_followed():
+    """A parameter whose storage is replaced between steps (p.data = a copy,
+    then p.data = p.data.to(bf16)) is stepped in its new storage and dtype, on
+    the steady path's terms: the descriptor rows follow the parameter, not the
+    storage they were built on.  The old storages stay referenced, so a stale
+    row would update them instead and show as a mismatch."""
+    from turboadam_amd import TurboAdam
+
+    dev = torch.device("cuda:0")
+    sizes = [5000, 4096 + 77, 300]
+    dts = [F32, F32, BF16]
+    rng = np.random.default_rng(52)
+    init = [to_bits((rng.standard_normal(n) * 0.02).astype(np.float32), dt) for n, dt in zip(sizes, dts)]
+    params = [torch.nn.Parameter(to_torch(a, dt, (n,), dev)) for a, dt, n in zip(init, dts, sizes)]
+    kw = dict(lr=1e-3, weight_decay=0.01)
+    opt = TurboAdam(params, philox_seed=22, **kw)
+    oparams = [a.copy() for a in init]
+    orc = O.OracleTurboAdam(oparams, dtypes=list(dts), seed=22, **kw)
+    old = []
+    for step in range(8):
+        if step == 3:  # same values, new storage
+            old.append(params[0].data)
+            params[0].data = params[0].data.clone()
+        if step == 5:  # fp32 -> bf16 (round to nearest even, as the oracle's copy)
+            old.append(params[1].data)
+            params[1].data = params[1].data.to(torch.bfloat16)
+            dts[1] = BF16
+            oparams[1] = to_bits(oparams[1], BF16)
+            orc.param_groups[0]["params"][1] = oparams[1]
+            orc.dtypes[1] = BF16
+        gs = [to_bits((rng.standard_normal(n) * 1e-3).astype(np.float32), dt) for n, dt in zip(sizes, dts)]
+        for p, g, dt, n in zip(params, gs, dts, sizes):
+            p.grad = to_torch(g, dt, (n,), dev)
+        opt.step()
+        orc.step(gs)
+        torch.cuda.synchronize()
+        bad = compare_with_oracle(opt, params, orc, oparams, f"step {step + 1}")
+        assert not bad, "\n".join(bad[:20])
+    assert params[1].dtype == torch.bfloat16
+    log("8 steps with a storage swap at step 4 and an fp32 -> bf16 swap at step 6")

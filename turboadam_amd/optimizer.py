@@ -165,8 +165,9 @@ class _FastStep:
     and every error-feedback residual written.  Such a step skips the
     per-parameter walk of _collect: the gradients are gathered by list
     comprehensions, checked only when a gradient object is new (dtype, layout,
-    contiguity, device), and the step numbers and bias corrections come from
-    the kept state dicts."""
+    contiguity, device), the parameters' storage pointers are compared with the
+    kept descriptor rows (p.data replaced: not steady), and the step numbers
+    and bias corrections come from the kept state dicts."""
 
     def __init__(self, version, device, params, absent, rows, states, grads, pdtypes, bc_src, plan):
         self.version = version
@@ -180,6 +181,8 @@ class _FastStep:
         self.pdtypes = pdtypes    # parameter dtypes, per row
         self.bc_src = bc_src      # (bc key, group betas, state dict whose step sets the group's bias corrections)
         self.plan = plan
+        self.row_params = [params[i] for i in rows]
+        self.ptrs = [p.data_ptr() for p in self.row_params]  # parameter storage the descriptor rows point at
 
 
 class TurboAdam(Optimizer):
@@ -716,7 +719,9 @@ class TurboAdam(Optimizer):
             bufs.order_on(torch.cuda.current_stream(device))
             if self._found_inf is not None:
                 self._skip_ptr = self._skip_flag(device, self._found_inf).data_ptr()
-        key = tuple(it[4] for it in items)
+        # a parameter whose storage was replaced (p.data = ..., a dtype or
+        # device change) needs its descriptor row rebuilt
+        key = (tuple(it[4] for it in items), tuple(it[0].data_ptr() for it in items))
         plan = self._plans.get(device)
         if plan is None or plan.key != (key, self._layout_version):
             plan = self._describe(device, items)
@@ -805,6 +810,8 @@ class TurboAdam(Optimizer):
             return False
         gs = [p.grad for p in f.params]
         if [g is None for g in gs] != f.absent:
+            return False
+        if [p.data_ptr() for p in f.row_params] != f.ptrs:
             return False
         grads = [gs[i] for i in f.rows]
         kept = f.grads
