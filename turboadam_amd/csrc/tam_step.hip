@@ -2048,7 +2048,7 @@ __global__ __launch_bounds__(TAM_WG) void tam_k_sel_minmax(const TamTensor* __re
 // 256-thread workgroup calls it and returns the same state.  Each thread sums
 // 8 consecutive bins; an exclusive scan of those sums finds the thread whose
 // range holds rank k, and that thread finds the digit among its 8 bins.
-__device__ TamSel tam_sel_pick_wg(TamSel st, const uint32_t* __restrict__ gh) {
+__device__ __forceinline__ TamSel tam_sel_pick_wg(TamSel st, const uint32_t* __restrict__ gh) {
   __shared__ uint32_t wsum[TAM_WG / 64];
   __shared__ uint32_t found[2][2];  // per rank: digit, rank within the digit's keys
   if (st.top < 0) return st;        // uniform: every bit is fixed
@@ -2057,10 +2057,12 @@ __device__ TamSel tam_sel_pick_wg(TamSel st, const uint32_t* __restrict__ gh) {
   tam_sel_window(st.top, sh, dmask);
   const bool same = st.prefix[0] == st.prefix[1];
   const uint32_t tid = threadIdx.x, lane = tid & 63u, w = tid >> 6;
-  if (tid < 2) {
-    found[tid][0] = 0u;
-    found[tid][1] = st.k[tid];
+  if (tid == 0) {
+    found[0][0] = found[1][0] = 0u;
+    found[0][1] = st.k[0];
+    found[1][1] = st.k[1];
   }
+#pragma unroll
   for (int r = 0; r < 2; ++r) {
     const TAM_GLOBAL TamW4* hr = tam_g((const TamW4*)(gh + (same ? 0u : (uint32_t)r) * 2048u));
     const TamW4 a = hr[2u * tid], b = hr[2u * tid + 1u];
