@@ -1460,7 +1460,9 @@ __device__ __forceinline__ void tam_k1_full_body(const TamTensor* __restrict__ T
 #define TAM_K1_WAVES_F16 4
 #endif
 #ifndef TAM_K1_WAVES_F32
-#define TAM_K1_WAVES_F32 4
+// fp32 parameters and gradients hold twice the registers of 16-bit ones: at 4
+// waves the kernel spills, at 3 (136 VGPRs) it does not and runs 1-2.5% faster
+#define TAM_K1_WAVES_F32 3
 #endif
 TAM_K1_FULL_KERNEL(tam_k1_main_bf16, TAM_DTYPE_BF16, TAM_K1_WAVES_BF16)
 TAM_K1_FULL_KERNEL(tam_k1_main_f16, TAM_DTYPE_F16, TAM_K1_WAVES_F16)
