@@ -39,6 +39,7 @@
 #define TAM_EPL 8
 #define TAM_BPT 16  // blocks per tile
 #define TAM_TILE_ELEMS (TAM_BPT * TAM_BLOCK_SIZE)
+#define TAM_SEL_WG 1024
 
 // ---------------------------------------------------------------------------
 // error reporting
@@ -1914,26 +1915,20 @@ tam_k2_encode(const TamTensor* __restrict__ T, int nT, uint32_t total_tiles, con
 // Ratios are >= +0 or NaN, so their fp32 bit patterns order like torch.sort
 // (NaN last).  The selection is an MSD radix select on those patterns, spread
 // over slices of 8192 keys so that large tensors use many workgroups:
-//   tam_k_sel_reset   per tensor: reset the selection state and the three
-//                     round histograms;
+//   tam_k_sel_reset   per tensor: reset the selection state and histograms;
 //   tam_k_sel_minmax  per slice: min / max of the keys (atomic min / max per
-//                     tensor) -- the bits all keys share need no round;
-//   tam_k_sel_hist    per slice, rounds 0, 1, 2: first the pick of the previous
-//                     round (prefix sums of its histogram find the digit
-//                     holding each rank; every workgroup of the tensor computes
-//                     the same state, and the tensor's first slice stores it for
-//                     the next round), then an LDS histogram of the next 11-bit
+//                     tensor) -- the bits all keys share need no pass;
+//   tam_k_sel_hist    per slice, three times: LDS histogram of the next 11-bit
 //                     digit below the bits already fixed, for the keys that
-//                     match the prefix of each of the two ranks, added into the
-//                     tensor's histogram of this round;
-//   tam_k_sel_labels  per slice: the last round's pick, labels from the two
-//                     thresholds, alpha write-back.
-// Each round has its own histogram (cleared by tam_k_sel_reset) and the
-// states of consecutive rounds go to alternate arrays, so no workgroup reads
-// what another workgroup of the same launch writes.
+//                     match the prefix of each of the two ranks (keys of
+//                     similar magnitude spread over the bins), added into the
+//                     tensor's histogram;
+//   tam_k_sel_pick    per tensor, after each histogram: prefix sums of the
+//                     histogram pick the digit holding each rank;
+//   tam_k_sel_labels  per slice: labels from the two thresholds; alpha
+//                     write-back.
 #define TAM_SLICE 8192u
-#define TAM_SEL_ROUNDS 3u
-#define TAM_SEL_HIST (2u * 2048u)  // one round's histogram: 2048 bins per rank
+#define TAM_SEL_WG 1024
 
 // Selection state of one tensor (workspace).
 struct TamSel {
@@ -1974,29 +1969,22 @@ __device__ __forceinline__ void tam_slice_keys(const uint32_t* __restrict__ keys
   }
 }
 
-// The state before round 0, from the key range: bits above the highest
-// differing bit are shared by every key (all of them when every key is equal).
-__device__ __forceinline__ TamSel tam_sel_start(TamSel s) {
+// Initial prefix state from the key range: bits above the highest differing
+// bit are shared by every key.
+__device__ __forceinline__ void tam_sel_start(const TamSel& s, uint32_t* prefix, uint32_t& mask, int& top) {
   const uint32_t diff = s.kmin ^ s.kmax;
-  s.top = diff ? 31 - __builtin_clz(diff) : -1;
-  s.mask = s.top >= 31 ? 0u : (0xffffffffu << (s.top + 1));
-  s.prefix[0] = s.prefix[1] = s.kmin & s.mask;
-  return s;
+  top = diff ? 31 - __builtin_clz(diff) : -1;
+  mask = top >= 31 ? 0u : (0xffffffffu << (top + 1));
+  prefix[0] = prefix[1] = s.kmin & mask;
 }
 
-// Current digit window of a tensor: bits [sh, top] below the fixed prefix.
-__device__ __forceinline__ void tam_sel_window(int top, int& sh, uint32_t& dmask) {
-  sh = top >= 10 ? top - 10 : 0;
-  dmask = (1u << (top - sh + 1)) - 1u;
-}
-
-__global__ __launch_bounds__(TAM_WG) void tam_k_sel_reset(const TamTensor* __restrict__ T, TamSel* __restrict__ base,
+__global__ __launch_bounds__(TAM_WG) void tam_k_sel_reset(const TamTensor* __restrict__ T, TamSel* __restrict__ sel,
                                                           uint32_t* __restrict__ hist) {
   if (tam_step_skipped(T)) return;
   const TamTensor& d = T[blockIdx.x];
   if (!(d.flags & TAM_FLAG_COSTATE)) return;
-  TamW4* h = (TamW4*)(hist + (uint64_t)blockIdx.x * (TAM_SEL_ROUNDS * TAM_SEL_HIST));
-  for (uint32_t i = threadIdx.x; i < TAM_SEL_ROUNDS * TAM_SEL_HIST / 4u; i += TAM_WG) h[i] = TamW4{0u, 0u, 0u, 0u};
+  uint32_t* h = hist + (uint64_t)blockIdx.x * 4096u;
+  for (uint32_t i = threadIdx.x; i < 4096u; i += TAM_WG) h[i] = 0u;
   if (threadIdx.x == 0) {
     TamSel z;
     z.kmin = 0xffffffffu;
@@ -2005,13 +1993,13 @@ __global__ __launch_bounds__(TAM_WG) void tam_k_sel_reset(const TamTensor* __res
     z.k[0] = d.k_lo;
     z.k[1] = d.k_hi;
     z.mask = 0u;
-    z.top = -1;
-    base[blockIdx.x] = z;
+    z.top = 32;  // not started
+    sel[blockIdx.x] = z;
   }
 }
 
 __global__ __launch_bounds__(TAM_WG) void tam_k_sel_minmax(const TamTensor* __restrict__ T, int nT,
-                                                           const float* __restrict__ ratios, TamSel* __restrict__ base) {
+                                                           const float* __restrict__ ratios, TamSel* __restrict__ sel) {
   if (tam_step_skipped(T)) return;
   __shared__ uint32_t red[2][TAM_WG / 64];
   const int t = tam_slice_tensor(T, nT, blockIdx.x);
@@ -2039,105 +2027,42 @@ __global__ __launch_bounds__(TAM_WG) void tam_k_sel_minmax(const TamTensor* __re
       kmin = red[0][w] < kmin ? red[0][w] : kmin;
       kmax = red[1][w] > kmax ? red[1][w] : kmax;
     }
-    atomicMin(&base[t].kmin, kmin);
-    atomicMax(&base[t].kmax, kmax);
+    atomicMin(&sel[t].kmin, kmin);
+    atomicMax(&sel[t].kmax, kmax);
   }
 }
 
-// One round's pick for one tensor: from the state before the round and the
-// round's histogram gh (2048 bins per rank; the first half serves both ranks
-// when they share the prefix), the state after it.  Every thread of the
-// 256-thread workgroup calls it and returns the same state.  Each thread sums
-// 8 consecutive bins; an exclusive scan of those sums finds the thread whose
-// range holds rank k, and that thread finds the digit among its 8 bins.
-__device__ __forceinline__ TamSel tam_sel_pick_wg(TamSel st, const uint32_t* __restrict__ gh) {
-  __shared__ uint32_t wsum[TAM_WG / 64];
-  __shared__ uint32_t found[2][2];  // per rank: digit, rank within the digit's keys
-  if (st.top < 0) return st;        // uniform: every bit is fixed
-  int sh;
-  uint32_t dmask;
-  tam_sel_window(st.top, sh, dmask);
-  const bool same = st.prefix[0] == st.prefix[1];
-  const uint32_t tid = threadIdx.x, lane = tid & 63u, w = tid >> 6;
-  if (tid == 0) {
-    found[0][0] = found[1][0] = 0u;
-    found[0][1] = st.k[0];
-    found[1][1] = st.k[1];
-  }
-#pragma unroll
-  for (int r = 0; r < 2; ++r) {
-    const TAM_GLOBAL TamW4* hr = tam_g((const TamW4*)(gh + (same ? 0u : (uint32_t)r) * 2048u));
-    const TamW4 a = hr[2u * tid], b = hr[2u * tid + 1u];
-    const uint32_t h[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-    const uint32_t s = ((h[0] + h[1]) + (h[2] + h[3])) + ((h[4] + h[5]) + (h[6] + h[7]));
-    uint32_t inc = s;  // inclusive scan over the wave, then over the waves
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const uint32_t t = __shfl_up(inc, off);
-      if (lane >= (uint32_t)off) inc += t;
-    }
-    if (lane == 63u) wsum[w] = inc;
-    __syncthreads();
-    uint32_t pre = inc - s;
-    for (uint32_t j = 0; j < w; ++j) pre += wsum[j];
-    const uint32_t k = st.k[r];
-    if (k >= pre && k < pre + s) {  // one thread: the first of its bins whose end passes k
-      uint32_t acc = pre, dig = 7u, below = 0u;
-      bool done = false;
-#pragma unroll
-      for (uint32_t j = 0; j < 8u; ++j) {
-        if (!done && k < acc + h[j]) {
-          dig = j;
-          below = acc;
-          done = true;
-        }
-        acc += h[j];
-      }
-      if (!done) below = acc - h[7];
-      found[r][0] = 8u * tid + dig;
-      found[r][1] = k - below;
-    }
-    __syncthreads();  // found[] written, wsum free for the next rank
-  }
-  TamSel o = st;
-  o.prefix[0] = st.prefix[0] | (found[0][0] << sh);
-  o.prefix[1] = st.prefix[1] | (found[1][0] << sh);
-  o.k[0] = found[0][1];
-  o.k[1] = found[1][1];
-  o.mask = st.mask | (dmask << sh);
-  o.top = sh - 1;
-  __syncthreads();  // found[] read before a later call rewrites it
-  return o;
+// Current digit window of a tensor: bits [sh, top] below the fixed prefix.
+__device__ __forceinline__ void tam_sel_window(int top, int& sh, uint32_t& dmask) {
+  sh = top >= 10 ? top - 10 : 0;
+  dmask = (1u << (top - sh + 1)) - 1u;
 }
 
-// Round `round` of the selection (0, 1, 2): the state before it is the key
-// range's start (round 0), the pick of round 0's histogram (round 1), or the
-// pick of the previous round's histogram from the state the tensor's first
-// slice stored in sel_prev (round 2); rounds 1 and 2 store their state in
-// sel_next.
 __global__ __launch_bounds__(TAM_WG) void tam_k_sel_hist(const TamTensor* __restrict__ T, int nT,
                                                          const float* __restrict__ ratios,
-                                                         const TamSel* __restrict__ base,
-                                                         const TamSel* __restrict__ sel_prev,
-                                                         TamSel* __restrict__ sel_next, uint32_t* __restrict__ hist,
-                                                         int round) {
+                                                         const TamSel* __restrict__ sel, uint32_t* __restrict__ hist) {
   if (tam_step_skipped(T)) return;
   __shared__ uint32_t h[2][2048];
   const int t = tam_slice_tensor(T, nT, blockIdx.x);
   const TamTensor& d = T[t];
-  uint32_t* gt = hist + (uint64_t)t * (TAM_SEL_ROUNDS * TAM_SEL_HIST);
-  TamSel st = round <= 1 ? tam_sel_start(base[t]) : sel_prev[t];
-  if (round >= 1) {
-    st = tam_sel_pick_wg(st, gt + (uint32_t)(round - 1) * TAM_SEL_HIST);
-    if (blockIdx.x == d.slice0 && threadIdx.x == 0) sel_next[t] = st;
+  const TamSel st = sel[t];
+  uint32_t prefix[2], mask;
+  int top;
+  if (st.top == 32) {
+    tam_sel_start(st, prefix, mask, top);
+  } else {
+    prefix[0] = st.prefix[0];
+    prefix[1] = st.prefix[1];
+    mask = st.mask;
+    top = st.top;
   }
-  if (st.top < 0) return;  // uniform over the workgroup
+  if (top < 0) return;  // uniform over the workgroup
   int sh;
   uint32_t dmask;
-  tam_sel_window(st.top, sh, dmask);
+  tam_sel_window(top, sh, dmask);
   for (uint32_t i = threadIdx.x; i < 4096u; i += TAM_WG) (&h[0][0])[i] = 0u;
   __syncthreads();
-  const uint32_t p0 = st.prefix[0], p1 = st.prefix[1], mask = st.mask;
+  const uint32_t p0 = prefix[0], p1 = prefix[1];
   const bool same = p0 == p1;
   const uint32_t k0 = (blockIdx.x - d.slice0) * TAM_SLICE;
   const uint32_t k1 = k0 + TAM_SLICE < d.nb ? k0 + TAM_SLICE : d.nb;
@@ -2148,31 +2073,113 @@ __global__ __launch_bounds__(TAM_WG) void tam_k_sel_hist(const TamTensor* __rest
     if (!same && km == p1) atomicAdd(&h[1][dg], 1u);
   });
   __syncthreads();
-  uint32_t* gh = gt + (uint32_t)round * TAM_SEL_HIST;
+  uint32_t* gh = hist + (uint64_t)t * 4096u;
   for (uint32_t i = threadIdx.x; i < 4096u; i += TAM_WG) {
     const uint32_t c = (&h[0][0])[i];
     if (c) atomicAdd(&gh[i], c);
   }
 }
 
-// The last round's pick (from the state round 2 stored in sel_prev), labels
-// from the two thresholds, alpha write-back; the tensor's first slice stores
-// the final state in sel_final.
+// Exclusive prefix sum over the 1024 threads of the workgroup.
+__device__ uint32_t tam_wg_excl_scan(uint32_t v, uint32_t* wsum) {
+  const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
+  uint32_t inc = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t t = __shfl_up(inc, off);
+    if (lane >= (uint32_t)off) inc += t;
+  }
+  if (lane == 63u) wsum[w] = inc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t acc = 0;
+    for (int i = 0; i < TAM_SEL_WG / 64; ++i) {
+      const uint32_t t = wsum[i];
+      wsum[i] = acc;
+      acc += t;
+    }
+  }
+  __syncthreads();
+  const uint32_t r = wsum[w] + inc - v;
+  __syncthreads();
+  return r;
+}
+
+__global__ __launch_bounds__(TAM_SEL_WG) void tam_k_sel_pick(const TamTensor* __restrict__ T, TamSel* __restrict__ sel,
+                                                             uint32_t* __restrict__ hist) {
+  if (tam_step_skipped(T)) return;
+  __shared__ uint32_t wsum[TAM_SEL_WG / 64];
+  __shared__ uint32_t new_prefix[2], new_k[2];
+  const TamTensor& d = T[blockIdx.x];
+  if (!(d.flags & TAM_FLAG_COSTATE)) return;
+  const TamSel st = sel[blockIdx.x];
+  uint32_t prefix[2], mask;
+  int top;
+  if (st.top == 32) {
+    tam_sel_start(st, prefix, mask, top);
+  } else {
+    prefix[0] = st.prefix[0];
+    prefix[1] = st.prefix[1];
+    mask = st.mask;
+    top = st.top;
+  }
+  const uint32_t tid = threadIdx.x;
+  if (top >= 0) {
+    int sh;
+    uint32_t dmask;
+    tam_sel_window(top, sh, dmask);
+    uint32_t* gh = hist + (uint64_t)blockIdx.x * 4096u;
+    const bool same = prefix[0] == prefix[1];
+    if (tid < 2) {
+      new_prefix[tid] = prefix[tid];
+      new_k[tid] = st.k[tid];
+    }
+    __syncthreads();
+    for (int r = 0; r < 2; ++r) {
+      const uint32_t* hr = gh + (same ? 0u : (uint32_t)r) * 2048u;
+      const uint32_t h0 = hr[2 * tid], h1 = hr[2 * tid + 1];
+      const uint32_t pre = tam_wg_excl_scan(h0 + h1, wsum);
+      const uint32_t k = st.k[r];
+      if (k >= pre && k < pre + h0 + h1) {
+        const bool first = k < pre + h0;
+        const uint32_t digit = 2 * tid + (first ? 0u : 1u);
+        new_k[r] = k - (first ? pre : pre + h0);
+        new_prefix[r] = prefix[r] | (digit << sh);
+      }
+      __syncthreads();
+    }
+    // clear the histogram for the next pass
+    for (uint32_t i = tid; i < 4096u; i += TAM_SEL_WG) gh[i] = 0u;
+    if (tid == 0) {
+      TamSel o = st;
+      o.prefix[0] = new_prefix[0];
+      o.prefix[1] = new_prefix[1];
+      o.k[0] = new_k[0];
+      o.k[1] = new_k[1];
+      o.mask = mask | (dmask << sh);
+      o.top = sh - 1;
+      sel[blockIdx.x] = o;
+    }
+  } else if (tid == 0 && st.top == 32) {
+    TamSel o = st;  // every key equal: both thresholds are that key
+    o.prefix[0] = prefix[0];
+    o.prefix[1] = prefix[1];
+    o.mask = mask;
+    o.top = -1;
+    sel[blockIdx.x] = o;
+  }
+}
+
 __global__ __launch_bounds__(TAM_WG) void tam_k_sel_labels(const TamTensor* __restrict__ T, int nT,
                                                            const float* __restrict__ alpha_new,
                                                            const float* __restrict__ ratios,
-                                                           const TamSel* __restrict__ sel_prev,
-                                                           TamSel* __restrict__ sel_final,
-                                                           const uint32_t* __restrict__ hist, char* __restrict__ ws,
+                                                           const TamSel* __restrict__ sel, char* __restrict__ ws,
                                                            float* __restrict__ alpha_old) {
   if (tam_step_skipped(T)) return;
   const int t = tam_slice_tensor(T, nT, blockIdx.x);
   const TamTensor& d = T[t];
-  const TamSel st = tam_sel_pick_wg(sel_prev[t], hist + (uint64_t)t * (TAM_SEL_ROUNDS * TAM_SEL_HIST) +
-                                                     (TAM_SEL_ROUNDS - 1u) * TAM_SEL_HIST);
-  if (blockIdx.x == d.slice0 && threadIdx.x == 0) sel_final[t] = st;
-  const float tau0 = tam_u2f(st.prefix[0]);
-  const float tau1 = tam_u2f(st.prefix[1]);
+  const float tau0 = tam_u2f(sel[t].prefix[0]);
+  const float tau1 = tam_u2f(sel[t].prefix[1]);
   const uint32_t k0 = (blockIdx.x - d.slice0) * TAM_SLICE;
   const uint32_t k1 = k0 + TAM_SLICE < d.nb ? k0 + TAM_SLICE : d.nb;
   const float* r = ratios + d.ratio_off;
@@ -2431,15 +2438,10 @@ __global__ void tam_k_classify(const float* __restrict__ ratios, uint64_t nb, co
   labels[i] = x >= tau1 ? (uint8_t)2 : (x >= tau0 ? (uint8_t)1 : (uint8_t)0);
 }
 
-// The two thresholds of one tensor's selection: the last round's pick from
-// the state round 2 stored (256 threads).
-__global__ __launch_bounds__(TAM_WG) void tam_k_sel_taus(const TamSel* __restrict__ sel_prev,
-                                                         const uint32_t* __restrict__ hist, float* __restrict__ taus) {
-  const TamSel st = tam_sel_pick_wg(sel_prev[0], hist + (TAM_SEL_ROUNDS - 1u) * TAM_SEL_HIST);
-  if (threadIdx.x == 0) {
-    taus[0] = tam_u2f(st.prefix[0]);
-    taus[1] = tam_u2f(st.prefix[1]);
-  }
+// The two thresholds of a finished selection.
+__global__ void tam_k_sel_taus(const TamSel* __restrict__ sel, float* __restrict__ taus) {
+  taus[0] = tam_u2f(sel[0].prefix[0]);
+  taus[1] = tam_u2f(sel[0].prefix[1]);
 }
 
 // fused_v_update (quantize.py:222-299) for one tensor: the 1Q half of pass 1
@@ -2745,10 +2747,10 @@ int tam_prepare(TamTensor* tensors, int n_tensors, TamStepInfo* info) {
   off = tam_align_up(off + ratio_blocks * sizeof(float), 256);
   info->off_chunks = off;
   off = tam_align_up(off + chunks * sizeof(double2), 256);
-  info->off_sel = off;  // three states per tensor: before round 0 (key range), after rounds 1/3, after round 2
-  off = tam_align_up(off + 3u * (uint64_t)n_tensors * sizeof(TamSel), 256);
+  info->off_sel = off;
+  off = tam_align_up(off + (uint64_t)n_tensors * sizeof(TamSel), 256);
   info->off_hist = off;
-  off = tam_align_up(off + (uint64_t)n_tensors * (TAM_SEL_ROUNDS * TAM_SEL_HIST) * sizeof(uint32_t), 256);
+  off = tam_align_up(off + (uint64_t)n_tensors * 4096u * sizeof(uint32_t), 256);
   info->n_ef = nef;
   info->n_device_step = ndev;
   info->off_ef_alpha = off;
@@ -2820,23 +2822,22 @@ static int tam_launch_pass(int pass, const TamTensor* d_tensors, const TamStepIn
                          dim3(TAM_K1U_WG), 0, s,
                          d_tensors, info->n_tensors, info->total_tiles, alpha_new, ratios, ws);
       break;
-    default: {
-      TamSel* sel_a = sel + info->n_tensors;  // states after rounds 1 and 3
-      TamSel* sel_b = sel_a + info->n_tensors;  // state after round 2
+    default:
       hipLaunchKernelGGL(tam_k_sel_reset, dim3(info->n_tensors), dim3(TAM_WG), 0, s, d_tensors, sel, hist);
       TAM_HIP_CHECK(hipGetLastError());
       hipLaunchKernelGGL(tam_k_sel_minmax, dim3(info->total_slices), dim3(TAM_WG), 0, s, d_tensors,
                          info->n_tensors, ratios, sel);
       TAM_HIP_CHECK(hipGetLastError());
-      for (int r = 0; r < (int)TAM_SEL_ROUNDS; ++r) {  // 11-bit digits: three rounds fix all 32 bits
+      for (int r = 0; r < 3; ++r) {  // 11-bit digits: at most three rounds fix all 32 bits
         hipLaunchKernelGGL(tam_k_sel_hist, dim3(info->total_slices), dim3(TAM_WG), 0, s, d_tensors,
-                           info->n_tensors, ratios, sel, r == 2 ? sel_a : sel_b, r == 2 ? sel_b : sel_a, hist, r);
+                           info->n_tensors, ratios, sel, hist);
+        TAM_HIP_CHECK(hipGetLastError());
+        hipLaunchKernelGGL(tam_k_sel_pick, dim3(info->n_tensors), dim3(TAM_SEL_WG), 0, s, d_tensors, sel, hist);
         TAM_HIP_CHECK(hipGetLastError());
       }
       hipLaunchKernelGGL(tam_k_sel_labels, dim3(info->total_slices), dim3(TAM_WG), 0, s, d_tensors,
-                         info->n_tensors, alpha_new, ratios, sel_b, sel_a, hist, ws, alpha_old);
+                         info->n_tensors, alpha_new, ratios, sel, ws, alpha_old);
       break;
-    }
     case 4:
       hipLaunchKernelGGL(tam_k4_ef, dim3(grid_of(TAM_KS_K4_EF, (const void*)tam_k4_ef)), dim3(TAM_WG), 0, s, d_tensors,
                          info->n_tensors, info->total_tiles, alpha_new, alpha_old, ws);
@@ -3036,9 +3037,9 @@ int tam_block_ratios(const float* delta, const float* m, uint64_t n, float* rati
 static uint64_t tam_thresholds_layout(uint64_t* off_sel, uint64_t* off_hist) {
   uint64_t off = tam_align_up(sizeof(TamTensor), 256);
   *off_sel = off;
-  off = tam_align_up(off + 3u * sizeof(TamSel), 256);
+  off = tam_align_up(off + sizeof(TamSel), 256);
   *off_hist = off;
-  return tam_align_up(off + (TAM_SEL_ROUNDS * TAM_SEL_HIST) * sizeof(uint32_t), 256);
+  return tam_align_up(off + 4096u * sizeof(uint32_t), 256);
 }
 
 size_t tam_thresholds_workspace(uint64_t nb) {
@@ -3069,12 +3070,13 @@ int tam_thresholds(const float* ratios, uint64_t nb, uint32_t k_lo, uint32_t k_h
   TAM_HIP_CHECK(hipGetLastError());
   hipLaunchKernelGGL(tam_k_sel_minmax, dim3(slices), dim3(TAM_WG), 0, s, desc, 1, ratios, sel);
   TAM_HIP_CHECK(hipGetLastError());
-  for (int r = 0; r < (int)TAM_SEL_ROUNDS; ++r) {
-    hipLaunchKernelGGL(tam_k_sel_hist, dim3(slices), dim3(TAM_WG), 0, s, desc, 1, ratios, sel,
-                       r == 2 ? sel + 1 : sel + 2, r == 2 ? sel + 2 : sel + 1, hist, r);
+  for (int r = 0; r < 3; ++r) {
+    hipLaunchKernelGGL(tam_k_sel_hist, dim3(slices), dim3(TAM_WG), 0, s, desc, 1, ratios, sel, hist);
+    TAM_HIP_CHECK(hipGetLastError());
+    hipLaunchKernelGGL(tam_k_sel_pick, dim3(1), dim3(TAM_SEL_WG), 0, s, desc, sel, hist);
     TAM_HIP_CHECK(hipGetLastError());
   }
-  hipLaunchKernelGGL(tam_k_sel_taus, dim3(1), dim3(TAM_WG), 0, s, sel + 2, hist, taus);
+  hipLaunchKernelGGL(tam_k_sel_taus, dim3(1), dim3(1), 0, s, sel, taus);
   TAM_HIP_CHECK(hipGetLastError());
   return TAM_OK;
 }
