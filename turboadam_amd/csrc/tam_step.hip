@@ -1275,8 +1275,8 @@ __device__ __forceinline__ void tam_vunit_b(const TamTensor& d, uint32_t lane, u
 // One wave's unit: loads, first moment (CoState or fp32), second moment (1Q or
 // fp32), update, store; for CoState tensors the partial sums of g.g and m.g of
 // the unit's two quarters (part: quarter 2u's {g.g, m.g}, then 2u + 1's).
-// Every load of the unit is issued first and its value pinned, so the unit
-// waits on memory once.
+// Every load of the unit (but an fp32 parameter's) is issued first and its
+// value pinned, so the unit waits on memory once.
 template <uint32_t DT>
 __device__ __forceinline__ void tam_k1_unit(const TamTensor& d, uint32_t u, uint32_t lane, float* lutw,
                                             const TamLdsTabs* tabs, uint32_t seed_lo, uint32_t seed_hi,
@@ -1292,8 +1292,12 @@ __device__ __forceinline__ void tam_k1_unit(const TamTensor& d, uint32_t u, uint
   TamW4 gw[NW], pw[NW];
 #pragma unroll
   for (int k = 0; k < NW; ++k) gw[k] = tam_g((const TamW4*)((const char*)d.grad + off))[k];
+  // an fp32 parameter (16 registers) is loaded just before the update: held
+  // from here it would make the kernel spill at 4 waves per SIMD
+  if constexpr (DT != TAM_DTYPE_F32) {
 #pragma unroll
-  for (int k = 0; k < NW; ++k) pw[k] = tam_g((const TamW4*)((const char*)d.param + off))[k];
+    for (int k = 0; k < NW; ++k) pw[k] = tam_g((const TamW4*)((const char*)d.param + off))[k];
+  }
   uint32_t label = 0u, amp = 0u, sbytes = 0u;  // sbytes: sign bytes of elements e0..e0+7 (low) and e0+8..e0+15
   float nrm = 0.0f, alpha_prev = 0.0f;
   if (has_state) {
@@ -1313,7 +1317,7 @@ __device__ __forceinline__ void tam_k1_unit(const TamTensor& d, uint32_t u, uint
 #pragma unroll
   for (int k = 0; k < NW; ++k) {
     tam_pin(gw[k]);
-    tam_pin(pw[k]);
+    if constexpr (DT != TAM_DTYPE_F32) tam_pin(pw[k]);
   }
   tam_pin(label);
   tam_pin(nrm);
@@ -1326,9 +1330,8 @@ __device__ __forceinline__ void tam_k1_unit(const TamTensor& d, uint32_t u, uint
   if constexpr (DT == TAM_DTYPE_F32) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      const TamF4 gk = __builtin_bit_cast(TamF4, gw[k]), pk = __builtin_bit_cast(TamF4, pw[k]);
+      const TamF4 gk = __builtin_bit_cast(TamF4, gw[k]);
       g[4 * k] = gk.x; g[4 * k + 1] = gk.y; g[4 * k + 2] = gk.z; g[4 * k + 3] = gk.w;
-      p[4 * k] = pk.x; p[4 * k + 1] = pk.y; p[4 * k + 2] = pk.z; p[4 * k + 3] = pk.w;
     }
   } else {
     tam_unpack8<DT>(gw[0], g);
@@ -1382,6 +1385,13 @@ __device__ __forceinline__ void tam_k1_unit(const TamTensor& d, uint32_t u, uint
 
   // ---- parameter update -----------------------------------------------
   {
+    if constexpr (DT == TAM_DTYPE_F32) {
+#pragma unroll
+      for (int k = 0; k < NW; ++k) {
+        const TamF4 pk = __builtin_bit_cast(TamF4, tam_g((const TamW4*)((const char*)d.param + off))[k]);
+        p[4 * k] = pk.x; p[4 * k + 1] = pk.y; p[4 * k + 2] = pk.z; p[4 * k + 3] = pk.w;
+      }
+    }
     uint16_t pb[TAM_EPU];
     bool q_ok = false;
     if (DT != TAM_DTYPE_F32) {
@@ -1461,9 +1471,7 @@ __device__ __forceinline__ void tam_k1_full_body(const TamTensor* __restrict__ T
 #define TAM_K1_WAVES_F16 4
 #endif
 #ifndef TAM_K1_WAVES_F32
-// fp32 parameters and gradients hold twice the registers of 16-bit ones: at 4
-// waves the kernel spills, at 3 (136 VGPRs) it does not and runs 1-2.5% faster
-#define TAM_K1_WAVES_F32 3
+#define TAM_K1_WAVES_F32 4
 #endif
 TAM_K1_FULL_KERNEL(tam_k1_main_bf16, TAM_DTYPE_BF16, TAM_K1_WAVES_BF16)
 TAM_K1_FULL_KERNEL(tam_k1_main_f16, TAM_DTYPE_F16, TAM_K1_WAVES_F16)
