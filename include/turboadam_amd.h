@@ -112,8 +112,10 @@ typedef struct TamTensor {
                             /*      (reference optimizer.py:172-188)            */
   const float* bc_table;    /* [in] f32 pairs (1-beta1^t, 1-beta2^t), t = 1..bc_len */
   uint32_t bc_len;          /* [in] pairs in bc_table; later steps use the last */
-  float k_abs;              /* [derived] f32(2^-147 / bias_correction1): absolute */
-                            /*      error term of the certified 16-bit update   */
+  float k_abs;              /* [derived] absolute error term of the certified   */
+                            /*      16-bit update: 2^-147 / bias_correction1 *  */
+                            /*      min(1/eps, 2^63) * (1 + 2^-20) + 2^-148,     */
+                            /*      rounded up to f32                           */
   const float* found_inf;   /* [in] DEVICE_STEP, or NULL: the step leaves every */
                             /*      tensor and counter unchanged when           */
                             /*      *found_inf != 0 (a GradScaler skip).  Given */

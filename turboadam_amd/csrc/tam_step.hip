@@ -446,33 +446,48 @@ __device__ __forceinline__ float tam_div_sqrt_block(float x) {
 
 // ge is the gradient of the EMA term: g, or g + the error-feedback residual
 // (costate.py:410-416; the decode keeps g).
-// VMASK: the sign mask is held in a VGPR (false where the kernel has no
-// register to spare: it then comes from an SGPR).
+// The decoded EMA of 8 elements from their block's |s| (bit pattern) and sign
+// byte.  s * (1 - 2*bit), costate.py:207-209, :317-319: s has a clear sign bit
+// (a norm or an fp16 amplitude), so the bit becomes the sign of s; element i's
+// bit (bit 7 - i of the byte) reaches bit 31 of sh after i doublings.
+template <bool VMASK>
+__device__ __forceinline__ void tam_cs_decode_m(const TamTensor& d, uint32_t sabs, uint32_t byte, float alpha_prev,
+                                                const float* g, const float* ge, float* m) {
+  const uint32_t sign_bit = VMASK ? tam_vconst(0x80000000u) : 0x80000000u;
+  uint32_t sh = byte << 24;
+#pragma unroll
+  for (int i = 0; i < TAM_EPL; ++i) {
+    const float sd = tam_u2f(tam_and_or(sh, sign_bit, sabs));
+    sh = tam_dbl(sh);
+    const float mh = alpha_prev * g[i] + sd;
+    m[i] = d.beta1 * mh + d.one_minus_beta1 * ge[i];
+  }
+}
+// |s| of a valid block (bit pattern): the norm over sqrt(128) for label 1, the
+// fp16 amplitude for label 2, else 0; both candidates are evaluated and
+// selected without a branch.
+__device__ __forceinline__ uint32_t tam_cs_sabs(const TamCsIn& cs) {
+  const float sph = tam_div_sqrt_block(cs.nrm), af = tam_f16_to_f32((uint16_t)cs.amp);
+  return tam_f2u(cs.label == 1u ? sph : (cs.label == 2u ? af : 0.0f)) & 0x7fffffffu;
+}
+
+// VMASK: the sign mask is held in a VGPR and the block scale is selected
+// without a branch (false where the kernel has no register to spare: the mask
+// then comes from an SGPR and the scale from a branch).
 template <bool FULL, bool VMASK = true>
 __device__ __forceinline__ void tam_costate_m(const TamTensor& d, const TamWave& W, const TamCsIn& cs,
                                               float alpha_prev, const float* g, const float* ge, float* m) {
   const bool has = (d.flags & TAM_FLAG_HAS_STATE) != 0;  // uniform over the launch
   if (has) {
-    float s = 0.0f;
     const uint32_t byte = cs.byte;
-    if (FULL || W.bvalid) {
+    float s = 0.0f;
+    if constexpr (VMASK) {
+      s = (FULL || W.bvalid) ? tam_u2f(tam_cs_sabs(cs)) : 0.0f;
+    } else if (FULL || W.bvalid) {
       const float sph = tam_div_sqrt_block(cs.nrm);
       s = cs.label == 1u ? sph : (cs.label == 2u ? tam_f16_to_f32((uint16_t)cs.amp) : 0.0f);
     }
-    // s * (1 - 2*bit), costate.py:207-209, :317-319: s has a clear sign bit
-    // (a norm or an fp16 amplitude), so the bit becomes the sign of s;
-    // element i's bit (bit 7 - i of the byte) reaches bit 31 of sh after i
-    // doublings
-    const uint32_t sabs = tam_f2u(s) & 0x7fffffffu;
-    const uint32_t sign_bit = VMASK ? tam_vconst(0x80000000u) : 0x80000000u;
-    uint32_t sh = byte << 24;
-#pragma unroll
-    for (int i = 0; i < TAM_EPL; ++i) {
-      const float sd = tam_u2f(tam_and_or(sh, sign_bit, sabs));
-      sh = tam_dbl(sh);
-      const float mh = alpha_prev * g[i] + sd;
-      m[i] = d.beta1 * mh + d.one_minus_beta1 * ge[i];
-    }
+    tam_cs_decode_m<VMASK>(d, tam_f2u(s) & 0x7fffffffu, byte, alpha_prev, g, ge, m);
   } else {
 #pragma unroll
     for (int i = 0; i < TAM_EPL; ++i) m[i] = d.beta1 * 0.0f + d.one_minus_beta1 * ge[i];
@@ -815,11 +830,14 @@ __device__ __forceinline__ void tam_vpath_b(const TamTensor& d, const TamWave& W
 //    exhaustively on gfx950), 16 units of 2^-24, inside 2^-19;
 //  * absolute parts: e of fl(-lr*m) divided by t2 (at most
 //    2^-150 r/bc1 (1 + 2^-21)), e of c*m times r, and e of upd and u~, below
-//    k_abs r + 2^-149 with k_abs = fl(2^-147/bc1).
-// So |u~ - upd| <= 2^-19 |u~| + k_abs r + 2^-149, and when |u~| < 2^126 (upd
-// then finite), fl(p + upd) lies within
-//   E = 2^-19 |u~| + 2^-22 |s| + k_abs r + 2^-148
-// of s = fl(p + u~).  R_p and fl are monotone (overflow included), so
+//    2^-147 r/bc1 + 2^-149.
+// So |u~ - upd| <= 2^-19 |u~| + 2^-147 r/bc1 + 2^-149, and when |u~| < 2^126
+// (upd then finite), fl(p + upd) lies within 2^-19 |u~| + 2^-22 |s| +
+// 2^-147 r/bc1 + 2^-148 of s = fl(p + u~).  On a lane the test below accepts,
+// q >= 2^-126 and eps >= 0, so r <= min(1/eps, 2^63) (1 + 2^-21): the last two
+// terms are below the per-tensor constant k_abs (tam_abs_term), and
+//   E = 2^-19 |u~| + 2^-22 |s| + k_abs
+// bounds the distance.  R_p and fl are monotone (overflow included), so
 // R_p(fl(p + upd)) is accepted when R_p(fl(s - E)) == R_p(fl(s + E)) and s is
 // not a NaN (an infinite s makes fl(s - E) a NaN, which fails the equality).
 // Elements go in pairs: one packed conversion rounds both fl(s - E), another
@@ -833,6 +851,16 @@ __device__ __forceinline__ void tam_vpath_b(const TamTensor& d, const TamWave& W
 typedef float TamF2 __attribute__((ext_vector_type(2)));
 typedef __bf16 TamBf2 __attribute__((ext_vector_type(2)));
 typedef _Float16 TamH2 __attribute__((ext_vector_type(2)));
+// k_abs of the certified 16-bit update: 2^-147/bc1 * min(1/eps, 2^63) *
+// (1 + 2^-20) + 2^-148, evaluated in fp64 and rounded up to fp32 (host and
+// device prologue compute it the same way).
+__host__ __device__ inline float tam_abs_term(float bc1, float eps) {
+  const double ie = eps > 0.0f ? 1.0 / (double)eps : 0x1p63;
+  const double x = 0x1p-147 / (double)bc1 * (ie < 0x1p63 ? ie : 0x1p63) * (1.0 + 0x1p-20) + 0x1p-148;
+  float c = (float)x;
+  if ((double)c < x) c = tam_next_float(c, true);
+  return c;
+}
 // x and y rounded to the 16-bit dtype (round to nearest even) in one packed
 // conversion: x in the low half, y in the high half
 template <uint32_t DT>
@@ -860,13 +888,11 @@ __device__ __forceinline__ void tam_update(const TamTensor& d, float* p, const f
   float pw[TAM_EPL];
   // weight decay rounds to the parameter dtype (p.mul_ on a 16-bit tensor)
   if (wd && DT == TAM_DTYPE_BF16) {
+    // converting (0, x) puts bf16(x) in the high half over a zero low half:
+    // the word is bf16(x) as fp32, with no shift or mask
 #pragma unroll
-    for (int k = 0; k < TAM_EPL / 2; ++k) {  // two elements per conversion
-      const uint32_t r2 = __builtin_bit_cast(
-          uint32_t, __builtin_convertvector((TamF2){p[2 * k] * d.c_wd, p[2 * k + 1] * d.c_wd}, TamBf2));
-      pw[2 * k] = tam_u2f(r2 << 16);
-      pw[2 * k + 1] = tam_u2f(r2 & 0xffff0000u);
-    }
+    for (int i = 0; i < TAM_EPL; ++i)
+      pw[i] = tam_u2f(__builtin_bit_cast(uint32_t, __builtin_convertvector((TamF2){0.0f, p[i] * d.c_wd}, TamBf2)));
   } else if (wd) {
 #pragma unroll
     for (int i = 0; i < TAM_EPL; ++i) pw[i] = tam_h2f<DT>(tam_round16_hw<DT>(p[i] * d.c_wd));
@@ -892,8 +918,7 @@ __device__ __forceinline__ void tam_update(const TamTensor& d, float* p, const f
       const float r = __builtin_amdgcn_rcpf(s + d.eps);
       const float u = (c_lr * m[i]) * r;
       st[j] = pw[i] + u;
-      E[j] = __builtin_fmaf(__builtin_fabsf(u), 0x1p-19f,
-                            __builtin_fmaf(__builtin_fabsf(st[j]), 0x1p-22f, __builtin_fmaf(r, k_abs, 0x1p-148f)));
+      E[j] = __builtin_fmaf(__builtin_fabsf(u), 0x1p-19f, __builtin_fmaf(__builtin_fabsf(st[j]), 0x1p-22f, k_abs));
       umax = __builtin_fmaxf(umax, __builtin_fabsf(u));  // a NaN u makes st NaN
     }
     nacc = __builtin_fmaf(st[0], st[1], nacc);
@@ -986,7 +1011,7 @@ __global__ __launch_bounds__(1024) void tam_k_device_step(TamTensor* __restrict_
     d.inv_bc2 = 1.0 / (double)bc2;
     d.inv_bc2_f32 = (float)d.inv_bc2;
     d.c_lr = d.neg_lr / bc1;
-    d.k_abs = 0x1p-147f / bc1;
+    d.k_abs = tam_abs_term(bc1, d.eps);
     uint32_t f = d.flags & ~(TAM_FLAG_HAS_STATE | TAM_FLAG_HAS_EF);
     if (own > 0u) {
       if (f & TAM_FLAG_COSTATE) f |= TAM_FLAG_HAS_STATE;
@@ -1261,8 +1286,12 @@ __device__ __forceinline__ void tam_vunit_b(const TamTensor& d, uint32_t lane, u
   const float Bb = __builtin_fmaf(fnb * rsp, per_sp, flat) * (1.0f + 0x1p-16f);
   const bool blk_ok = (tam_u2f(kmn) >= 0x1p-126f) && (tam_u2f(kmx) < 0x1p100f) && !nan_seen && (sp <= 64.0f) &&
                       (Bb < 0.25f);
-  const float H = blk_ok ? 0.5f - (Bb + 0x1p-22f) : -1.0f;
+  // the fast path subtracts u' = floor(r / 2) 2^-23 (u with its lowest bit
+  // dropped: u - u' <= 2^-24) from c~ + 1: 2^-22 more in the bound covers that
+  // and the rounding of the larger c~ + 1 (another 2^-24)
+  const float H = blk_ok ? 0.5f - (Bb + 0x1p-21f) : -1.0f;
   const uint32_t byte_lsb = d.v_bits < 8u ? 0x01010101u : 0u;  // uniform
+  const uint32_t m23 = tam_vconst(0x7fffffu), one = tam_vconst(0x3f800000u), k7f = tam_vconst(0x7fu);
   // the lane's 16 elements are one group of draws (three Philox blocks): the
   // two halves of 8 one after the other, the first from blocks 3t and 3t + 1
   // (words w0..w5), the second from w6, w7 and block 3t + 2
@@ -1271,24 +1300,34 @@ __device__ __forceinline__ void tam_vunit_b(const TamTensor& d, uint32_t lane, u
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const float* vh = v + TAM_EPL * h;
-    uint32_t rw[TAM_EPL];
+    uint32_t w[6];
     if (h == 0) {
       const TamU4 a = tam_philox_block(c0, d.tensor_id, d.step, seed_lo, seed_hi);
       const TamU4 bb = tam_philox_block(c0 + 1u, d.tensor_id, d.step, seed_lo, seed_hi);
-      tam_split24(a.x, a.y, a.z, a.w, bb.x, bb.y, rw);
+      w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w; w[4] = bb.x; w[5] = bb.y;
       carry0 = bb.z;
       carry1 = bb.w;
     } else {
       const TamU4 c = tam_philox_block(c0 + 2u, d.tensor_id, d.step, seed_lo, seed_hi);
-      tam_split24(carry0, carry1, c.x, c.y, c.z, c.w, rw);
+      w[0] = carry0; w[1] = carry1; w[2] = c.x; w[3] = c.y; w[4] = c.z; w[5] = c.w;
     }
+    // draw i as the fp32 1 + u' (its top 23 bits under the exponent of 1.0):
+    // bits [24i + 1, 24i + 24) of the window w0..w5
+    const auto draw1 = [&](int i) -> float {
+      const uint32_t* ww = w + 3 * (i >> 2);
+      switch (i & 3) {
+        case 0: return tam_u2f(tam_and_or(ww[0] >> 1, m23, one));
+        case 1: return tam_u2f(tam_and_or(__builtin_amdgcn_alignbit(ww[1], ww[0], 25), m23, one));
+        case 2: return tam_u2f(tam_and_or(__builtin_amdgcn_alignbit(ww[2], ww[1], 17), m23, one));
+        default: return tam_u2f(__builtin_amdgcn_alignbit(k7f, ww[2], 9));  // 0x7f << 23 is 1.0's exponent
+      }
+    };
     uint32_t ow[2] = {0u, 0u};
     float tmax = 0.0f;
 #pragma unroll
     for (int i = 0; i < TAM_EPL; ++i) {
       const float l2 = __builtin_amdgcn_logf(vh[i] * rmin);
-      const float ct = __builtin_fmaf(l2, K, 0.5f);
-      const float dd = __builtin_fmaf(-(float)rw[i], 0x1p-24f, ct);  // fl(ct - u), u exact
+      const float dd = __builtin_fmaf(l2, K, 1.5f) - draw1(i);  // fl(fl(c~ + 1) - (1 + u'))
       const float q = __builtin_rintf(dd);
       tmax = __builtin_fmaxf(tmax, __builtin_fabsf(dd - q));
       // v_cvt_pk_u8_f32 saturates to [0, 255]; the exact path overwrites rejected elements
@@ -1301,11 +1340,13 @@ __device__ __forceinline__ void tam_vunit_b(const TamTensor& d, uint32_t lane, u
     ow[0] -= (ow[0] >> d.v_bits) & byte_lsb;
     ow[1] -= (ow[1] >> d.v_bits) & byte_lsb;
     if (!(tmax < H)) {  // false for a NaN bound (then H = -1)
-      // exact path: the reference's own sequence with correctly rounded log and division
+      // exact path: the reference's own sequence with correctly rounded log
+      // and division, and the whole 24-bit draws
+      uint32_t rw[TAM_EPL];
+      tam_split24(w[0], w[1], w[2], w[3], w[4], w[5], rw);
 #pragma unroll
       for (int i = 0; i < TAM_EPL; ++i) {
-        const float dd = __builtin_fmaf(-(float)rw[i], 0x1p-24f,
-                                        __builtin_fmaf(__builtin_amdgcn_logf(vh[i] * rmin), K, 0.5f));
+        const float dd = __builtin_fmaf(__builtin_amdgcn_logf(vh[i] * rmin), K, 1.5f) - draw1(i);
         if (!(__builtin_fabsf(dd - __builtin_rintf(dd)) < H)) {
           const float vc = vh[i] < 1e-38f ? 1e-38f : vh[i];  // quantize.py:275
           const float l = tam_logf_lds(vc, tabs);
@@ -1397,13 +1438,14 @@ __device__ __forceinline__ void tam_k1_unit(const TamTensor& d, uint32_t u, uint
 
   // ---- first moment ---------------------------------------------------
   if (costate) {
-    TamWave W;  // only its bvalid is read (full unit)
-    W.bvalid = true;
-    TamCsIn c0 = cs, c1 = cs;
-    c0.byte = sbytes & 0xffu;
-    c1.byte = sbytes >> 8;
-    tam_costate_m<true>(d, W, c0, alpha_prev, g, g, m);
-    tam_costate_m<true>(d, W, c1, alpha_prev, g + TAM_EPL, g + TAM_EPL, m + TAM_EPL);
+    if (has_state) {
+      const uint32_t sabs = tam_cs_sabs(cs);  // shared by the lane's two sign bytes
+      tam_cs_decode_m<true>(d, sabs, sbytes & 0xffu, alpha_prev, g, g, m);
+      tam_cs_decode_m<true>(d, sabs, sbytes >> 8, alpha_prev, g + TAM_EPL, g + TAM_EPL, m + TAM_EPL);
+    } else {
+#pragma unroll
+      for (int i = 0; i < TAM_EPU; ++i) m[i] = d.beta1 * 0.0f + d.one_minus_beta1 * g[i];
+    }
     // lane partials in fp32, their fp64 sum, then per block and quarter in fp64
     const double t = tam_unit_sum2((double)tam_lane_dot(g, g) + (double)tam_lane_dot(g + TAM_EPL, g + TAM_EPL),
                                    (double)tam_lane_dot(m, g) + (double)tam_lane_dot(m + TAM_EPL, g + TAM_EPL),
@@ -2785,7 +2827,7 @@ int tam_prepare(TamTensor* tensors, int n_tensors, TamStepInfo* info) {
     t.chunk0 = (uint32_t)chunks;
     t.slice0 = (uint32_t)slices;
     t.c_lr = t.neg_lr / t.bias_correction1;  // fp32 division, correctly rounded
-    t.k_abs = 0x1p-147f / t.bias_correction1;
+    t.k_abs = tam_abs_term(t.bias_correction1, t.eps);
     tiles += nt;
     chunks += tam_alpha_chunks(t.flags, t.ntiles);
     slices += tam_sel_slices(t.flags, t.nb);
