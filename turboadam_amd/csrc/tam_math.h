@@ -45,6 +45,19 @@ struct TamU4 {
   uint32_t x, y, z, w;
 };
 
+// fma(a, b, k) for a constant k that is not an inline operand: on the device
+// one v_fma_f64 reading k from an SGPR pair (the compiler would copy k into
+// the accumulator of a v_fmac_f64 first, a 64-bit move per use).  Same result.
+TAM_HD double tam_fma_k(double a, double b, double k) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  double r;
+  asm("v_fma_f64 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "s"(k));
+  return r;
+#else
+  return __builtin_fma(a, b, k);
+#endif
+}
+
 // a ^ b ^ c in one gfx950 three-input bitwise instruction (truth table 0x96).
 TAM_HD uint32_t tam_xor3(uint32_t a, uint32_t b, uint32_t c) {
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -319,7 +332,7 @@ TAM_HD float tam_logf_with(float x, Tab tab) {
   // log1p(r) ~ r + r^2 * (-1/2 + r/3 - r^2/4 + r^3/5 - r^4/6)
   double q = __builtin_fma(r, -0x1.5555555555555p-3, 0x1.999999999999ap-3);
   q = __builtin_fma(r, q, -0.25);
-  q = __builtin_fma(r, q, 0x1.5555555555555p-2);
+  q = tam_fma_k(r, q, 0x1.5555555555555p-2);
   q = __builtin_fma(r, q, -0.5);
   const double p = __builtin_fma(r * r, q, r);
   const double de = (double)e;
@@ -383,8 +396,8 @@ TAM_HD float tam_expf_with(float xf, Tab tab) {
   const double r = rh + (-kd * TAM_LN2_64_LO);
   // e^r - 1 ~ r + r^2 * (1/2 + r/6 + r^2/24 + r^3/120 + r^4/720)
   double q = __builtin_fma(r, 0x1.6c16c16c16c17p-10, 0x1.1111111111111p-7);
-  q = __builtin_fma(r, q, 0x1.5555555555555p-5);
-  q = __builtin_fma(r, q, 0x1.5555555555555p-3);
+  q = tam_fma_k(r, q, 0x1.5555555555555p-5);
+  q = tam_fma_k(r, q, 0x1.5555555555555p-3);
   q = __builtin_fma(r, q, 0.5);
   const double em1 = __builtin_fma(r * r, q, r);
   const int k = (int)kd;
