@@ -426,6 +426,25 @@ def test_update_betas_outside_unit_interval(betas):
     _check(_edge_run(BF16, init, grads, lr=1e-3, betas=betas))
 
 
+@pytest.mark.parametrize("dt", [BF16, F16])
+def test_update_nonfinite_and_huge_params_beside_finite_ones(dt):
+    # the 16-bit update certifies elements in pairs: NaN, +-inf and finite
+    # values at or above 2^126 (f16: its largest finite values) in one or both
+    # halves of a pair, next to ordinary values
+    log(f"edge: non-finite and huge parameters in pairs, dtype={dt}")
+    rng = np.random.default_rng(78)
+    n = 4096 + 77
+    p = (rng.standard_normal(n) * 0.02).astype(np.float32)
+    big = np.float32(2.0 ** 126 * 1.5) if dt == BF16 else np.float32(60000.0)
+    p[10], p[21], p[22] = np.nan, np.nan, -np.float32(np.nan)  # NaN beside a finite value, NaN pair
+    p[40], p[51], p[60:62] = np.inf, -np.inf, [np.inf, -np.inf]
+    p[100:164:2] = big  # even halves of pairs
+    p[201:265:2] = -big  # odd halves
+    p[300:310] = big
+    grads = _edge_grads(rng, [n], 3, 1e-3)
+    _check(_edge_run(dt, [p], grads, lr=1e-3, weight_decay=0.1))
+
+
 def test_update_near_overflow():
     # parameters near the bf16 maximum and updates near fp32 overflow
     log("edge: near-overflow parameters and updates, bf16")
