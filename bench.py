@@ -150,17 +150,35 @@ def cpu_info():
     return model, os.cpu_count() or 1, usable
 
 
-def cpu_sample(shapes, with_embeddings=False):
-    """The tensors the CPU baseline steps: the whole workload when it has at
-    most FULL_SAMPLE_MAX parameters, otherwise its first decoder layer (the
-    32 identical layers hold 87% of the 8B-shaped set's parameters) and, with
-    with_embeddings, the embedding and the output head as well; in workload
-    order."""
+def cpu_sample(shapes):
+    """The parts of a workload the CPU baseline steps, as (tensors, count)
+    pairs: the whole workload once when it has at most FULL_SAMPLE_MAX
+    parameters; otherwise one tensor of each distinct shape, counted as many
+    times as the workload holds that shape.  On the 8B-shaped set that is the
+    first decoder layer's five shapes, the RMSNorm, and the 525M-parameter
+    embedding standing for itself and the output head (the reference's largest
+    sorts, costate.py:114-118); every tensor of one shape costs the same.
+    Returns (parts, sampled)."""
     total = sum(math.prod(shp) for _, shp in shapes)
     if total <= FULL_SAMPLE_MAX:
-        return list(shapes), False
-    keep = [(n, shp) for n, shp in shapes if n.startswith("l0.") or (with_embeddings and n in ("embed", "lm_head"))]
-    return (keep or list(shapes[:1])), True
+        return [(list(shapes), 1)], False
+    first, count = {}, {}
+    for name, shp in shapes:
+        first.setdefault(shp, name)
+        count[shp] = count.get(shp, 0) + 1
+    return [([(first[shp], shp)], count[shp]) for shp in first], True
+
+
+def host_ram_gib() -> float:
+    """Total host memory in GiB (/proc/meminfo), 0 when unknown."""
+    try:
+        with open("/proc/meminfo") as f:
+            for line in f:
+                if line.startswith("MemTotal:"):
+                    return int(line.split()[1]) / 2**20
+    except (OSError, ValueError, IndexError):
+        pass
+    return 0.0
 
 
 def _time_mirror(TM, shapes, dtype, kw, log_sigma, threads, min_steps, budget_s, gen):
@@ -186,18 +204,20 @@ def _time_mirror(TM, shapes, dtype, kw, log_sigma, threads, min_steps, budget_s,
         torch.set_num_threads(prev)
 
 
-def cpu_baseline(shapes, dtype, kw, log_sigma, budget_s=20.0, with_embeddings=False):
+def cpu_baseline(shapes, dtype, kw, log_sigma, budget_s=20.0):
     """The reference's CPU step timed on this host (BASELINE's CPU plan).
 
     Runs oracle/torch_mirror.py in faithful mode -- the reference CPU path
     restated op for op in torch (it reproduces the reference's outputs bit for
-    bit, tests/test_golden.py) -- on cpu_sample(shapes) with every CPU this
-    process may use (at most OMP_NUM_THREADS when that is set), median of the
-    steady-state steps.  The per-step cost is linear in the parameter count, so
-    a sampled workload's whole step is extrapolated as params / rate.  A
-    1-thread figure is taken on the sample's first tensors up to
-    ONE_THREAD_PARAMS parameters (a leading 1-D slice of the first tensor when
-    that alone is larger).
+    bit, tests/test_golden.py) -- with every CPU this process may use (at most
+    OMP_NUM_THREADS when that is set), median of the steady-state steps.  A
+    workload above FULL_SAMPLE_MAX parameters is timed part by part
+    (cpu_sample: one tensor of each distinct shape) and its whole step is the
+    sum of each part's time times its count; two whole steps of the 8B-shaped
+    set would take several minutes of CPU time (the figure is reported), more
+    than this run may hold the GPU.  A 1-thread figure is taken on the first
+    tensors up to ONE_THREAD_PARAMS parameters (a leading 1-D slice of the
+    first tensor when that alone is larger).
     """
     from oracle import torch_mirror as TM
 
@@ -206,13 +226,20 @@ def cpu_baseline(shapes, dtype, kw, log_sigma, budget_s=20.0, with_embeddings=Fa
     if os.environ.get("OMP_NUM_THREADS", "").isdigit():
         threads = max(1, min(threads, int(os.environ["OMP_NUM_THREADS"])))
     gen = torch.Generator().manual_seed(7)
-    sample, sampled = cpu_sample(shapes, with_embeddings)
-    n_sample = sum(math.prod(shp) for _, shp in sample)
+    parts, sampled = cpu_sample(shapes)
     n_all = sum(math.prod(shp) for _, shp in shapes)
-    t, steps = _time_mirror(TM, sample, dtype, kw, log_sigma, threads, 2, budget_s, gen)
+    n_part = [sum(math.prod(shp) for _, shp in tensors) for tensors, _ in parts]
+    n_sample = sum(n_part)
+    t_step, t_sample, steps = 0.0, 0.0, []
+    for (tensors, count), n in zip(parts, n_part):
+        # each part's share of the time budget follows its size
+        t, k = _time_mirror(TM, tensors, dtype, kw, log_sigma, threads, 2, max(2.0, budget_s * n / n_sample), gen)
+        t_step += count * t
+        t_sample += t
+        steps.append(k)
 
     one, n_one = [], 0
-    for name, shp in sample:
+    for name, shp in (tensors[0] for tensors, _ in parts) if sampled else parts[0][0]:
         n = math.prod(shp)
         if n_one + n > 2 * ONE_THREAD_PARAMS:
             if not one:
@@ -224,18 +251,21 @@ def cpu_baseline(shapes, dtype, kw, log_sigma, budget_s=20.0, with_embeddings=Fa
             break
     t1, steps1 = _time_mirror(TM, one, dtype, kw, log_sigma, 1, 2, budget_s / 2, gen)
 
-    names = ", ".join(n for n, _ in sample[:3]) + (", ..." if len(sample) > 3 else "")
-    part = "first decoder layer + embed + lm_head" if with_embeddings else "first decoder layer"
-    how = (f"{part} ({len(sample)} tensors: {names}; {n_sample} of {n_all} params), "
-           f"whole-step time extrapolated by parameter count" if sampled else
-           f"the whole workload ({len(sample)} tensors, {n_sample} params)")
-    return {"value": n_sample / t, "unit": "params/s", "cores": threads, "kind": "port",
-            "sample": f"{how}, {str(dtype)[6:]}; {steps} steps, median of steps 2+; reference CPU step restated "
-                      f"in torch ops (faithful mirror, bit-identical to the reference), {threads} threads",
-            "ms_per_step_workload": n_all / (n_sample / t) * 1e3,
+    if sampled:
+        listing = "; ".join(f"{tensors[0][0]} {list(tensors[0][1])} x{count}" for tensors, count in parts)
+        how = (f"one tensor of each distinct shape ({listing}; {n_sample} of {n_all} params), each timed on its "
+               f"own; whole step = sum of count x time ({min(steps)}-{max(steps)} steps per part)")
+    else:
+        how = f"the whole workload ({len(parts[0][0])} tensors, {n_sample} params; {steps[0]} steps)"
+    return {"value": n_all / t_step, "unit": "params/s", "cores": threads, "kind": "port",
+            "sample": f"{how}, {str(dtype)[6:]}; median of steps 2+; reference CPU step restated in torch ops "
+                      f"(faithful mirror, bit-identical to the reference), {threads} threads",
+            "ms_per_step_workload": t_step * 1e3,
+            "sample_params_per_s": n_sample / t_sample,
             "one_thread": {"value": n_one / t1, "unit": "params/s", "steps": steps1,
                            "sample": ", ".join(n for n, _ in one) + f" ({n_one} params)"},
-            "cpu_model": model, "cpus_online": online, "cpus_usable": usable}
+            "cpu_model": model, "cpus_online": online, "cpus_usable": usable,
+            "host_ram_gib": round(host_ram_gib(), 1)}
 
 
 # ---------------------------------------------------------------- HBM traffic
@@ -357,9 +387,6 @@ def main():
                     help="extra steps after the timed region, issued pass by pass, that time pass 0")
     ap.add_argument("--stream-rounds", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-with-embeddings", action="store_true",
-                    help="include the embedding and output head in a sampled workload's CPU baseline "
-                         "(several minutes of CPU time on the 8B-shaped set)")
     ap.add_argument("--cpu-baseline-only", action="store_true",
                     help="time only the CPU baseline of the workload (no GPU work)")
     args = ap.parse_args()
@@ -381,7 +408,7 @@ def main():
     shapes = shapes_fn()
     if args.cpu_baseline_only:
         print(json.dumps({"workload": desc, "cpu_baseline": cpu_baseline(
-            shapes, dtype, kw, log_sigma, with_embeddings=args.cpu_with_embeddings)}), flush=True)
+            shapes, dtype, kw, log_sigma)}), flush=True)
         return
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -500,7 +527,7 @@ def main():
         },
     }
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(shapes, dtype, kw, log_sigma, with_embeddings=args.cpu_with_embeddings)
+        out["cpu_baseline"] = cpu_baseline(shapes, dtype, kw, log_sigma)
     print(json.dumps(out), flush=True)
 
 

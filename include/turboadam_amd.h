@@ -68,14 +68,18 @@ extern "C" {
 typedef struct TamTensor {
   void* param;          /* [in] n elements of dtype, updated in place        */
   const void* grad;     /* [in] n elements of dtype                          */
-  uint8_t* v_idx;       /* [in] COMPRESS_V: u8[nb*128] 1Q indices (in/out)   */
-  uint16_t* v_scales;   /* [in] COMPRESS_V: f16[nb*2] (log_min, log_max)     */
+  uint8_t* v_idx;       /* [in] COMPRESS_V: u8[nb*128] 1Q indices (in/out),  */
+                        /*      16-byte aligned                              */
+  uint16_t* v_scales;   /* [in] COMPRESS_V: f16[nb*2] (log_min, log_max),    */
+                        /*      4-byte aligned                               */
   float* exp_avg_sq;    /* [in] !COMPRESS_V: f32[n] second moment            */
   float* exp_avg;       /* [in] !COSTATE: f32[n] first moment                */
-  uint8_t* signs;       /* [in] COSTATE: u8[ceil(n/8)] sign bits, MSB first  */
+  uint8_t* signs;       /* [in] COSTATE: u8[ceil(n/8)] sign bits, MSB first, */
+                        /*      2-byte aligned                               */
   uint8_t* labels;      /* [in] COSTATE: u8[nb] 0 null, 1 phase, 2 amplitude */
   float* norms;         /* [in] COSTATE: f32[nb] residual block L2 norms     */
   uint16_t* amp;        /* [in] COSTATE: f16[nb] amplitude scales            */
+                        /*      (norms and alpha 4-byte, amp 2-byte aligned) */
   float* alpha;         /* [in] COSTATE: f32[1] projection alpha (in/out)    */
   uint64_t n;           /* [in] number of elements (>= 1)                    */
   uint32_t dtype;       /* [in] TAM_DTYPE_* of param and grad                */

@@ -69,17 +69,20 @@ def test_ragged_sweep_workloads():
 
 
 def test_cpu_baseline_sample():
-    # workloads up to 300M parameters run whole; the 8B-shaped set samples its first decoder layer
+    # workloads up to 300M parameters run whole; the 8B-shaped set is timed one
+    # tensor per distinct shape, each counted as often as the set holds it
     for name in ("c0", "c1", "c2", "c4"):
         shapes = bench.WORKLOADS[name][0]()
-        assert bench.cpu_sample(shapes) == (list(shapes), False)
-    sample, sampled = bench.cpu_sample(bench.llama3_8b_shapes())
-    assert sampled and [n for n, _ in sample] == [f"l0.{k}" for k in
-                                                   ("q", "k", "v", "o", "gate", "up", "down", "norm1", "norm2")]
-    assert _count(sample)[1] == 218_112_000
-    sample, _ = bench.cpu_sample(bench.llama3_8b_shapes(), with_embeddings=True)
-    assert [n for n, _ in sample][0] == "embed" and [n for n, _ in sample][-1] == "lm_head"
-    assert _count(sample) == (11, 218_112_000 + 2 * 128256 * 4096)
+        assert bench.cpu_sample(shapes) == ([(list(shapes), 1)], False)
+    shapes = bench.llama3_8b_shapes()
+    parts, sampled = bench.cpu_sample(shapes)
+    assert sampled
+    names = {tensors[0][0]: count for tensors, count in parts}
+    assert names == {"embed": 2, "l0.q": 64, "l0.k": 64, "l0.gate": 64, "l0.down": 32, "l0.norm1": 65}
+    assert all(len(tensors) == 1 for tensors, _ in parts)
+    # the counts rebuild the whole set
+    assert sum(math.prod(t[0][1]) * c for t, c in parts) == _count(shapes)[1] == 8_030_261_248
+    assert len(shapes) == sum(c for _, c in parts)
 
 
 def test_kernel_source_sha_gates_the_traffic_figure():

@@ -151,3 +151,35 @@ def test_steps_on_alternating_streams_equal_one_stream():
             bad.append(f"tensor {i}: params differ")
         bad += compare_states(gpu_state(ob, b), gpu_state(oa, a), f"tensor {i}")
     assert not bad, "\n".join(bad[:20])
+
+
+def test_capturable_eager_steps_follow_a_betas_change():
+    """Eager steps of a capturable optimizer whose betas change mid-run: the
+    bias corrections come from the device table of the betas in force (the
+    descriptor table is rebuilt for the new betas), as the oracle computes
+    them from the group's betas at each step."""
+    from turboadam_amd import TurboAdam
+
+    dev = torch.device("cuda:0")
+    sizes = [5000, 300, 9000]
+    dts = [F32, F32, BF16]
+    rng = np.random.default_rng(33)
+    init = [to_bits((rng.standard_normal(n) * 0.02).astype(np.float32), dt) for n, dt in zip(sizes, dts)]
+    params = [torch.nn.Parameter(to_torch(a, dt, (n,), dev)) for a, dt, n in zip(init, dts, sizes)]
+    kw = dict(lr=1e-3, weight_decay=0.01)
+    opt = TurboAdam(params, capturable=True, philox_seed=778, **kw)
+    oparams = [a.copy() for a in init]
+    orc = O.OracleTurboAdam(oparams, dtypes=list(dts), seed=778, **kw)
+    for step in range(6):
+        if step == 3:
+            opt.param_groups[0]["betas"] = (0.8, 0.99)
+            orc.param_groups[0]["betas"] = (0.8, 0.99)
+        gs = [to_bits((rng.standard_normal(n) * 1e-3).astype(np.float32), dt) for n, dt in zip(sizes, dts)]
+        for p, g, dt, n in zip(params, gs, dts, sizes):
+            p.grad = to_torch(g, dt, (n,), dev)
+        opt.step()
+        orc.step(gs)
+        torch.cuda.synchronize()
+        bad = compare_with_oracle(opt, params, orc, oparams, f"step {step + 1}", sizes)
+        assert not bad, "\n".join(bad[:20])
+    log("6 eager capturable steps, betas changed before step 4")

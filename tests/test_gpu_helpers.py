@@ -273,3 +273,22 @@ def test_compress_v_logscale_init_closed_form():
     assert torch.equal(comp["indices"], init["indices"])
     assert torch.equal(comp["scales"].view(torch.int16), init["scales"].view(torch.int16))
     assert comp["original_length"] == 5000 and comp["original_shape"] == p.shape
+
+
+def test_compress_v_logscale_matches_reference_fixture():
+    """compress_v_logscale on a ragged v (5000 elements: the last block is padded
+    with max(min(v), 1e-38), formed on the device) equals the reference's own
+    output (golden_compress_b4: exact zeros, ~35 e-folds of range)."""
+    import os
+
+    from tests.golden import make_golden as MG
+    from turboadam_amd import oneq
+
+    z = np.load(os.path.join(os.path.dirname(__file__), "golden", "golden_compress_b4.npz"))
+    v = z["v"]
+    case = MG.Q_CASES["compress_b4"]
+    comp = oneq.compress_v_logscale(_t(v), n_bits=case["bits"])
+    log(f"compress_v_logscale n={v.size} bits={case['bits']} vs the reference fixture")
+    assert _same(_np(comp["indices"]), z["indices"])
+    assert _same(_np(comp["scales"]).reshape(-1), z["scales"].reshape(-1))
+    assert comp["original_length"] == v.size and comp["original_shape"] == torch.Size([v.size])

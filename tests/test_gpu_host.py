@@ -121,3 +121,74 @@ def test_replaced_parameter_storage_is_followed():
         assert not bad, "\n".join(bad[:20])
     assert params[1].dtype == torch.bfloat16
     log("8 steps with a storage swap at step 4 and an fp32 -> bf16 swap at step 6")
+
+
+def test_replaced_or_reset_state_is_followed():
+    """State tensors replaced between steps by copies of themselves (exp_avg,
+    the 1Q indices and scales, every CoState array and alpha), and state
+    reset by opt.state[p] = {} and by opt.state.clear(): each following step
+    must step the state that opt.state now holds, re-initialised where it was
+    reset, as the oracle does.  The replaced tensors stay referenced, so a
+    descriptor row that kept pointing at them would update them instead and
+    show as a mismatch.  Gradients are new tensors every step, so every other
+    step takes the steady path."""
+    from turboadam_amd import TurboAdam
+
+    dev = torch.device("cuda:0")
+    sizes = [5000, 300, 4096 + 77, 9000]
+    dts = [F32, F32, BF16, BF16]
+    rng = np.random.default_rng(53)
+    init = [to_bits((rng.standard_normal(n) * 0.02).astype(np.float32), dt) for n, dt in zip(sizes, dts)]
+    params = [torch.nn.Parameter(to_torch(a, dt, (n,), dev)) for a, dt, n in zip(init, dts, sizes)]
+    kw = dict(lr=1e-3, weight_decay=0.02)
+    opt = TurboAdam(params, philox_seed=23, **kw)
+    oparams = [a.copy() for a in init]
+    orc = O.OracleTurboAdam(oparams, dtypes=list(dts), seed=23, **kw)
+    taken = []
+    fast_step = opt._fast_step
+
+    def spy():
+        r = fast_step()
+        taken.append(r)
+        return r
+
+    opt._fast_step = spy
+    old = []  # replaced tensors, kept alive
+
+    def swap(holder, key):
+        old.append(holder[key])
+        holder[key] = holder[key].clone()
+
+    for step in range(14):
+        if step == 3:  # same values, new tensors
+            st0, st1 = opt.state[params[0]], opt.state[params[1]]
+            swap(st1, "exp_avg")
+            swap(st0["compressed_v"], "indices")
+            swap(st1["compressed_v"], "scales")
+            enc = st0["m_mgr"]._encoded
+            for key in ("sign_packed", "labels", "block_norms", "scales"):
+                swap(enc, key)
+        if step == 5:
+            mgr = opt.state[params[2]]["m_mgr"]
+            old.append(mgr._alpha)
+            mgr._alpha = mgr._alpha.clone()
+        if step == 7:  # one parameter's state reset: initialised again at this step
+            opt.state[params[2]] = {}
+            del orc.state[2]
+        if step == 10:  # every state reset
+            opt.state.clear()
+            orc.state.clear()
+        gs = [to_bits((rng.standard_normal(n) * 1e-3 * (1 + step % 3)).astype(np.float32), dt)
+              for n, dt in zip(sizes, dts)]
+        for p, g, dt, n in zip(params, gs, dts, sizes):
+            p.grad = to_torch(g, dt, (n,), dev)
+        opt.step()
+        orc.step(gs)
+        torch.cuda.synchronize()
+        bad = compare_with_oracle(opt, params, orc, oparams, f"step {step + 1}")
+        assert not bad, "\n".join(bad[:20])
+    steady = [i + 1 for i, r in enumerate(taken) if r]
+    log(f"14 steps; steady path taken at steps {steady}")
+    for s in (4, 6, 8, 11):  # the step after each change takes the full path
+        assert s not in steady
+    assert taken[-1]

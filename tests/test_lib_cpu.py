@@ -88,6 +88,12 @@ def test_prepare_layout():
     (lambda t: setattr(t, "dtype", 7), "dtype"),
     (lambda t: setattr(t, "alpha", 0), "CoState"),
     (lambda t: setattr(t, "v_idx", 0x30001), "misaligned"),
+    (lambda t: setattr(t, "v_idx", 0x30008), "misaligned v state"),  # pass 0 loads 16 bytes per lane
+    (lambda t: setattr(t, "v_scales", 0x40002), "misaligned v state"),
+    (lambda t: setattr(t, "signs", 0x60001), "misaligned CoState"),
+    (lambda t: setattr(t, "norms", 0x60002), "misaligned CoState"),
+    (lambda t: setattr(t, "amp", 0x60001), "misaligned CoState"),
+    (lambda t: setattr(t, "alpha", 0x60002), "misaligned CoState"),
     (lambda t: setattr(t, "k_hi", 10_000), "rank"),
     (lambda t: setattr(t, "sqrt_block", 11.0), "sqrt_block"),
     (lambda t: setattr(t, "found_inf", 0x4000), "found_inf"),  # a skip flag needs DEVICE_STEP
@@ -167,3 +173,60 @@ def test_philox_seed_keyword():
         TurboAdam(ps, philox_seed=-1)
     with pytest.raises(TypeError):
         TurboAdam(ps, 1e-3, (0.9, 0.999), 1e-8, 0.0, 128, 4, True, True, 0.1, 0.9, False, False, 4096, 7)
+
+
+def test_steady_step_sees_replaced_or_reset_state():
+    """The steady path's state check (TurboAdam._fast_state_kept): a replaced
+    state tensor, a reset per-parameter dict or a cleared opt.state make the
+    next step take the full path; an unchanged state passes.  The state is
+    built on the CPU in the optimizer's layout (no step runs here)."""
+    from turboadam_amd.costate import CoStateManager
+    from turboadam_amd.optimizer import TurboAdam, _FastStep, _row_tensors, _tensor_ptrs
+
+    params = [torch.nn.Parameter(torch.zeros(n)) for n in (5000, 300)]
+    opt = TurboAdam(params)
+    for p in params:
+        st = opt.state[p]
+        st["step"] = 3
+        st["compressed_v"] = {"indices": torch.zeros(128 * ((p.numel() + 127) // 128), dtype=torch.uint8),
+                              "scales": torch.zeros(2 * ((p.numel() + 127) // 128), dtype=torch.float16)}
+        st["_compress_m"] = p.numel() >= 4096
+        if st["_compress_m"]:
+            mgr = st["m_mgr"] = CoStateManager()
+            mgr.allocate(p.numel(), torch.device("cpu"))
+        else:
+            st["exp_avg"] = torch.zeros(p.numel())
+
+    class Plan:
+        row_cv = [True, True]
+
+    def fast():
+        states = [opt.state[p] for p in params]
+        return _FastStep(0, torch.device("cuda", 0), params, [True, True], [0, 1], states, [None, None],
+                         [torch.float32] * 2, [], Plan, opt.state)
+
+    assert opt._fast_state_kept(fast())
+    replace = [
+        lambda: opt.state[params[1]].__setitem__("exp_avg", torch.zeros(300)),
+        lambda: opt.state[params[0]]["compressed_v"].__setitem__("indices", torch.zeros(5120, dtype=torch.uint8)),
+        lambda: opt.state[params[1]]["compressed_v"].__setitem__("scales", torch.zeros(6, dtype=torch.float16)),
+        lambda: opt.state[params[0]]["m_mgr"]._encoded.__setitem__("labels", torch.zeros(40, dtype=torch.uint8)),
+        lambda: setattr(opt.state[params[0]]["m_mgr"], "_alpha", torch.zeros(())),
+        lambda: opt.state.__setitem__(params[0], {}),
+        lambda: opt.state.clear(),
+    ]
+    for k, change in enumerate(replace):
+        f = fast()
+        saved = {p: dict(opt.state[p]) for p in params}
+        mgr = opt.state[params[0]]["m_mgr"]
+        saved_mgr = (mgr._alpha, dict(mgr._encoded))
+        change()
+        assert not opt._fast_state_kept(f), k
+        for p in params:  # restore for the next case
+            opt.state[p] = saved[p]
+        mgr._alpha, mgr._encoded = saved_mgr[0], saved_mgr[1]
+        for p in params:
+            opt.state[p]["compressed_v"] = dict(saved[p]["compressed_v"])
+    # the full path compares device addresses of the same tensors
+    rows = [_row_tensors(opt.state[p], True) for p in params]
+    assert len(_tensor_ptrs(rows)) == 8 + 3 and _tensor_ptrs(rows)[7] == 0  # no error-feedback residual

@@ -2792,7 +2792,9 @@ int tam_prepare(TamTensor* tensors, int n_tensors, TamStepInfo* info) {
       if (!(t.v_bits == 2 || t.v_bits == 3 || t.v_bits == 4 || t.v_bits == 6 || t.v_bits == 8))
         return tam_fail(TAM_E_INVALID, "%stensor %ld: v_bits must be 2, 3, 4, 6 or 8", "", i);
       if (!t.v_idx || !t.v_scales) return tam_fail(TAM_E_INVALID, "%stensor %ld: null v state", "", i);
-      if (((uintptr_t)t.v_idx & 7u) || ((uintptr_t)t.v_scales & 3u))
+      // 16-byte index loads and stores of a unit's 16 elements per lane; one
+      // 32-bit (lmin, lmax) word per block
+      if (((uintptr_t)t.v_idx & 15u) || ((uintptr_t)t.v_scales & 3u))
         return tam_fail(TAM_E_INVALID, "%stensor %ld: misaligned v state", "", i);
     } else if (!t.exp_avg_sq || ((uintptr_t)t.exp_avg_sq & 15u)) {
       return tam_fail(TAM_E_INVALID, "%stensor %ld: exp_avg_sq null or misaligned", "", i);
@@ -2800,6 +2802,11 @@ int tam_prepare(TamTensor* tensors, int n_tensors, TamStepInfo* info) {
     if (t.flags & TAM_FLAG_COSTATE) {
       if (!t.signs || !t.labels || !t.norms || !t.amp || !t.alpha)
         return tam_fail(TAM_E_INVALID, "%stensor %ld: null CoState state", "", i);
+      // 16-bit sign loads and stores (a lane's 16 elements), f32 norms and
+      // alpha, f16 amplitudes
+      if (((uintptr_t)t.signs & 1u) || ((uintptr_t)t.norms & 3u) || ((uintptr_t)t.amp & 1u) ||
+          ((uintptr_t)t.alpha & 3u))
+        return tam_fail(TAM_E_INVALID, "%stensor %ld: misaligned CoState state", "", i);
       if (t.k_lo >= nb || t.k_hi >= nb) return tam_fail(TAM_E_INVALID, "%stensor %ld: rank out of range", "", i);
       t.ratio_off = ratio_blocks;
       ratio_blocks += (nb + 3) & ~3ull;  // 16-byte aligned per tensor
@@ -3077,6 +3084,8 @@ int tam_costate_decode(const uint8_t* labels, const uint8_t* signs, const float*
   tam_err_buf[0] = 0;
   if (!g || !m_out || (has_state && (!labels || !signs || !norms || !amp || !alpha)))
     return tam_fail(TAM_E_INVALID, "%snull argument", "");
+  if (((uintptr_t)norms | (uintptr_t)alpha) & 3u || (uintptr_t)amp & 1u)
+    return tam_fail(TAM_E_INVALID, "%smisaligned CoState state", "");
   if (tam_check_dtype(g_dtype)) return TAM_E_INVALID;
   if (n == 0) return TAM_OK;
   hipLaunchKernelGGL(tam_k_decode, dim3(tam_tiles_of(n)), dim3(TAM_WG), 0, (hipStream_t)stream, labels, signs, norms,
@@ -3199,6 +3208,7 @@ int tam_classify(const float* ratios, uint64_t nb, const float* taus, uint8_t* l
 int tam_costate_encode(const float* delta, uint64_t n, uint8_t* signs, float* norms, uint16_t* amp, void* stream) {
   tam_err_buf[0] = 0;
   if (!delta || !signs || !norms || !amp) return tam_fail(TAM_E_INVALID, "%snull argument", "");
+  if ((uintptr_t)norms & 3u || (uintptr_t)amp & 1u) return tam_fail(TAM_E_INVALID, "%smisaligned CoState state", "");
   if (n == 0) return TAM_OK;
   hipLaunchKernelGGL(tam_k_encode, dim3(tam_tiles_of(n)), dim3(TAM_WG), 0, (hipStream_t)stream, delta, n, signs,
                      norms, amp);

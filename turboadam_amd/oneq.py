@@ -10,7 +10,7 @@ import torch
 
 from . import _lib
 from .quantize import DEFAULT_SEED, _dequantize_operands, quantize_logscale_nbits
-from .utils import BLOCK_SIZE, num_blocks, pad_to_blocks
+from .utils import BLOCK_SIZE, num_blocks
 
 # TurboAdam starts v from full(1e-30) quantised deterministically
 # (reference optimizer.py:273-280 -> oneq.py:13-48 -> quantize.py:177-178):
@@ -38,24 +38,24 @@ def init_v_state(param: torch.Tensor, n_bits: int, block_size: int = BLOCK_SIZE)
 def compress_v_logscale(v: torch.Tensor, n_bits: int = 3, block_size: int = BLOCK_SIZE,
                         stochastic_round: bool = False, *, tensor_id: int = 0, step: int = 1,
                         seed: int = DEFAULT_SEED) -> dict:
-    """Compress v (reference oneq.py:13-48): pad to whole blocks with
-    max(min(v), 1e-38), then quantize_logscale_nbits."""
-    original_shape = v.shape
-    v_flat = v.reshape(-1).float()
-    v_min = v_flat.min().item()
-    pad_value = max(v_min, 1e-38)
-    v_padded, original_length = pad_to_blocks(v_flat, block_size, pad_value=pad_value)
-    indices, scales, _ = quantize_logscale_nbits(v_padded, n_bits=n_bits, block_size=block_size,
+    """Compress v into the 1Q state dict (reference oneq.py:13-48).
+
+    The last block is filled up to block_size elements with the fp32 value
+    max(min(v), 1e-38): padding can then neither lower the block's minimum
+    nor (a log of zero) make it infinite.  That value is formed on the device
+    (the reference reads min(v) back to the host first); the blocks then go
+    through quantize_logscale_nbits."""
+    flat = v.reshape(-1).to(torch.float32)
+    count = flat.numel()
+    blocks = torch.empty(num_blocks(count, block_size) * block_size, dtype=torch.float32, device=flat.device)
+    blocks[:count] = flat
+    if blocks.numel() > count:
+        blocks[count:] = flat.min().clamp(min=1e-38)  # NaN stays NaN, as Python's max(nan, 1e-38)
+    indices, scales, _ = quantize_logscale_nbits(blocks, n_bits=n_bits, block_size=block_size,
                                                  stochastic_round=stochastic_round, tensor_id=tensor_id,
                                                  step=step, seed=seed)
-    return {
-        "indices": indices,
-        "scales": scales,
-        "n_bits": n_bits,
-        "original_shape": original_shape,
-        "original_length": original_length,
-        "block_size": block_size,
-    }
+    return dict(indices=indices, scales=scales, n_bits=n_bits, original_shape=v.shape, original_length=count,
+                block_size=block_size)
 
 
 def decompress_v(compressed: dict) -> torch.Tensor:

@@ -12,6 +12,8 @@ loop.  Parameters must live on a HIP device; there is no CPU path.
 
 import ctypes
 import math
+import operator
+from itertools import chain
 
 import numpy as np
 import torch
@@ -50,6 +52,29 @@ _ROW_FIELDS = ("param", "grad", "v_idx", "v_scales", "exp_avg_sq", "exp_avg", "s
 _GROUP_FIELDS = ("c_wd", "beta1", "one_minus_beta1", "beta2", "one_minus_beta2", "bias_correction1",
                  "bias_correction2", "inv_bc2", "inv_bc2_f32", "eps", "neg_lr", "sqrt_block")
 _SQRT_BLOCK_F32 = _f32(math.sqrt(BLOCK_SIZE))
+
+
+def _row_tensors(state, compress_v: bool) -> tuple:
+    """The state tensors a descriptor row points at, in a fixed order (None
+    where a row has no such array).  A kept descriptor table is valid only
+    while these are the same tensors: code that replaces one (a reset, an
+    offload round trip) must make the next step rebuild its row."""
+    if compress_v:
+        cv = state["compressed_v"]
+        v = (cv["indices"], cv["scales"])
+    else:
+        v = (state["exp_avg_sq"],)
+    if state["_compress_m"]:
+        mgr = state["m_mgr"]
+        enc = mgr._encoded
+        return v + (enc["sign_packed"], enc["labels"], enc["block_norms"], enc["scales"], mgr._alpha,
+                    mgr._ef_residual)
+    return v + (state["exp_avg"],)
+
+
+def _tensor_ptrs(rows) -> list:
+    """Device addresses of _row_tensors rows, flattened (0 for None)."""
+    return [0 if t is None else t.data_ptr() for row in rows for t in row]
 
 
 class _DeviceBuffers:
@@ -119,6 +144,8 @@ class _StepPlan:
 
     def __init__(self, key, table, gsel, groups, static_flags, costate, ef, capturable):
         self.key = key
+        self.state_ptrs = None  # _tensor_ptrs of the rows' state tensors when the table was built
+        self.row_cv = None      # compress_v of each row's group when the table was built
         self.table = table
         self.gsel = gsel              # group row of each descriptor row
         self.groups = groups          # (group, group_idx) of each group row
@@ -167,10 +194,22 @@ class _FastStep:
     comprehensions, checked only when a gradient object is new (dtype, layout,
     contiguity, device), the parameters' storage pointers are compared with the
     kept descriptor rows (p.data replaced: not steady), and the step numbers
-    and bias corrections come from the kept state dicts."""
+    and bias corrections come from the kept state dicts.
 
-    def __init__(self, version, device, params, absent, rows, states, grads, pdtypes, bc_src, plan):
+    A step is not steady either when opt.state no longer holds the kept
+    per-parameter dicts in the same order (cleared, an entry replaced or
+    removed) or when a row's state tensors (_row_tensors) are not the kept
+    objects; the full path then rebuilds what changed.  A state tensor is
+    recognised by identity here; the full path compares device addresses."""
+
+    def __init__(self, version, device, params, absent, rows, states, grads, pdtypes, bc_src, plan, state_map):
         self.version = version
+        # the optimizer's state mapping and its per-parameter dicts, in order:
+        # opt.state.clear(), opt.state[p] = {} or a new mapping is not steady
+        self.state_map = state_map
+        self.state_values = list(state_map.values())
+        # the state tensors of each row (_row_tensors), by identity
+        self.tensors = [t for st, cv in zip(states, plan.row_cv) for t in _row_tensors(st, cv)]
         self.device = device
         self.dev_index = device.index if device.index is not None else torch.cuda.current_device()
         self.params = params      # every parameter of the optimizer, in order
@@ -584,6 +623,8 @@ class TurboAdam(Optimizer):
             self._describe_device_step(table, device, device_step)
         plan.static_flags = table["flags"] & np.uint32(
             ~(_lib.TAM_FLAG_HAS_STATE | _lib.TAM_FLAG_HAS_EF | _lib.TAM_FLAG_WD) & 0xFFFFFFFF)
+        plan.row_cv = [bool(group["compress_v"]) for _, _, group, _, _ in items]
+        plan.state_ptrs = _tensor_ptrs(_row_tensors(it[1], cv) for it, cv in zip(items, plan.row_cv))
         return plan
 
     def _set_group_fields(self, plan, device, group_rows=None) -> None:
@@ -720,9 +761,21 @@ class TurboAdam(Optimizer):
             if self._found_inf is not None:
                 self._skip_ptr = self._skip_flag(device, self._found_inf).data_ptr()
         # a parameter whose storage was replaced (p.data = ..., a dtype or
-        # device change) needs its descriptor row rebuilt
-        key = (tuple(it[4] for it in items), tuple(it[0].data_ptr() for it in items))
+        # device change) needs its descriptor row rebuilt; so does a row whose
+        # state tensors were replaced, and a capturable group whose betas
+        # changed (its bias-correction table, _describe_device_step)
+        key = (tuple(it[4] for it in items), tuple(it[0].data_ptr() for it in items),
+               tuple(tuple(g["betas"]) for g in self.param_groups if g.get("capturable")))
         plan = self._plans.get(device)
+        if plan is not None and plan.key == (key, self._layout_version):
+            try:
+                row_cv = [bool(it[2]["compress_v"]) for it in items]
+                same = row_cv == plan.row_cv and _tensor_ptrs(
+                    _row_tensors(it[1], cv) for it, cv in zip(items, row_cv)) == plan.state_ptrs
+            except KeyError:
+                same = False
+            if not same:
+                plan = None
         if plan is None or plan.key != (key, self._layout_version):
             plan = self._describe(device, items)
             plan.key = (key, self._layout_version)  # after _describe, which may create an EF residual
@@ -801,12 +854,25 @@ class TurboAdam(Optimizer):
                 bc_src.append(((group_idx, device.type, device.index), group, src))
         self._fast = _FastStep(self._layout_version, device, params, [p.grad is None for p in params], rows,
                                [it[1] for it in items], [it[0].grad for it in items], [it[0].dtype for it in items],
-                               bc_src, plan)
+                               bc_src, plan, self.state)
+
+    def _fast_state_kept(self, f) -> bool:
+        """Whether opt.state still holds f's per-parameter dicts, in order, and
+        each descriptor row's state tensors are the objects f kept."""
+        st = self.state
+        if st is not f.state_map or len(st) != len(f.state_values) or \
+                not all(map(operator.is_, st.values(), f.state_values)):
+            return False
+        try:
+            cur = list(chain.from_iterable(map(_row_tensors, f.states, f.plan.row_cv)))
+        except KeyError:  # a state entry was removed
+            return False
+        return len(cur) == len(f.tensors) and all(map(operator.is_, cur, f.tensors))
 
     def _fast_step(self) -> bool:
         """A steady step (_FastStep) if this one is; False (nothing done) otherwise."""
         f = self._fast
-        if f is None or f.version != self._layout_version:
+        if f is None or f.version != self._layout_version or not self._fast_state_kept(f):
             return False
         gs = [p.grad for p in f.params]
         if [g is None for g in gs] != f.absent:
