@@ -327,52 +327,132 @@ def copy_reference(args):
 
 # ---------------------------------------------------------------- streaming ceiling
 STREAM_KINDS = {"read": (0, 1), "write": (1, 1), "copy": (2, 2), "2r1w": (3, 3), "inplace": (4, 3)}
+STREAM_LAYOUTS = {0: "grid-stride", 1: "wave-contiguous", 2: "lane-contiguous"}
 
 
-def stream_reference(args):
-    """Bandwidth of plain streaming kernels (turboadam_amd/csrc/tam_stream.hip):
-    read, write, copy, two reads + one write to a third array, and an in-place
-    read-modify-write of one array with a read of a second (the access shape of
-    the step's parameter update), each with ordinary and with nontemporal loads
-    and stores, over 4 GiB per array.  Prints one JSON line per kernel."""
+def _stream_lib():
     import ctypes
 
     from turboadam_amd.build import STREAM_LIB_PATH
 
     lib = ctypes.CDLL(STREAM_LIB_PATH)
     lib.tam_stream_run.restype = ctypes.c_long
-    lib.tam_stream_run.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
-                                   ctypes.c_uint64, ctypes.c_int, ctypes.c_void_p]
+    lib.tam_stream_run.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                   ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint64, ctypes.c_int,
+                                   ctypes.c_void_p]
+    lib.tam_stream_pass0.restype = ctypes.c_long
+    lib.tam_stream_pass0.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint64, ctypes.c_int, ctypes.c_int,
+                                     ctypes.c_int, ctypes.c_uint32, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    lib.tam_stream_pass0_sizes.restype = None
+    lib.tam_stream_pass0_sizes.argtypes = [ctypes.c_uint64, ctypes.POINTER(ctypes.c_uint64)]
+    return lib
+
+
+def _time_launches(launch, warmup: int, steps: int, stream) -> float:
+    """Milliseconds per launch (HIP events on the launch stream)."""
+    for _ in range(max(1, warmup)):
+        launch()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for _ in range(steps):
+        launch()
+    b.record(stream)
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / steps
+
+
+def stream_reference(args):
+    """Bandwidth of plain streaming kernels (turboadam_amd/csrc/tam_stream.hip)
+    over 4 GiB per array: read, write, copy, two reads + one write to a third
+    array, and an in-place read-modify-write of one array with a read of a
+    second (the access shape of the step's parameter update).  Sweeps words in
+    flight per lane (4, 8, 16), workgroup size (256, 512, 1024), grid rounds
+    (1-16), nontemporal loads and stores off and on, and three access layouts
+    (STREAM_LAYOUTS).  Prints one JSON line per variant, then the best variant
+    of each kind."""
+    lib = _stream_lib()
     dev = torch.device("cuda:0")
     n16 = 1 << 28  # 16-byte words per array: 4 GiB
     bufs = [torch.ones(n16 * 4, dtype=torch.int32, device=dev) for _ in range(3)]
     stream = torch.cuda.current_stream(dev)
-    results = {}
+    best = {}
     for name, (kind, arrays) in STREAM_KINDS.items():
         for nt in (0, 1):
-            def launch():
-                g = lib.tam_stream_run(kind, nt, bufs[0].data_ptr(), bufs[1].data_ptr(), bufs[2].data_ptr(), n16,
-                                       args.stream_rounds, stream.cuda_stream)
-                if g < 0:
-                    raise RuntimeError(f"tam_stream_run failed ({g})")
-                return g
-            for _ in range(max(1, args.warmup)):
-                grid = launch()
-            torch.cuda.synchronize()
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record(stream)
-            for _ in range(args.steps):
-                launch()
-            b.record(stream)
-            torch.cuda.synchronize()
-            ms = a.elapsed_time(b) / args.steps
-            nbytes = arrays * n16 * 16
-            gbps = nbytes / (ms * 1e-3) / 1e9
-            results[f"{name}{'_nt' if nt else ''}"] = gbps
-            print(json.dumps({"workload": "stream", "kernel": name, "nontemporal": bool(nt), "grid": grid,
-                              "ms_per_launch": ms, "bytes_per_launch": nbytes, "GBps": gbps,
-                              "frac_of_8TBps": gbps / HBM_PEAK_GBPS}), flush=True)
-    print(json.dumps({"workload": "stream", "summary_GBps": results}), flush=True)
+            for words in (4, 8, 16):
+                for wg in (256, 512, 1024):
+                    for layout in STREAM_LAYOUTS:
+                        for rounds in (1, 2, 4, 8, 16):
+                            grid = [0]
+
+                            def launch():
+                                grid[0] = lib.tam_stream_run(kind, nt, words, wg, layout, bufs[0].data_ptr(),
+                                                             bufs[1].data_ptr(), bufs[2].data_ptr(), n16, rounds,
+                                                             stream.cuda_stream)
+                                if grid[0] < 0:
+                                    raise ValueError(grid[0])
+
+                            try:
+                                ms = _time_launches(launch, 1, args.steps, stream)
+                            except ValueError:
+                                continue  # a combination the library refuses (register budget)
+                            nbytes = arrays * n16 * 16
+                            gbps = nbytes / (ms * 1e-3) / 1e9
+                            rec = {"workload": "stream", "kernel": name, "nontemporal": bool(nt), "words": words,
+                                   "wg": wg, "layout": STREAM_LAYOUTS[layout], "rounds": rounds, "grid": grid[0],
+                                   "ms_per_launch": ms, "bytes_per_launch": nbytes, "GBps": gbps,
+                                   "frac_of_8TBps": gbps / HBM_PEAK_GBPS}
+                            print(json.dumps(rec), flush=True)
+                            if gbps > best.get(name, {}).get("GBps", 0.0):
+                                best[name] = rec
+    print(json.dumps({"workload": "stream", "best": best}), flush=True)
+
+
+def stream_pass0_reference(args):
+    """Bandwidth of a stream with the step's first pass's arrays and access
+    widths (tam_stream_pass0: 16-bit parameter and gradient, u8 1Q indices,
+    per-block scales and CoState bytes, partial sums), 2^30 elements, across
+    workgroup sizes, workgroups per CU, grid rounds, and with or without an
+    LDS allocation that caps a CU at 4 waves per SIMD (the main pass-0 kernels'
+    register budget), for two element-to-lane layouts with and without
+    nontemporal access.  One JSON line per variant, then the best."""
+    import ctypes
+
+    lib = _stream_lib()
+    dev = torch.device("cuda:0")
+    units = 1 << 20
+    sizes = (ctypes.c_uint64 * 9)()
+    lib.tam_stream_pass0_sizes(units, sizes)
+    bufs = [torch.ones((int(s) + 255) // 4, dtype=torch.int32, device=dev) for s in sizes]
+    ptrs = (ctypes.c_void_p * 9)(*[b.data_ptr() for b in bufs])
+    stream = torch.cuda.current_stream(dev)
+    # bytes per launch: the parameter and indices and scales are read and written
+    nbytes = int(sum(sizes)) + int(sizes[0]) + int(sizes[2]) + int(sizes[3])
+    best = None
+    variants = [(layout, nt, wg, per_cu, rounds, cap) for layout, nt in ((0, 0), (0, 1), (1, 0), (1, 1))
+                for wg in (128, 256) for per_cu in (4, 8, 16) for rounds in (1, 4, 16) for cap in (False, True)]
+    # larger grids, up to one unit per wave (lane layout, capped)
+    variants += [(0, nt, wg, per_cu, rounds, True) for nt in (0, 1) for wg in (128, 256)
+                 for per_cu in (32, 64) for rounds in (16, 64)]
+    for layout, nt, wg, per_cu, rounds, cap in variants:
+        lds = (163840 // (16 * 64 // wg)) if cap else 0  # 16 waves per CU when capped
+
+        def launch():
+            g = lib.tam_stream_pass0(ptrs, units, wg, per_cu, rounds, lds, layout, nt,
+                                     stream.cuda_stream)
+            if g < 0:
+                raise RuntimeError(f"tam_stream_pass0 failed ({g})")
+
+        ms = _time_launches(launch, 1, args.steps, stream)
+        gbps = nbytes / (ms * 1e-3) / 1e9
+        rec = {"workload": "stream-pass0", "layout": ["lane 16 elements", "wave-contiguous 2x8"][layout],
+               "nontemporal": bool(nt), "wg": wg, "wgs_per_cu": per_cu, "rounds": rounds,
+               "cap_4_waves_per_simd": cap, "elements": units * 1024, "ms_per_launch": ms,
+               "bytes_per_launch": nbytes, "GBps": gbps, "frac_of_8TBps": gbps / HBM_PEAK_GBPS}
+        print(json.dumps(rec), flush=True)
+        if best is None or gbps > best["GBps"]:
+            best = rec
+    print(json.dumps({"workload": "stream-pass0", "best": best}), flush=True)
 
 
 # ---------------------------------------------------------------- main
@@ -381,11 +461,10 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="c3", choices=sorted(WORKLOADS) + ["copy", "stream"])
+    ap.add_argument("--workload", default="c3", choices=sorted(WORKLOADS) + ["copy", "stream", "stream-pass0"])
     ap.add_argument("--grad-sets", type=int, default=2)
     ap.add_argument("--pass-steps", type=int, default=5,
                     help="extra steps after the timed region, issued pass by pass, that time pass 0")
-    ap.add_argument("--stream-rounds", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-baseline-only", action="store_true",
                     help="time only the CPU baseline of the workload (no GPU work)")
@@ -403,6 +482,9 @@ def main():
         return
     if args.workload == "stream":
         stream_reference(args)
+        return
+    if args.workload == "stream-pass0":
+        stream_pass0_reference(args)
         return
     shapes_fn, dtype, kw, log_sigma, desc = WORKLOADS[args.workload]
     shapes = shapes_fn()

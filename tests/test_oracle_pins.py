@@ -96,6 +96,26 @@ def test_bf16_rounding_matches_torch():
     assert np.array_equal(got, want)
 
 
+@pytest.mark.parametrize("dtype,delta", [(torch.bfloat16, 2.0**-10), (torch.float16, 2.0**-13)])
+def test_small_weight_decay_leaves_16bit_parameters_unchanged(dtype, delta):
+    """The kernels skip decoupled weight decay on a 16-bit parameter when
+    1 - delta <= c <= 1 (c = f32(1 - lr*wd)): R_p(fl(x*c)) == x for every
+    finite 16-bit x and every such c.  Checked on all 65536 patterns at the
+    bound, just inside it, at C3's lr*wd and at 1 - 2^-24; and the bound is
+    not vacuous: at 4*delta some values change."""
+    xs = torch.arange(0, 1 << 16, dtype=torch.int32).to(torch.int16).view(dtype)
+    xs = xs[torch.isfinite(xs)]
+    x32 = xs.to(torch.float32)
+    for c in (1.0 - delta, 1.0 - delta + 2.0**-24, 1.0 - delta / 3, float(np.float32(1.0 - 3e-4 * 0.1)),
+              1.0 - 2.0**-24, 1.0):
+        c32 = torch.tensor(c, dtype=torch.float32)
+        assert float(c32) >= 1.0 - delta
+        y = (x32 * c32).to(dtype)  # fp32 product (correctly rounded), then round to nearest even
+        assert torch.equal(y.view(torch.int16), xs.view(torch.int16)), c
+    y = (x32 * torch.tensor(1.0 - 4 * delta, dtype=torch.float32)).to(dtype)
+    assert not torch.equal(y.view(torch.int16), xs.view(torch.int16))
+
+
 # ---------------------------------------------------------------- log / exp
 decimal.getcontext().prec = 50
 

@@ -837,7 +837,8 @@ __device__ __forceinline__ void tam_vpath_b(const TamTensor& d, const TamWave& W
 // q >= 2^-126 and eps >= 0, so r <= min(1/eps, 2^63) (1 + 2^-21): the last two
 // terms are below the per-tensor constant k_abs (tam_abs_term), and
 //   E = 2^-19 |u~| + 2^-22 |s| + k_abs
-// bounds the distance.  R_p and fl are monotone (overflow included), so
+// bounds the distance; the kernels use the larger 2^-19 max|u~| + 2^-22 |s|
+// + k_abs, max over the lane's elements.  R_p and fl are monotone (overflow included), so
 // R_p(fl(p + upd)) is accepted when R_p(fl(s - E)) == R_p(fl(s + E)) and s is
 // not a NaN (an infinite s makes fl(s - E) a NaN, which fails the equality).
 // Elements go in pairs: one packed conversion rounds both fl(s - E), another
@@ -907,23 +908,27 @@ __device__ __forceinline__ void tam_update(const TamTensor& d, float* p, const f
   bool okp[TAM_EPL / 2];
   bool all_ok = true;
   float umax = 0.0f, nacc = 0.0f;
+  float st[TAM_EPL];
+#pragma unroll
+  for (int i = 0; i < TAM_EPL; ++i) {
+    const float q = v[i] * d.inv_bc2_f32;
+    const float s = __builtin_amdgcn_sqrtf(q);
+    const float r = __builtin_amdgcn_rcpf(s + d.eps);
+    const float u = (c_lr * m[i]) * r;
+    st[i] = pw[i] + u;
+    umax = __builtin_fmaxf(umax, __builtin_fabsf(u));  // a NaN u makes st NaN
+  }
+  // 2^-19 |u| + k_abs of every element of the lane is at most this one term
+  // (E only grows: the test can only reject more)
+  const float eu = __builtin_fmaf(umax, 0x1p-19f, k_abs);
 #pragma unroll
   for (int k = 0; k < TAM_EPL / 2; ++k) {
-    float st[2], E[2];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int i = 2 * k + j;
-      const float q = v[i] * d.inv_bc2_f32;
-      const float s = __builtin_amdgcn_sqrtf(q);
-      const float r = __builtin_amdgcn_rcpf(s + d.eps);
-      const float u = (c_lr * m[i]) * r;
-      st[j] = pw[i] + u;
-      E[j] = __builtin_fmaf(__builtin_fabsf(u), 0x1p-19f, __builtin_fmaf(__builtin_fabsf(st[j]), 0x1p-22f, k_abs));
-      umax = __builtin_fmaxf(umax, __builtin_fabsf(u));  // a NaN u makes st NaN
-    }
-    nacc = __builtin_fmaf(st[0], st[1], nacc);
-    const uint32_t lo = tam_pack16<DT>(st[0] - E[0], st[1] - E[1]);
-    const uint32_t hi = tam_pack16<DT>(st[0] + E[0], st[1] + E[1]);
+    const float s0 = st[2 * k], s1 = st[2 * k + 1];
+    const float e0 = __builtin_fmaf(__builtin_fabsf(s0), 0x1p-22f, eu);
+    const float e1 = __builtin_fmaf(__builtin_fabsf(s1), 0x1p-22f, eu);
+    nacc = __builtin_fmaf(s0, s1, nacc);
+    const uint32_t lo = tam_pack16<DT>(s0 - e0, s1 - e1);
+    const uint32_t hi = tam_pack16<DT>(s0 + e0, s1 + e1);
     pw2[k] = lo;
     okp[k] = lo == hi;
     all_ok &= okp[k];
@@ -1131,7 +1136,13 @@ __device__ __forceinline__ void tam_k1_quarter(const TamTensor& d, uint32_t wq, 
 // elements of a lane instead of 8, and loads and stores move 32 bytes per lane
 // and array.  The unit's two quarter partials go to their quarters' slots.
 #define TAM_EPU 16   // elements per lane in a unit
-#define TAM_K1U_WG 128  // threads of a main pass-0 workgroup: two waves, one unit each per tile
+#define TAM_K1U_WG 128  // threads of a (virtual) main pass-0 workgroup: two waves, one unit each per tile
+// Virtual workgroups per hardware workgroup of the main pass-0 kernels: each
+// pair of waves strides over the tiles as a workgroup of its own
+#ifndef TAM_K1_VWG
+#define TAM_K1_VWG 1
+#endif
+#define TAM_K1_BLOCK (TAM_K1U_WG * TAM_K1_VWG)
 
 // Minimum / maximum / or over the 8 lanes of a half-row (one block).
 __device__ __forceinline__ uint32_t tam_half_umin(uint32_t v) {
@@ -1223,11 +1234,14 @@ __device__ __forceinline__ TamVExt tam_vunit_a(const TamTensor& d, uint32_t lane
   }
   TamVExt x;
   if (d.beta2 >= 0.0f && d.one_minus_beta2 >= 0.0f) {  // uniform: v >= +0 or NaN (see tam_vpath_a)
+    // v is never -0 here (vo >= +0 from the levels, g*g >= +0, and an fma
+    // whose addends are +0 and -0 gives +0), so its bit pattern orders as
+    // the value; a NaN of either sign lies above +inf
     uint32_t xmn = 0xffffffffu, xmx = 0u;
 #pragma unroll
     for (int i = 0; i < TAM_EPU; ++i) {
       v[i] = __builtin_fmaf(d.one_minus_beta2, g[i] * g[i], vo[i] * d.beta2);
-      const uint32_t k = tam_f2u(v[i]) & 0x7fffffffu;
+      const uint32_t k = tam_f2u(v[i]);
       xmn = __builtin_elementwise_min(xmn, k);
       xmx = __builtin_elementwise_max(xmx, k);
     }
@@ -1526,15 +1540,17 @@ __device__ __forceinline__ void tam_k1_full_body(const TamTensor* __restrict__ T
                                                  double2* __restrict__ partials) {
   if (tam_step_skipped(T)) return;
   // rows of 64 levels, 256-byte aligned (tam_vunit_a forms addresses by or)
-  __shared__ __attribute__((aligned(256))) float lut[TAM_K1U_WG / 64][8 * 64];
+  __shared__ __attribute__((aligned(256))) float lut[TAM_K1_BLOCK / 64][8 * 64];
   __shared__ TamLdsTabs tabs;
   tam_lds_tabs_fill(&tabs);
-  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63u;
-  float* lutw = lut[wave];
+  const uint32_t hw_wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63u;
+  const uint32_t wave = hw_wave & 1u;  // within the virtual workgroup
+  const uint32_t stride = gridDim.x * TAM_K1_VWG;
+  float* lutw = lut[hw_wave];
   // tensor by tensor: the descriptor is read once per tensor, then the wave
   // takes its units of the tensor in grid strides
-  uint32_t tile = blockIdx.x;
-  int ti = tam_find_tensor(T, nT, tile);
+  uint32_t tile = blockIdx.x * TAM_K1_VWG + (hw_wave >> 1);
+  int ti = tam_find_tensor(T, nT, tile < total_tiles ? tile : total_tiles - 1u);
   while (tile < total_tiles) {
     ti = tam_advance_tensor(T, nT, ti, tile);
     const TamTensor& d = T[ti];
@@ -1544,19 +1560,19 @@ __device__ __forceinline__ void tam_k1_full_body(const TamTensor* __restrict__ T
       // rest are tam_k1_tail's, and u grows with the tile
       const bool aligned = (((uintptr_t)d.param | (uintptr_t)d.grad) & 15u) == 0;
       const uint64_t nfull = aligned ? d.n / (8u * TAM_BLOCK_SIZE) : 0u;
-      for (; tile < end; tile += gridDim.x) {
+      for (; tile < end; tile += stride) {
         const uint32_t u = (tile - d.tile0) * 2u + wave;  // unit within the tensor
         if (u >= nfull) break;
         double* part = (double*)(partials + (uint64_t)tile * 4u + 2u * wave);
         tam_k1_unit<DT>(d, u, lane, lutw, &tabs, seed_lo, seed_hi, part);
       }
     }
-    while (tile < end) tile += gridDim.x;  // this workgroup's first tile past the tensor
+    while (tile < end) tile += stride;  // this workgroup's first tile past the tensor
   }
 }
 
 #define TAM_K1_FULL_KERNEL(NAME, DT, WAVES)                                                                     \
-  __global__ __launch_bounds__(TAM_K1U_WG) __attribute__((amdgpu_waves_per_eu(WAVES, WAVES))) void NAME(      \
+  __global__ __launch_bounds__(TAM_K1_BLOCK) __attribute__((amdgpu_waves_per_eu(WAVES, WAVES))) void NAME(    \
       const TamTensor* __restrict__ T, int nT, uint32_t total_tiles, uint32_t seed_lo, uint32_t seed_hi,      \
       double2* __restrict__ partials) {                                                                       \
     tam_k1_full_body<DT>(T, nT, total_tiles, seed_lo, seed_hi, partials);                                     \
@@ -2722,6 +2738,25 @@ static uint64_t tam_align_up(uint64_t x, uint64_t a) { return (x + a - 1) / a * 
 // bytes u8[ceil(n/8)] at 7nb.
 static uint64_t tam_ef_stage_bytes(uint64_t n, uint64_t nb) { return 7u * nb + (n + 7) / 8; }
 
+// Whether decoupled weight decay leaves every 16-bit parameter unchanged:
+// R_p(fl(x * c)) == x for every bf16 x when 1 - 2^-10 <= c <= 1 (fp16: 1 -
+// 2^-13), c = f32(1 - lr * wd) (optimizer.py:106-107 on a 16-bit tensor).
+// For x > 0 (x < 0 is symmetric; 0 and inf map to themselves, a NaN stays a
+// NaN that the update then propagates): fl is monotone and x is an fp32
+// value, so x (1 - d)(1 - 2^-24) - 2^-150 <= fl(x c) <= x with d = 1 - c.
+// The predecessor of a normal x is at least x 2^-8 below it for bf16 (2^-11
+// for fp16), and R_p returns x for anything above the midpoint x (1 - 2^-9)
+// (fp16: x (1 - 2^-12)), which (1 - 2^-10)(1 - 2^-24) x - 2^-150 exceeds.
+// Subnormal x = k 2^-133 (bf16, k < 128; fp16 k 2^-24, k < 1024) moves by less
+// than k d x-units + 2^-150 < half their spacing.  tests/test_oracle_pins.py
+// checks the claim on every 16-bit pattern at the bounds.  The kernels then
+// skip the product and its rounding.
+static bool tam_wd_keeps_16bit(uint32_t dtype, float c_wd) {
+  if (dtype == TAM_DTYPE_BF16) return c_wd <= 1.0f && c_wd >= 1.0f - 0x1p-10f;
+  if (dtype == TAM_DTYPE_F16) return c_wd <= 1.0f && c_wd >= 1.0f - 0x1p-13f;
+  return false;
+}
+
 // Workgroups of a kernel that fit on the device at once (CUs times the
 // occupancy its registers and LDS allow), cached per device and kernel.  The
 // tile loops launch TAM_GRID_ROUNDS times that many workgroups, pass 2
@@ -2823,6 +2858,7 @@ int tam_prepare(TamTensor* tensors, int n_tensors, TamStepInfo* info) {
     } else if (t.flags & (TAM_FLAG_EF | TAM_FLAG_HAS_EF)) {
       return tam_fail(TAM_E_INVALID, "%stensor %ld: error feedback needs CoState", "", i);
     }
+    if ((t.flags & TAM_FLAG_WD) && tam_wd_keeps_16bit(t.dtype, t.c_wd)) t.flags &= ~TAM_FLAG_WD;
     t.nb = (uint32_t)nb;
     t.ntiles = (uint32_t)nt;
     t.tile0 = (uint32_t)tiles;
@@ -2891,10 +2927,12 @@ static int tam_launch_pass(int pass, const TamTensor* d_tensors, const TamStepIn
   TamSel* sel = (TamSel*)(ws + info->off_sel);
   uint32_t* hist = (uint32_t*)(ws + info->off_hist);
   float* alpha_old = (float*)(ws + info->off_ef_alpha);
-  auto grid_of = [&](int which, const void* kernel, int block = TAM_WG) {
+  // vwg: virtual workgroups (each striding over the tiles on its own) per workgroup
+  auto grid_of = [&](int which, const void* kernel, int block = TAM_WG, uint32_t vwg = 1u) {
     const uint32_t rounds = which == TAM_KS_K2 ? TAM_K2_GRID_ROUNDS : TAM_GRID_ROUNDS;
     const uint32_t g = tam_resident_grid(which, kernel, block) * rounds;
-    return info->total_tiles < g ? info->total_tiles : g;
+    const uint32_t need = (info->total_tiles + vwg - 1u) / vwg;
+    return need < g ? need : g;
   };
   switch (pass) {
     case 0:
@@ -2903,16 +2941,19 @@ static int tam_launch_pass(int pass, const TamTensor* d_tensors, const TamStepIn
         TAM_HIP_CHECK(hipGetLastError());
       }
       if (info->dtype_mask & (1u << TAM_DTYPE_BF16))
-        hipLaunchKernelGGL(tam_k1_main_bf16, dim3(grid_of(TAM_KS_K1_BF16, (const void*)tam_k1_main_bf16, TAM_K1U_WG)),
-                           dim3(TAM_K1U_WG), 0, s, d_tensors, info->n_tensors, info->total_tiles, (uint32_t)seed,
+        hipLaunchKernelGGL(tam_k1_main_bf16,
+                           dim3(grid_of(TAM_KS_K1_BF16, (const void*)tam_k1_main_bf16, TAM_K1_BLOCK, TAM_K1_VWG)),
+                           dim3(TAM_K1_BLOCK), 0, s, d_tensors, info->n_tensors, info->total_tiles, (uint32_t)seed,
                            (uint32_t)(seed >> 32), partials);
       if (info->dtype_mask & (1u << TAM_DTYPE_F16))
-        hipLaunchKernelGGL(tam_k1_main_f16, dim3(grid_of(TAM_KS_K1_F16, (const void*)tam_k1_main_f16, TAM_K1U_WG)),
-                           dim3(TAM_K1U_WG), 0, s, d_tensors, info->n_tensors, info->total_tiles, (uint32_t)seed,
+        hipLaunchKernelGGL(tam_k1_main_f16,
+                           dim3(grid_of(TAM_KS_K1_F16, (const void*)tam_k1_main_f16, TAM_K1_BLOCK, TAM_K1_VWG)),
+                           dim3(TAM_K1_BLOCK), 0, s, d_tensors, info->n_tensors, info->total_tiles, (uint32_t)seed,
                            (uint32_t)(seed >> 32), partials);
       if (info->dtype_mask & (1u << TAM_DTYPE_F32))
-        hipLaunchKernelGGL(tam_k1_main_f32, dim3(grid_of(TAM_KS_K1_F32, (const void*)tam_k1_main_f32, TAM_K1U_WG)),
-                           dim3(TAM_K1U_WG), 0, s, d_tensors, info->n_tensors, info->total_tiles, (uint32_t)seed,
+        hipLaunchKernelGGL(tam_k1_main_f32,
+                           dim3(grid_of(TAM_KS_K1_F32, (const void*)tam_k1_main_f32, TAM_K1_BLOCK, TAM_K1_VWG)),
+                           dim3(TAM_K1_BLOCK), 0, s, d_tensors, info->n_tensors, info->total_tiles, (uint32_t)seed,
                            (uint32_t)(seed >> 32), partials);
       if (info->n_ef)
         hipLaunchKernelGGL(tam_k1_ef, dim3(grid_of(TAM_KS_K1_EF, (const void*)tam_k1_ef)), dim3(TAM_WG), 0, s,
