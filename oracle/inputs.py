@@ -15,7 +15,7 @@ GEN_SEED = 0x6E6F726D616C2121  # separate key from the optimizer's rounding stre
 
 def normal(n: int, stream: int, draw: int, seed: int = GEN_SEED) -> np.ndarray:
     """n approximately N(0,1) float64 values of (stream, draw)."""
-    u = O.philox_uniforms(stream & 0xFFFFFFFF, draw & 0xFFFFFFFF, seed, 12 * n).astype(np.float64)
+    u = O.input_uniforms(stream & 0xFFFFFFFF, draw & 0xFFFFFFFF, seed, 12 * n).astype(np.float64)
     return u.reshape(n, 12).sum(axis=1) - 6.0
 
 

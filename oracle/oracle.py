@@ -54,6 +54,7 @@ def lib():
         L = ctypes.CDLL(LIB_PATH)
         L.or_step_tensor.argtypes = [ctypes.POINTER(OrTensor), ctypes.c_uint64]
         L.or_philox_uniforms.argtypes = [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_uint64, _VP]
+        L.or_input_uniforms.argtypes = [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_uint64, _VP]
         L.or_philox4x32_10.argtypes = [_VP, ctypes.c_uint32, ctypes.c_uint32, _VP]
         L.or_logf.argtypes = [ctypes.c_float]
         L.or_logf.restype = ctypes.c_float
@@ -99,8 +100,16 @@ def f32(x: float) -> float:
 
 
 def philox_uniforms(tensor_id: int, step: int, seed: int, count: int) -> np.ndarray:
+    """The stochastic-rounding uniforms of (tensor_id, step) for elements 0 .. count-1."""
     out = np.empty(count, dtype=np.float32)
     lib().or_philox_uniforms(tensor_id, step, seed, count, ptr(out))
+    return out
+
+
+def input_uniforms(stream: int, draw: int, seed: int, count: int) -> np.ndarray:
+    """Uniforms of the synthetic test inputs (another bit layout of the same generator)."""
+    out = np.empty(count, dtype=np.float32)
+    lib().or_input_uniforms(stream, draw, seed, count, ptr(out))
     return out
 
 

@@ -18,8 +18,10 @@
  * addcmul_).  Stochastic-rounding uniforms: Philox4x32-10 (its own
  * implementation here): elements in groups of 16, group t = e/16 taking the
  * 384 bits of the blocks with counters (3t + j, tensor_id, step, (3t+j)>>32),
- * j = 0..2, key seed, little endian; element 16t + k takes bits
- * [24k, 24k+24), u = that integer * 2^-24.  Compiled with -ffp-contract=off.
+ * j = 0..2, key seed, little endian; element 16t + k takes the 24-bit
+ * integer whose high 16 bits are bits [16k, 16k+16) (blocks 3t and 3t + 1)
+ * and whose low 8 bits are bits [256 + 8k, 256 + 8k + 8) (block 3t + 2),
+ * u = that integer * 2^-24.  Compiled with -ffp-contract=off.
  * Loops over independent blocks or elements run under OpenMP; each iteration
  * writes its own outputs and every reduction runs in its fixed order after
  * the loop, so results do not depend on the thread count.
@@ -55,12 +57,9 @@ void or_philox4x32_10(const uint32_t ctr[4], uint32_t k0, uint32_t k1, uint32_t 
   out[0] = c0; out[1] = c1; out[2] = c2; out[3] = c3;
 }
 
-/* The 16 uniforms of draw group t (elements 16t .. 16t+15): the 384 bits of
- * the Philox blocks with counters (3t + j, tid, step, (3t + j) >> 32), j =
- * 0, 1, 2, as a little-endian bit string; element 16t + k takes the 24-bit
- * integer at bits [24k, 24k + 24), times 2^-24. */
-static void or_group_uniforms(uint64_t t, uint32_t tid, uint32_t step, uint64_t seed, float* u16) {
-  uint8_t bytes[48];
+/* The 384 bits of draw group t: the Philox blocks with counters (3t + j,
+ * tid, step, (3t + j) >> 32), j = 0, 1, 2, as little-endian bytes. */
+static void or_group_bytes(uint64_t t, uint32_t tid, uint32_t step, uint64_t seed, uint8_t bytes[48]) {
   for (int j = 0; j < 3; ++j) {
     uint64_t c = 3 * t + (uint64_t)j;
     uint32_t ctr[4] = {(uint32_t)c, tid, step, (uint32_t)(c >> 32)};
@@ -69,9 +68,32 @@ static void or_group_uniforms(uint64_t t, uint32_t tid, uint32_t step, uint64_t 
     for (int i = 0; i < 4; ++i)
       for (int b = 0; b < 4; ++b) bytes[16 * j + 4 * i + b] = (uint8_t)(w[i] >> (8 * b));
   }
+}
+
+/* The 16 stochastic-rounding uniforms of draw group t (elements 16t ..
+ * 16t+15): element 16t + k takes the 24-bit integer with high 16 bits from
+ * bits [16k, 16k + 16) of the group (bytes 2k, 2k + 1) and low 8 bits from
+ * bits [256 + 8k, 256 + 8k + 8) (byte 32 + k), times 2^-24.  The high parts
+ * come from the first two blocks alone. */
+static void or_group_uniforms(uint64_t t, uint32_t tid, uint32_t step, uint64_t seed, float* u16) {
+  uint8_t bytes[48];
+  or_group_bytes(t, tid, step, seed, bytes);
   for (int k = 0; k < 16; ++k) {
-    uint32_t d = (uint32_t)bytes[3 * k] | ((uint32_t)bytes[3 * k + 1] << 8) | ((uint32_t)bytes[3 * k + 2] << 16);
+    uint32_t d = ((uint32_t)bytes[2 * k] << 8) | ((uint32_t)bytes[2 * k + 1] << 16) | (uint32_t)bytes[32 + k];
     u16[k] = (float)d * (1.0f / 16777216.0f);
+  }
+}
+
+/* Uniforms of the synthetic test inputs (oracle/inputs.py): the same group
+ * bits, element 16t + k taking the 24-bit integer at bits [24k, 24k + 24). */
+void or_input_uniforms(uint32_t tid, uint32_t step, uint64_t seed, uint64_t count, float* out) {
+  uint8_t bytes[48];
+  for (uint64_t t = 0; t * 16 < count; ++t) {
+    or_group_bytes(t, tid, step, seed, bytes);
+    for (int k = 0; k < 16 && t * 16 + (uint64_t)k < count; ++k) {
+      uint32_t d = (uint32_t)bytes[3 * k] | ((uint32_t)bytes[3 * k + 1] << 8) | ((uint32_t)bytes[3 * k + 2] << 16);
+      out[t * 16 + (uint64_t)k] = (float)d * (1.0f / 16777216.0f);
+    }
   }
 }
 

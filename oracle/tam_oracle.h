@@ -42,6 +42,8 @@ typedef struct OrTensor {
 /* One parameter's TurboAdam step on host arrays (the caller advances the step
  * counter and supplies the fp32 scalars and flags). */
 void or_step_tensor(OrTensor* t, uint64_t seed);
+/* The stochastic-rounding uniforms of (tid, step) for elements 0 .. count-1. */
+void or_philox_uniforms(uint32_t tid, uint32_t step, uint64_t seed, uint64_t count, float* out);
 uint16_t or_f32_to_bf16(float x);
 float or_bf16_to_f32(uint16_t b);
 

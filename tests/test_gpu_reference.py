@@ -64,6 +64,16 @@ def _rel(a, b):
     return d / s if s > 0 else d
 
 
+def _ulp16_flips(a, b):
+    """Elements of two 16-bit parameter arrays (bit patterns) that differ, and
+    whether each differs by one unit in the last place only (neighbouring
+    patterns of one sign)."""
+    a16, b16 = a.astype(np.int32), b.astype(np.int32)
+    diff = a16 != b16
+    one_ulp = (np.abs(a16 - b16) == 1) & ((a16 & 0x8000) == (b16 & 0x8000))
+    return int(diff.sum()), bool(one_ulp[diff].all())
+
+
 @pytest.mark.parametrize("name", SHORT)
 def test_gpu_matches_reference_fixtures(name):
     log(f"GPU vs reference fixture {name}")
@@ -76,10 +86,24 @@ def test_gpu_matches_reference_fixtures(name):
     # which the following steps' m carry: the CPU restatement in exact mode
     # (which the GPU equals bit for bit) ends 4.7e-5 from the reference on
     # ef_f32 (tests/test_golden.py::test_error_feedback_end_to_end_ties).
+    # End to end, a 16-bit parameter can also land one unit in the last place
+    # off: CoState's first-step sign bits follow alpha's last bit (see above),
+    # so m differs by rounding noise from the first step on, and now and then
+    # an update sits on a 16-bit rounding boundary.  One such element of a
+    # small tensor exceeds 1e-6 norm-wise (one fp16 ulp of 8192 elements is
+    # 4e-6); each step from a common state stays within 1e-6
+    # (tests/test_golden.py::test_exact_and_faithful_differ_only_by_ties).
     tol = 1e-4 if case["kw"].get("error_feedback") else 1e-6
     for i, p in enumerate(params):
-        pr = _rel(_as_f32(from_torch(p.data), dt), _as_f32(z[f"param_{i}"], dt))
-        assert pr <= tol, f"{name} tensor {i}: param rel {pr:.3g}"
+        got, want = from_torch(p.data), z[f"param_{i}"]
+        pr = _rel(_as_f32(got, dt), _as_f32(want, dt))
+        if pr > tol and dt != 0:
+            nd, one_ulp = _ulp16_flips(got, want)
+            assert one_ulp and nd <= max(2, 1e-3 * got.size), \
+                f"{name} tensor {i}: param rel {pr:.3g}, {nd} elements differ (one ulp each: {one_ulp})"
+            log(f"{name} tensor {i}: {nd} element(s) one 16-bit ulp off the reference (rel {pr:.3g})")
+        else:
+            assert pr <= tol, f"{name} tensor {i}: param rel {pr:.3g}"
         st = gpu_state(opt, p)
         for k in ("indices",):
             if f"{k}_{i}" in z.files:

@@ -44,12 +44,16 @@ def test_philox_known_answers(ctr, key, want):
 
 def test_philox_uniform_layout():
     # group t = e // 16: the three blocks with counters (3t + j, tid, step,
-    # (3t + j) >> 32) as one little-endian 384-bit integer; element e takes
-    # bits [24 (e % 16), 24 (e % 16) + 24) -- here as Python big-integer
-    # arithmetic over the KAT-pinned generator, including a counter past 2^32
+    # (3t + j) >> 32) as one little-endian 384-bit integer; element k = e % 16
+    # takes the 24-bit integer with high 16 bits at [16k, 16k + 16) (the first
+    # two blocks) and low 8 bits at [256 + 8k, 256 + 8k + 8) (the third) --
+    # here as Python big-integer arithmetic over the KAT-pinned generator,
+    # including a counter past 2^32.  The synthetic inputs use the same bits
+    # with element k at [24k, 24k + 24).
     seed = 0x0123456789ABCDEF
     n = 16 * 5 + 7
     u = O.philox_uniforms(5, 9, seed, n)
+    ui = O.input_uniforms(5, 9, seed, n)
 
     def block(c):
         ctr = np.array([c & 0xFFFFFFFF, 5, 9, c >> 32], np.uint32)
@@ -60,7 +64,9 @@ def test_philox_uniform_layout():
     for e in range(n):
         t, k = divmod(e, 16)
         bits = sum(block(3 * t + j) << (128 * j) for j in range(3))
-        assert u[e] == np.float32(((bits >> (24 * k)) & 0xFFFFFF) * 2.0**-24), e
+        hi, lo = (bits >> (16 * k)) & 0xFFFF, (bits >> (256 + 8 * k)) & 0xFF
+        assert u[e] == np.float32(((hi << 8) | lo) * 2.0**-24), e
+        assert ui[e] == np.float32(((bits >> (24 * k)) & 0xFFFFFF) * 2.0**-24), e
     assert (u >= 0).all() and (u < 1).all()
     # a group whose counters pass 2^32 (group t = 2^32 // 3 + 1): the slice
     # draws of a block0 offset reach it through or_fused_v_update

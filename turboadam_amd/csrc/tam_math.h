@@ -93,9 +93,12 @@ TAM_HD TamU4 tam_philox4x32_10(TamU4 c, uint32_t k0, uint32_t k1) {
 // consecutive ones, e = 16t + k; group t takes the 384 bits of three
 // Philox4x32-10 blocks with counters (3t + j, tid, step, (3t + j) >> 32),
 // j = 0, 1, 2, key (seed_lo, seed_hi), read as the little-endian words
-// w0..w11, and element k's draw is the 24-bit integer at bits [24k, 24k+24):
-// uniform = that integer * 2^-24 (exact).  Every output bit is used (four
-// draws per three words).
+// w0..w11.  Element k's draw is the 24-bit integer whose high 16 bits are
+// bits [16k, 16k+16) (half k % 2 of word k / 2: the first two blocks) and
+// whose low 8 bits are bits [256 + 8k, 256 + 8k + 8) (byte k of the third
+// block): uniform = that integer * 2^-24 (exact).  Every output bit is used.
+// The high parts of elements 8h .. 8h + 7 are block 3t + h alone, which is
+// all that the certified fast path of the re-quantisation reads.
 TAM_HD TamU4 tam_philox_block(uint64_t ctr, uint32_t tid, uint32_t step, uint32_t seed_lo, uint32_t seed_hi) {
   TamU4 c;
   c.x = (uint32_t)ctr;
@@ -105,33 +108,26 @@ TAM_HD TamU4 tam_philox_block(uint64_t ctr, uint32_t tid, uint32_t step, uint32_
   return tam_philox4x32_10(c, seed_lo, seed_hi);
 }
 
-// The eight 24-bit draws of a 192-bit window (six consecutive words w0..w5
-// of a group: words 0..5 for elements 0..7 of the group, words 6..11 for
-// elements 8..15): draw k takes bits [24k, 24k+24) of the window, which for
-// k = 1, 2, 5, 6 run over a word boundary (v_alignbit of the word pair).
-TAM_HD void tam_split24(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3, uint32_t w4, uint32_t w5,
-                        uint32_t* r) {
-  r[0] = w0 & 0xffffffu;
-  r[1] = (uint32_t)((((uint64_t)w1 << 32) | w0) >> 24) & 0xffffffu;
-  r[2] = (uint32_t)((((uint64_t)w2 << 32) | w1) >> 16) & 0xffffffu;
-  r[3] = w2 >> 8;
-  r[4] = w3 & 0xffffffu;
-  r[5] = (uint32_t)((((uint64_t)w4 << 32) | w3) >> 24) & 0xffffffu;
-  r[6] = (uint32_t)((((uint64_t)w5 << 32) | w4) >> 16) & 0xffffffu;
-  r[7] = w5 >> 8;
+// The 24-bit draw of element 2i + o (o = 0 or 1) of a half-group: high 16
+// bits from half o of word a (word i of the half's first block), low 8 bits
+// the low byte of lo8.
+TAM_HD uint32_t tam_draw24(uint32_t a, uint32_t o, uint32_t lo8) {
+  return ((o ? (a >> 16) : (a & 0xffffu)) << 8) | (lo8 & 0xffu);
 }
 
 // The draws of the 8 consecutive elements e0 .. e0+7 (e0 a multiple of 8) of
-// group t = e0/16: half h = (e0/8) % 2 of the group needs blocks 3t + h and
-// 3t + h + 1, a = block 3t + h, b = block 3t + h + 1:
-// h = 0: w0..w5 = a0..a3, b0, b1;  h = 1: w6..w11 = a2, a3, b0..b3.
+// group t = e0/16, half h = (e0/8) % 2: high parts from block 3t + h, low
+// bytes 8h .. 8h+7 of block 3t + 2 (its words 2h and 2h + 1).
 TAM_HD void tam_draws8(uint64_t e0, uint32_t tid, uint32_t step, uint32_t seed_lo, uint32_t seed_hi,
                        uint32_t* r) {
-  const bool h = (e0 >> 3) & 1u;
-  const uint64_t c0 = 3u * (e0 >> 4) + (h ? 1u : 0u);
-  const TamU4 a = tam_philox_block(c0, tid, step, seed_lo, seed_hi);
-  const TamU4 b = tam_philox_block(c0 + 1u, tid, step, seed_lo, seed_hi);
-  tam_split24(h ? a.z : a.x, h ? a.w : a.y, h ? b.x : a.z, h ? b.y : a.w, h ? b.z : b.x, h ? b.w : b.y, r);
+  const uint32_t h = (uint32_t)(e0 >> 3) & 1u;
+  const uint64_t c0 = 3u * (e0 >> 4);
+  const TamU4 a = tam_philox_block(c0 + h, tid, step, seed_lo, seed_hi);
+  const TamU4 c = tam_philox_block(c0 + 2u, tid, step, seed_lo, seed_hi);
+  const uint32_t aw[4] = {a.x, a.y, a.z, a.w};
+  const uint32_t c0w = h ? c.z : c.x, c1w = h ? c.w : c.y;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) r[j] = tam_draw24(aw[j >> 1], (uint32_t)j & 1u, (j < 4 ? c0w : c1w) >> (8 * (j & 3)));
 }
 
 // Uniform of a 24-bit draw.

@@ -1300,41 +1300,26 @@ __device__ __forceinline__ void tam_vunit_b(const TamTensor& d, uint32_t lane, u
   const float Bb = __builtin_fmaf(fnb * rsp, per_sp, flat) * (1.0f + 0x1p-16f);
   const bool blk_ok = (tam_u2f(kmn) >= 0x1p-126f) && (tam_u2f(kmx) < 0x1p100f) && !nan_seen && (sp <= 64.0f) &&
                       (Bb < 0.25f);
-  // the fast path subtracts u' = floor(r / 2) 2^-23 (u with its lowest bit
-  // dropped: u - u' <= 2^-24) from c~ + 1: 2^-22 more in the bound covers that
-  // and the rounding of the larger c~ + 1 (another 2^-24)
-  const float H = blk_ok ? 0.5f - (Bb + 0x1p-21f) : -1.0f;
+  // The fast path subtracts u' = hi 2^-16 + 2^-17 from c~ + 1, hi the high 16
+  // bits of the draw: |u - u'| <= 2^-17.  The quarter path's bound plus 2^-17
+  // covers that, plus 2^-21 the rounding of the larger c~ + 1.
+  const float H = blk_ok ? 0.5f - (Bb + (0x1p-17f + 0x1p-21f)) : -1.0f;
   const uint32_t byte_lsb = d.v_bits < 8u ? 0x01010101u : 0u;  // uniform
-  const uint32_t m23 = tam_vconst(0x7fffffu), one = tam_vconst(0x3f800000u), k7f = tam_vconst(0x7fu);
-  // the lane's 16 elements are one group of draws (three Philox blocks): the
-  // two halves of 8 one after the other, the first from blocks 3t and 3t + 1
-  // (words w0..w5), the second from w6, w7 and block 3t + 2
+  const uint32_t m16 = tam_vconst(0x7fff80u), one = tam_vconst(0x3f800040u);  // 1 + 2^-17
+  // the lane's 16 elements are one group of draws (tam_draws8): half h of 8
+  // takes its high parts from block 3t + h; the low bytes (block 3t + 2) are
+  // computed only where the exact path runs
   const uint64_t c0 = 3u * (e0 >> 4);
-  uint32_t carry0 = 0u, carry1 = 0u;
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const float* vh = v + TAM_EPL * h;
-    uint32_t w[6];
-    if (h == 0) {
-      const TamU4 a = tam_philox_block(c0, d.tensor_id, d.step, seed_lo, seed_hi);
-      const TamU4 bb = tam_philox_block(c0 + 1u, d.tensor_id, d.step, seed_lo, seed_hi);
-      w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w; w[4] = bb.x; w[5] = bb.y;
-      carry0 = bb.z;
-      carry1 = bb.w;
-    } else {
-      const TamU4 c = tam_philox_block(c0 + 2u, d.tensor_id, d.step, seed_lo, seed_hi);
-      w[0] = carry0; w[1] = carry1; w[2] = c.x; w[3] = c.y; w[4] = c.z; w[5] = c.w;
-    }
-    // draw i as the fp32 1 + u' (its top 23 bits under the exponent of 1.0):
-    // bits [24i + 1, 24i + 24) of the window w0..w5
+    const TamU4 a = tam_philox_block(c0 + (uint32_t)h, d.tensor_id, d.step, seed_lo, seed_hi);
+    const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+    // draw i as the fp32 1 + u': the high 16 bits of the draw (half i % 2 of
+    // word i / 2) at mantissa bits 7..22 over 1 + 2^-17
     const auto draw1 = [&](int i) -> float {
-      const uint32_t* ww = w + 3 * (i >> 2);
-      switch (i & 3) {
-        case 0: return tam_u2f(tam_and_or(ww[0] >> 1, m23, one));
-        case 1: return tam_u2f(tam_and_or(__builtin_amdgcn_alignbit(ww[1], ww[0], 25), m23, one));
-        case 2: return tam_u2f(tam_and_or(__builtin_amdgcn_alignbit(ww[2], ww[1], 17), m23, one));
-        default: return tam_u2f(__builtin_amdgcn_alignbit(k7f, ww[2], 9));  // 0x7f << 23 is 1.0's exponent
-      }
+      const uint32_t x = w[i >> 1];
+      return tam_u2f(tam_and_or((i & 1) ? x >> 9 : __builtin_amdgcn_alignbit(x, x, 25), m16, one));
     };
     uint32_t ow[2] = {0u, 0u};
     float tmax = 0.0f;
@@ -1356,8 +1341,11 @@ __device__ __forceinline__ void tam_vunit_b(const TamTensor& d, uint32_t lane, u
     if (!(tmax < H)) {  // false for a NaN bound (then H = -1)
       // exact path: the reference's own sequence with correctly rounded log
       // and division, and the whole 24-bit draws
+      const TamU4 c = tam_philox_block(c0 + 2u, d.tensor_id, d.step, seed_lo, seed_hi);
+      const uint32_t lo0 = h ? c.z : c.x, lo1 = h ? c.w : c.y;
       uint32_t rw[TAM_EPL];
-      tam_split24(w[0], w[1], w[2], w[3], w[4], w[5], rw);
+#pragma unroll
+      for (int i = 0; i < TAM_EPL; ++i) rw[i] = tam_draw24(w[i >> 1], (uint32_t)i & 1u, (i < 4 ? lo0 : lo1) >> (8 * (i & 3)));
 #pragma unroll
       for (int i = 0; i < TAM_EPL; ++i) {
         const float dd = __builtin_fmaf(__builtin_amdgcn_logf(vh[i] * rmin), K, 1.5f) - draw1(i);
