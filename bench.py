@@ -455,6 +455,36 @@ def stream_pass0_reference(args):
     print(json.dumps({"workload": "stream-pass0", "best": best}), flush=True)
 
 
+# ---------------------------------------------------------------- fallback rates
+def fallback_stats(args, opt, params, set_grads, desc):
+    """Step the workload with the counting build and print, for each requested
+    step, how many lanes and elements of pass 0's full units fell back from
+    the certified fast paths to the exact sequence (the re-quantisation of v,
+    per half unit, and the 16-bit update, per half unit), with their rates."""
+    import ctypes
+
+    from turboadam_amd import _lib
+
+    lib = _lib.load()
+    lib.tam_stats_read.restype = ctypes.c_int
+    lib.tam_stats_read.argtypes = [ctypes.POINTER(ctypes.c_uint64), ctypes.c_int]
+    out = (ctypes.c_uint64 * 4)()
+    want = sorted({int(x) for x in args.fallback_stats.split(",") if x.strip()})
+    units = sum(p.numel() // 1024 for p in params)  # full units (every tensor here is aligned)
+    _lib.check(lib.tam_stats_read(out, 1), "tam_stats_read")
+    for s in range(1, want[-1] + 1):
+        set_grads(s - 1)
+        opt.step()
+        _lib.check(lib.tam_stats_read(out, 1), "tam_stats_read")
+        if s in want:
+            vq_l, vq_e, up_l, up_p = (int(x) for x in out)
+            print(json.dumps({"workload": desc, "step": s, "full_units": units,
+                              "vq_lanes": vq_l, "vq_lane_frac": vq_l / (128 * units),
+                              "vq_elems": vq_e, "vq_elem_frac": vq_e / (1024 * units),
+                              "update_lanes": up_l, "update_lane_frac": up_l / (128 * units),
+                              "update_pairs": up_p, "update_pair_frac": up_p / (512 * units)}), flush=True)
+
+
 # ---------------------------------------------------------------- main
 def main():
     ap = argparse.ArgumentParser()
@@ -468,6 +498,10 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-baseline-only", action="store_true",
                     help="time only the CPU baseline of the workload (no GPU work)")
+    ap.add_argument("--fallback-stats", default="",
+                    help="comma-separated step numbers: instead of timing, step the workload with the counting "
+                         "build (python -m turboadam_amd.build --stats) and print how often pass 0's certified "
+                         "fast paths fell back to the exact sequence at those steps")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the optimizer step is single-device); "
@@ -476,6 +510,10 @@ def main():
 
     from turboadam_amd import TurboAdam, _lib
 
+    if args.fallback_stats:
+        from turboadam_amd.build import STATS_LIB_PATH
+
+        _lib.load(STATS_LIB_PATH)  # the counting build serves every call of this process
     _lib.load()
     if args.workload == "copy":
         copy_reference(args)
@@ -519,6 +557,9 @@ def main():
         for p, g in zip(params, grad_sets[k % args.grad_sets]):
             p.grad = g
 
+    if args.fallback_stats:
+        fallback_stats(args, opt, params, set_grads, desc)
+        return
     for s in range(args.warmup):
         set_grads(s)
         opt.step()

@@ -113,6 +113,25 @@ def test_gpu_matches_reference_fixtures(name):
     assert max(frac_bad, default=0.0) <= 1e-3, f"{name}: 1Q index mismatch fraction {max(frac_bad):.3g}"
 
 
+def test_gpu_gpt2_block_matches_reference_samples():
+    """The GPT-2-small block (12 fp32 tensors, 7.1M params, 3 steps): the
+    reference fixture keeps every 997th element of each final parameter
+    (golden_gpt2_block psample_*); the GPU's are within 1e-6 norm-wise.  The
+    fixture's per-step digests cover the CoState sign bits, which differ at
+    the ties described above; tests/test_golden.py checks them on the CPU."""
+    log("GPU vs reference fixture gpt2_block (sampled parameters)")
+    z = np.load(os.path.join(HERE, "golden", "golden_gpt2_block.npz"))
+    meta = json.loads(str(z["meta"]))
+    case, opt, params = _run("gpt2_block")
+    assert meta["steps"] == case["steps"]
+    for i, p in enumerate(params):
+        got = from_torch(p.data)[::997].astype(np.float64)
+        want = z[f"psample_{i}"].astype(np.float64)
+        assert got.shape == want.shape
+        pr = _rel(got, want)
+        assert pr <= 1e-6, f"gpt2_block tensor {i}: sampled param rel {pr:.3g}"
+
+
 def test_gpu_200_step_trajectory_matches_reference():
     log("GPU vs reference 200-step trajectory (traj_f32)")
     z = np.load(os.path.join(HERE, "golden", "golden_traj_f32.npz"))

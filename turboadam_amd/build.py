@@ -35,10 +35,10 @@ HIP_FLAGS = [
 ]
 
 
-def _hipcc(sources, out: str, verbose: bool) -> str:
+def _hipcc(sources, out: str, verbose: bool, extra=()) -> str:
     os.makedirs(BUILD_DIR, exist_ok=True)
     tmp = out + ".tmp"
-    cmd = [HIPCC, *HIP_FLAGS, "-o", tmp, *sources]
+    cmd = [HIPCC, *HIP_FLAGS, *extra, "-o", tmp, *sources]
     if verbose:
         print(" ".join(cmd))
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -54,5 +54,17 @@ def build_library(verbose: bool = False) -> str:
     return _hipcc(SOURCES, LIB_PATH, verbose)
 
 
+# A measurement build of the same sources that counts the fast paths' exact
+# fallbacks (TAM_STATS; read by bench.py --fallback-stats); never the library
+# the optimizer loads.
+STATS_LIB_PATH = os.path.join(BUILD_DIR, "libturboadam_amd_stats.so")
+
+
+def build_stats_library(verbose: bool = False) -> str:
+    return _hipcc(SOURCES, STATS_LIB_PATH, verbose, ["-DTAM_STATS=1"])
+
+
 if __name__ == "__main__":
     print(build_library(verbose="-v" in sys.argv))
+    if "--stats" in sys.argv:
+        print(build_stats_library(verbose="-v" in sys.argv))

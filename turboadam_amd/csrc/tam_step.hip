@@ -59,6 +59,25 @@ static int tam_fail(int code, const char* fmt, const char* a = "", long b = 0) {
   } while (0)
 
 // ---------------------------------------------------------------------------
+// fallback counters (measurement builds only: -DTAM_STATS=1)
+// ---------------------------------------------------------------------------
+// How often the certified fast paths of pass 0's full units hand elements to
+// the exact sequence: lanes (per half unit) whose re-quantisation runs the
+// exact path, elements it recomputes, lanes whose 16-bit update runs the exact
+// sequence, and pairs it recomputes.  Read with tam_stats_read, which exists
+// only in such builds; the product library has neither.
+#ifndef TAM_STATS
+#define TAM_STATS 0
+#endif
+enum { TAM_ST_VQ_LANES, TAM_ST_VQ_ELEMS, TAM_ST_UPD_LANES, TAM_ST_UPD_PAIRS, TAM_ST_COUNT };
+#if TAM_STATS
+__device__ unsigned long long tam_stats[TAM_ST_COUNT];
+#define TAM_STAT(i) atomicAdd(&tam_stats[i], 1ull)
+#else
+#define TAM_STAT(i) ((void)0)
+#endif
+
+// ---------------------------------------------------------------------------
 // global-memory access
 // ---------------------------------------------------------------------------
 // Device pointers read from a TamTensor are generic (flat) pointers; casting
@@ -937,9 +956,11 @@ __device__ __forceinline__ void tam_update(const TamTensor& d, float* p, const f
   const bool lane_ok = q_ok && umax < 0x1p126f && __builtin_fabsf(nacc) < __builtin_inff() && d.eps >= 0.0f &&
                        d.eps < 0x1p124f;
   if (!(lane_ok && all_ok)) {
+    TAM_STAT(TAM_ST_UPD_LANES);
 #pragma unroll
     for (int k = 0; k < TAM_EPL / 2; ++k) {
       if (!(lane_ok && okp[k])) {
+        TAM_STAT(TAM_ST_UPD_PAIRS);
         uint32_t w = 0u;
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
@@ -961,6 +982,21 @@ __device__ __forceinline__ int tam_find_tensor(const TamTensor* __restrict__ T, 
     if (T[mid].tile0 <= tile) lo = mid; else hi = mid - 1;
   }
   return lo;
+}
+
+// Position of workgroup b among the G workgroups of a tile loop.  Workgroups
+// are dispatched to the 8 XCDs in turn (b % 8); with TAM_XCD_TILES the
+// workgroups of one XCD take consecutive positions, so the tiles one round of
+// the loop gives an XCD are consecutive and the small per-block arrays'
+// 128-byte lines are written whole within one L2 (a line written in parts
+// from two XCDs reaches memory as two partial writes, each a
+// read-modify-write).  A permutation of 0 .. G-1 when G is a multiple of 8.
+#ifndef TAM_XCD_TILES
+#define TAM_XCD_TILES 1
+#endif
+__device__ __forceinline__ uint32_t tam_tile_slot(uint32_t b, uint32_t G) {
+  if (!TAM_XCD_TILES || (G & 7u)) return b;
+  return (b & 7u) * (G >> 3) + (b >> 3);
 }
 
 // The tensor holding `tile`, given that tensor ti or a later one holds it
@@ -1339,6 +1375,7 @@ __device__ __forceinline__ void tam_vunit_b(const TamTensor& d, uint32_t lane, u
     ow[0] -= (ow[0] >> d.v_bits) & byte_lsb;
     ow[1] -= (ow[1] >> d.v_bits) & byte_lsb;
     if (!(tmax < H)) {  // false for a NaN bound (then H = -1)
+      TAM_STAT(TAM_ST_VQ_LANES);
       // exact path: the reference's own sequence with correctly rounded log
       // and division, and the whole 24-bit draws
       const TamU4 c = tam_philox_block(c0 + 2u, d.tensor_id, d.step, seed_lo, seed_hi);
@@ -1350,6 +1387,7 @@ __device__ __forceinline__ void tam_vunit_b(const TamTensor& d, uint32_t lane, u
       for (int i = 0; i < TAM_EPL; ++i) {
         const float dd = __builtin_fmaf(__builtin_amdgcn_logf(vh[i] * rmin), K, 1.5f) - draw1(i);
         if (!(__builtin_fabsf(dd - __builtin_rintf(dd)) < H)) {
+          TAM_STAT(TAM_ST_VQ_ELEMS);
           const float vc = vh[i] < 1e-38f ? 1e-38f : vh[i];  // quantize.py:275
           const float l = tam_logf_lds(vc, tabs);
           const float c = ((l - lmn) / sp) * fnb;  // quantize.py:284-285
@@ -1537,7 +1575,7 @@ __device__ __forceinline__ void tam_k1_full_body(const TamTensor* __restrict__ T
   float* lutw = lut[hw_wave];
   // tensor by tensor: the descriptor is read once per tensor, then the wave
   // takes its units of the tensor in grid strides
-  uint32_t tile = blockIdx.x * TAM_K1_VWG + (hw_wave >> 1);
+  uint32_t tile = tam_tile_slot(blockIdx.x, gridDim.x) * TAM_K1_VWG + (hw_wave >> 1);
   int ti = tam_find_tensor(T, nT, tile < total_tiles ? tile : total_tiles - 1u);
   while (tile < total_tiles) {
     ti = tam_advance_tensor(T, nT, ti, tile);
@@ -1985,8 +2023,8 @@ tam_k2_encode(const TamTensor* __restrict__ T, int nT, uint32_t total_tiles, con
     }
     return false;
   };
-  uint32_t tile = blockIdx.x;
-  int ti = tam_find_tensor(T, nT, blockIdx.x);
+  uint32_t tile = tam_tile_slot(blockIdx.x, gridDim.x);
+  int ti = tam_find_tensor(T, nT, tile < total_tiles ? tile : total_tiles - 1u);
   bool have = next(tile, ti);
   TamK2U pre = {};
   bool pre_ok = have && tam_k2u_prefetchable(desc(ti), (tile - desc(ti).tile0) * 2u + wave);
@@ -3280,3 +3318,21 @@ int tam_v_quantize(const float* v, uint64_t n_padded, uint32_t v_bits, int stoch
 }
 
 }  // extern "C"
+
+#if TAM_STATS
+extern "C" {
+// The fallback counters (TAM_ST_COUNT values) into out; reset them to zero
+// when reset != 0.  Synchronous.  Measurement builds only.
+int tam_stats_read(uint64_t* out, int reset) {
+  unsigned long long h[TAM_ST_COUNT];
+  TAM_HIP_CHECK(hipDeviceSynchronize());
+  TAM_HIP_CHECK(hipMemcpyFromSymbol(h, HIP_SYMBOL(tam_stats), sizeof(h)));
+  for (int i = 0; i < TAM_ST_COUNT; ++i) out[i] = (uint64_t)h[i];
+  if (reset) {
+    memset(h, 0, sizeof(h));
+    TAM_HIP_CHECK(hipMemcpyToSymbol(HIP_SYMBOL(tam_stats), h, sizeof(h)));
+  }
+  return TAM_OK;
+}
+}  // extern "C"
+#endif
