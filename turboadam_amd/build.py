@@ -49,9 +49,29 @@ def _hipcc(sources, out: str, verbose: bool, extra=()) -> str:
 
 
 def build_library(verbose: bool = False) -> str:
-    """The optimizer library and the streaming-kernel library bench.py uses."""
+    """The optimizer library, the host module of steady steps and the
+    streaming-kernel library bench.py uses."""
     _hipcc(STREAM_SOURCES, STREAM_LIB_PATH, verbose)
+    build_host_module(verbose)
     return _hipcc(SOURCES, LIB_PATH, verbose)
+
+
+# The host side of a steady step in C++ (csrc/tam_host.cpp), a torch extension
+# module imported from _build/host by turboadam_amd.optimizer.
+HOST_BUILD_DIR = os.path.join(BUILD_DIR, "host")
+HOST_SOURCES = [os.path.join(PKG_DIR, "csrc", "tam_host.cpp")]
+HOST_MODULE_PATH = os.path.join(HOST_BUILD_DIR, "_tam_host.so")
+
+
+def build_host_module(verbose: bool = False) -> str:
+    """Compile csrc/tam_host.cpp against torch's C++ API (the CPU compiler;
+    no device code)."""
+    from torch.utils import cpp_extension
+
+    os.makedirs(HOST_BUILD_DIR, exist_ok=True)
+    cpp_extension.load(name="_tam_host", sources=HOST_SOURCES, build_directory=HOST_BUILD_DIR,
+                       extra_cflags=["-O2"], verbose=verbose)
+    return HOST_MODULE_PATH
 
 
 # A measurement build of the same sources that counts the fast paths' exact

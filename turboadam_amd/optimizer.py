@@ -13,7 +13,7 @@ loop.  Parameters must live on a HIP device; there is no CPU path.
 import ctypes
 import math
 import operator
-from itertools import chain
+import os
 
 import numpy as np
 import torch
@@ -52,6 +52,35 @@ _ROW_FIELDS = ("param", "grad", "v_idx", "v_scales", "exp_avg_sq", "exp_avg", "s
 _GROUP_FIELDS = ("c_wd", "beta1", "one_minus_beta1", "beta2", "one_minus_beta2", "bias_correction1",
                  "bias_correction2", "inv_bc2", "inv_bc2_f32", "eps", "neg_lr", "sqrt_block")
 _SQRT_BLOCK_F32 = _f32(math.sqrt(BLOCK_SIZE))
+
+
+_host_module = None
+
+
+def _host():
+    """The C++ host module of steady steps (csrc/tam_host.cpp, built by
+    turboadam_amd.build); raises when it is missing."""
+    global _host_module
+    if _host_module is None:
+        import importlib.machinery
+        import importlib.util
+
+        from .build import HOST_MODULE_PATH
+
+        if not os.path.exists(HOST_MODULE_PATH):
+            raise RuntimeError(f"turboadam_amd: host module not built ({HOST_MODULE_PATH}); "
+                               "run turboadam_amd.build.build_library()")
+        loader = importlib.machinery.ExtensionFileLoader("_tam_host", HOST_MODULE_PATH)
+        spec = importlib.util.spec_from_loader("_tam_host", loader)
+        mod = importlib.util.module_from_spec(spec)
+        loader.exec_module(mod)
+        _host_module = mod
+    return _host_module
+
+
+# byte offsets of the per-step fields a steady step rewrites in each descriptor row
+_GRAD_OFF = _DESC.fields["grad"][1]
+_STEP_OFF = _DESC.fields["step"][1]
 
 
 def _row_tensors(state, compress_v: bool) -> tuple:
@@ -217,7 +246,7 @@ class _FastStep:
         self.rows = rows          # positions (in params) of the descriptor rows
         self.states = states      # their state dicts
         self.grads = grads        # the gradient objects last checked, per row
-        self.pdtypes = pdtypes    # parameter dtypes, per row
+        self.pcodes = [_DTYPES[dt] for dt in pdtypes]  # their TAM_DTYPE_* codes
         self.bc_src = bc_src      # (bc key, group betas, state dict whose step sets the group's bias corrections)
         self.plan = plan
         self.row_params = [params[i] for i in rows]
@@ -863,32 +892,25 @@ class TurboAdam(Optimizer):
         if st is not f.state_map or len(st) != len(f.state_values) or \
                 not all(map(operator.is_, st.values(), f.state_values)):
             return False
-        try:
-            cur = list(chain.from_iterable(map(_row_tensors, f.states, f.plan.row_cv)))
-        except KeyError:  # a state entry was removed
-            return False
-        return len(cur) == len(f.tensors) and all(map(operator.is_, cur, f.tensors))
+        return _host().states_kept(f)
 
     def _fast_step(self) -> bool:
         """A steady step (_FastStep) if this one is; False (nothing done) otherwise."""
         f = self._fast
-        if f is None or f.version != self._layout_version or not self._fast_state_kept(f):
+        if f is None or f.version != self._layout_version:
             return False
-        gs = [p.grad for p in f.params]
-        if [g is None for g in gs] != f.absent:
+        st = self.state
+        if st is not f.state_map or len(st) != len(f.state_values) or \
+                not all(map(operator.is_, st.values(), f.state_values)):
             return False
-        if [p.data_ptr() for p in f.row_params] != f.ptrs:
-            return False
-        grads = [gs[i] for i in f.rows]
-        kept = f.grads
-        for j, g in enumerate(grads):
-            if g is not kept[j]:  # a new gradient object: the checks of _grad_ptr
-                if not (g.dtype is f.pdtypes[j] and g.layout is torch.strided and g.is_contiguous()
-                        and g.get_device() == f.dev_index):
-                    return False
-                kept[j] = g
         plan = f.plan
         if self._plans.get(f.device) is not plan:
+            return False
+        t = plan.table
+        # per row, in C++: the same parameters with gradients, their dtypes and
+        # storage, each new gradient's checks, the state tensors; then the
+        # rows' gradient pointers and step numbers are written into t
+        if not _host().steady_rows(f, t.ctypes.data, t.itemsize, _GRAD_OFF, _STEP_OFF):
             return False
         device = f.device
         self._bc_values = {}
@@ -897,14 +919,10 @@ class TurboAdam(Optimizer):
             next_step = src["step"] + 1
             bc = (1.0 - beta1**next_step, 1.0 - beta2**next_step)
             self._bc_values[key] = bc
-            t = self._group_step_tensors.get(key)
-            if t is not None:
-                t["bc1"].fill_(bc[0])
-                t["bc2"].fill_(bc[1])
-        t = plan.table
-        t["grad"] = [g.data_ptr() for g in grads]
-        states = f.states
-        t["step"] = np.asarray([st["step"] for st in states], dtype=np.int64) + 1
+            tb = self._group_step_tensors.get(key)
+            if tb is not None:
+                tb["bc1"].fill_(bc[0])
+                tb["bc2"].fill_(bc[1])
         flags = plan.static_flags.copy()
         if plan.cost_rows.size:
             flags[plan.cost_rows] |= np.uint32(_lib.TAM_FLAG_HAS_STATE)
@@ -917,8 +935,7 @@ class TurboAdam(Optimizer):
         with torch.cuda.device(device):
             bufs.order_on(torch.cuda.current_stream(device))
         self._submit(lib, device, plan, bufs, False)
-        for st in states:
-            st["step"] += 1
+        _host().advance_steps(f.states)
         return True
 
     def _issue(self, lib, desc_ptr: int, arr, info, ws: torch.Tensor, stream: int) -> None:
