@@ -69,6 +69,10 @@ def build_host_module(verbose: bool = False) -> str:
     from torch.utils import cpp_extension
 
     os.makedirs(HOST_BUILD_DIR, exist_ok=True)
+    for name in ("_tam_host.so", "tam_host.o"):  # compile every time, as the other libraries
+        path = os.path.join(HOST_BUILD_DIR, name)
+        if os.path.exists(path):
+            os.remove(path)
     cpp_extension.load(name="_tam_host", sources=HOST_SOURCES, build_directory=HOST_BUILD_DIR,
                        extra_cflags=["-O2"], verbose=verbose)
     return HOST_MODULE_PATH
