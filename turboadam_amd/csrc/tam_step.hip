@@ -23,8 +23,9 @@
 //           tensor (pairwise trees over the partials).
 //   pass 2  tam_k2_encode: CoState tiles: recompute m, delta = m - alpha*g,
 //           sign bits, block norms, fp16 amplitudes, block ratios.
-//   pass 3  tam_k_sel_*: radix selection of the two order statistics over
-//           slices of the ratios, labels, alpha write-back.
+//   pass 3  tam_k_sel_hist and tam_k_sel_pick (three rounds), tam_k_sel_labels:
+//           radix selection of the two order statistics over slices of the
+//           ratios, labels, alpha write-back.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -39,7 +40,6 @@
 #define TAM_EPL 8
 #define TAM_BPT 16  // blocks per tile
 #define TAM_TILE_ELEMS (TAM_BPT * TAM_BLOCK_SIZE)
-#define TAM_SEL_WG 1024
 
 // ---------------------------------------------------------------------------
 // error reporting
@@ -1616,6 +1616,29 @@ TAM_K1_FULL_KERNEL(tam_k1_main_bf16, TAM_DTYPE_BF16, TAM_K1_WAVES_BF16)
 TAM_K1_FULL_KERNEL(tam_k1_main_f16, TAM_DTYPE_F16, TAM_K1_WAVES_F16)
 TAM_K1_FULL_KERNEL(tam_k1_main_f32, TAM_DTYPE_F32, TAM_K1_WAVES_F32)
 
+// ---------------------------------------------------------------------------
+// Selection state of a CoState tensor (workspace), set afresh every step by
+// pass 0's tail kernel
+// ---------------------------------------------------------------------------
+struct TamSel {
+  uint32_t prefix[2];  // bits fixed so far of the k_lo-th and k_hi-th smallest ratio
+  uint32_t k[2];       // rank within the ratios sharing that prefix
+};
+
+// Every thread of one workgroup: tensor d's selection state before the first
+// round and its cleared histogram (4096 counts).
+__device__ __forceinline__ void tam_sel_reset_wg(const TamTensor& d, TamSel* __restrict__ sel,
+                                                 uint32_t* __restrict__ hist) {
+  for (uint32_t i = threadIdx.x; i < 4096u; i += blockDim.x) tam_g(hist)[i] = 0u;
+  if (threadIdx.x == 0) {
+    TamSel z;
+    z.prefix[0] = z.prefix[1] = 0u;
+    z.k[0] = d.k_lo;
+    z.k[1] = d.k_hi;
+    *sel = z;
+  }
+}
+
 // The quarters outside full units: the last (at most five) quarters of each
 // tensor, or every quarter of a tensor whose parameter or gradient is not
 // 16-byte aligned.  An aligned tensor has one workgroup; an unaligned one has
@@ -1632,10 +1655,14 @@ __device__ __forceinline__ int tam_tail_tensor(const TamTensor* __restrict__ T, 
 }
 
 __global__ __launch_bounds__(TAM_WG) void tam_k1_tail(const TamTensor* __restrict__ T, int nT, uint32_t seed_lo,
-                                                      uint32_t seed_hi, double2* __restrict__ partials) {
+                                                      uint32_t seed_hi, double2* __restrict__ partials,
+                                                      TamSel* __restrict__ sel, uint32_t* __restrict__ hist) {
   if (tam_step_skipped(T)) return;
   const int ti = tam_tail_tensor(T, nT, blockIdx.x);
   const TamTensor& d = T[ti];
+  // the tensor's first tail workgroup sets its selection state
+  if ((d.flags & TAM_FLAG_COSTATE) && blockIdx.x == d.tail0)
+    tam_sel_reset_wg(d, sel + ti, hist + (uint64_t)ti * 4096u);
   if (d.flags & TAM_FLAG_EF) return;  // the whole workgroup: tam_k1_ef covers the tensor
   __shared__ float lut[TAM_WG / 64][4 * 64];
   __shared__ TamLdsTabs tabs;
@@ -2061,30 +2088,20 @@ tam_k2_encode(const TamTensor* __restrict__ T, int nT, uint32_t total_tiles, con
 // ---------------------------------------------------------------------------
 // Ratios are >= +0 or NaN, so their fp32 bit patterns order like torch.sort
 // (NaN last).  The selection is an MSD radix select on those patterns, spread
-// over slices of 8192 keys so that large tensors use many workgroups:
-//   tam_k_sel_reset   per tensor: reset the selection state and histograms;
-//   tam_k_sel_minmax  per slice: min / max of the keys (atomic min / max per
-//                     tensor) -- the bits all keys share need no pass;
-//   tam_k_sel_hist    per slice, three times: LDS histogram of the next 11-bit
-//                     digit below the bits already fixed, for the keys that
-//                     match the prefix of each of the two ranks (keys of
-//                     similar magnitude spread over the bins), added into the
-//                     tensor's histogram;
+// over slices of 8192 keys so that large tensors use many workgroups; three
+// rounds fix bits 31..21, 20..10 and 9..0 of both order statistics.
+//   tam_k_sel_hist    per slice, once per round: LDS histogram of the round's
+//                     digit for the keys that match the prefix fixed so far of
+//                     each of the two ranks, added into the tensor's
+//                     histogram;
 //   tam_k_sel_pick    per tensor, after each histogram: prefix sums of the
-//                     histogram pick the digit holding each rank;
+//                     histogram pick the digit holding each rank; the
+//                     histogram is cleared for the next round;
 //   tam_k_sel_labels  per slice: labels from the two thresholds; alpha
 //                     write-back.
+// The order statistics are exact whatever the digit windows: after the last
+// round each prefix is the whole key of its rank.
 #define TAM_SLICE 8192u
-#define TAM_SEL_WG 1024
-
-// Selection state of one tensor (workspace).
-struct TamSel {
-  uint32_t kmin, kmax;  // key range (tam_k_sel_minmax)
-  uint32_t prefix[2];   // bits fixed so far of the k_lo-th and k_hi-th key
-  uint32_t k[2];        // rank within the keys sharing the prefix
-  uint32_t mask;        // bits fixed so far
-  int32_t top;          // highest bit not yet fixed (-1: done)
-};
 
 __host__ __device__ __forceinline__ uint32_t tam_sel_slices(uint32_t flags, uint32_t nb) {
   return (flags & TAM_FLAG_COSTATE) ? (nb + TAM_SLICE - 1u) / TAM_SLICE : 0u;
@@ -2116,106 +2133,56 @@ __device__ __forceinline__ void tam_slice_keys(const uint32_t* __restrict__ keys
   }
 }
 
-// Initial prefix state from the key range: bits above the highest differing
-// bit are shared by every key.
-__device__ __forceinline__ void tam_sel_start(const TamSel& s, uint32_t* prefix, uint32_t& mask, int& top) {
-  const uint32_t diff = s.kmin ^ s.kmax;
-  top = diff ? 31 - __builtin_clz(diff) : -1;
-  mask = top >= 31 ? 0u : (0xffffffffu << (top + 1));
-  prefix[0] = prefix[1] = s.kmin & mask;
+// Digit window of selection round r: bits [sh, sh + width) below the bits
+// fixed by the earlier rounds (mask).
+struct TamSelRound {
+  uint32_t sh, dmask, mask;
+};
+__host__ __device__ __forceinline__ TamSelRound tam_sel_round(int r) {
+  TamSelRound w;
+  w.sh = r == 0 ? 21u : r == 1 ? 10u : 0u;
+  w.dmask = r == 2 ? 0x3ffu : 0x7ffu;
+  w.mask = r == 0 ? 0u : r == 1 ? 0xffe00000u : 0xfffffc00u;
+  return w;
 }
 
-__global__ __launch_bounds__(TAM_WG) void tam_k_sel_reset(const TamTensor* __restrict__ T, TamSel* __restrict__ sel,
-                                                          uint32_t* __restrict__ hist) {
-  if (tam_step_skipped(T)) return;
-  const TamTensor& d = T[blockIdx.x];
-  if (!(d.flags & TAM_FLAG_COSTATE)) return;
-  uint32_t* h = hist + (uint64_t)blockIdx.x * 4096u;
-  for (uint32_t i = threadIdx.x; i < 4096u; i += TAM_WG) h[i] = 0u;
-  if (threadIdx.x == 0) {
-    TamSel z;
-    z.kmin = 0xffffffffu;
-    z.kmax = 0u;
-    z.prefix[0] = z.prefix[1] = 0u;
-    z.k[0] = d.k_lo;
-    z.k[1] = d.k_hi;
-    z.mask = 0u;
-    z.top = 32;  // not started
-    sel[blockIdx.x] = z;
-  }
-}
-
-__global__ __launch_bounds__(TAM_WG) void tam_k_sel_minmax(const TamTensor* __restrict__ T, int nT,
-                                                           const float* __restrict__ ratios, TamSel* __restrict__ sel) {
-  if (tam_step_skipped(T)) return;
-  __shared__ uint32_t red[2][TAM_WG / 64];
-  const int t = tam_slice_tensor(T, nT, blockIdx.x);
-  const TamTensor& d = T[t];
-  const uint32_t k0 = (blockIdx.x - d.slice0) * TAM_SLICE;
-  const uint32_t k1 = k0 + TAM_SLICE < d.nb ? k0 + TAM_SLICE : d.nb;
-  uint32_t kmin = 0xffffffffu, kmax = 0u;
-  tam_slice_keys((const uint32_t*)(ratios + d.ratio_off), k0, k1, [&](uint32_t k) {
-    kmin = k < kmin ? k : kmin;
-    kmax = k > kmax ? k : kmax;
-  });
+// Exclusive prefix sum over the TAM_WG threads of the workgroup.
+__device__ uint32_t tam_wg_excl_scan(uint32_t v, uint32_t* wsum) {
+  const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
+  uint32_t inc = v;
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    const uint32_t a = __shfl_xor(kmin, off), b = __shfl_xor(kmax, off);
-    kmin = a < kmin ? a : kmin;
-    kmax = b > kmax ? b : kmax;
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t t = __shfl_up(inc, off);
+    if (lane >= (uint32_t)off) inc += t;
   }
-  if ((threadIdx.x & 63u) == 0) {
-    red[0][threadIdx.x >> 6] = kmin;
-    red[1][threadIdx.x >> 6] = kmax;
-  }
+  if (lane == 63u) wsum[w] = inc;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    for (int w = 1; w < TAM_WG / 64; ++w) {
-      kmin = red[0][w] < kmin ? red[0][w] : kmin;
-      kmax = red[1][w] > kmax ? red[1][w] : kmax;
-    }
-    atomicMin(&sel[t].kmin, kmin);
-    atomicMax(&sel[t].kmax, kmax);
-  }
+  uint32_t before = 0u;
+  for (uint32_t i = 0; i < w; ++i) before += wsum[i];
+  __syncthreads();  // wsum may be reused once every wave has read it
+  return before + inc - v;
 }
 
-// Current digit window of a tensor: bits [sh, top] below the fixed prefix.
-__device__ __forceinline__ void tam_sel_window(int top, int& sh, uint32_t& dmask) {
-  sh = top >= 10 ? top - 10 : 0;
-  dmask = (1u << (top - sh + 1)) - 1u;
-}
-
+// Round r of the selection (r = 0, 1, 2, one launch each, in order).
 __global__ __launch_bounds__(TAM_WG) void tam_k_sel_hist(const TamTensor* __restrict__ T, int nT,
                                                          const float* __restrict__ ratios,
-                                                         const TamSel* __restrict__ sel, uint32_t* __restrict__ hist) {
+                                                         const TamSel* __restrict__ sel, uint32_t* __restrict__ hist,
+                                                         int r) {
   if (tam_step_skipped(T)) return;
   __shared__ uint32_t h[2][2048];
   const int t = tam_slice_tensor(T, nT, blockIdx.x);
   const TamTensor& d = T[t];
   const TamSel st = sel[t];
-  uint32_t prefix[2], mask;
-  int top;
-  if (st.top == 32) {
-    tam_sel_start(st, prefix, mask, top);
-  } else {
-    prefix[0] = st.prefix[0];
-    prefix[1] = st.prefix[1];
-    mask = st.mask;
-    top = st.top;
-  }
-  if (top < 0) return;  // uniform over the workgroup
-  int sh;
-  uint32_t dmask;
-  tam_sel_window(top, sh, dmask);
+  const TamSelRound w = tam_sel_round(r);
   for (uint32_t i = threadIdx.x; i < 4096u; i += TAM_WG) (&h[0][0])[i] = 0u;
   __syncthreads();
-  const uint32_t p0 = prefix[0], p1 = prefix[1];
+  const uint32_t p0 = st.prefix[0], p1 = st.prefix[1];
   const bool same = p0 == p1;
   const uint32_t k0 = (blockIdx.x - d.slice0) * TAM_SLICE;
   const uint32_t k1 = k0 + TAM_SLICE < d.nb ? k0 + TAM_SLICE : d.nb;
   tam_slice_keys((const uint32_t*)(ratios + d.ratio_off), k0, k1, [&](uint32_t key) {
-    const uint32_t dg = (key >> sh) & dmask;
-    const uint32_t km = key & mask;
+    const uint32_t dg = (key >> w.sh) & w.dmask;
+    const uint32_t km = key & w.mask;
     if (km == p0) atomicAdd(&h[0][dg], 1u);
     if (!same && km == p1) atomicAdd(&h[1][dg], 1u);
   });
@@ -2227,92 +2194,55 @@ __global__ __launch_bounds__(TAM_WG) void tam_k_sel_hist(const TamTensor* __rest
   }
 }
 
-// Exclusive prefix sum over the 1024 threads of the workgroup.
-__device__ uint32_t tam_wg_excl_scan(uint32_t v, uint32_t* wsum) {
-  const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
-  uint32_t inc = v;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const uint32_t t = __shfl_up(inc, off);
-    if (lane >= (uint32_t)off) inc += t;
-  }
-  if (lane == 63u) wsum[w] = inc;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t acc = 0;
-    for (int i = 0; i < TAM_SEL_WG / 64; ++i) {
-      const uint32_t t = wsum[i];
-      wsum[i] = acc;
-      acc += t;
-    }
-  }
-  __syncthreads();
-  const uint32_t r = wsum[w] + inc - v;
-  __syncthreads();
-  return r;
-}
-
-__global__ __launch_bounds__(TAM_SEL_WG) void tam_k_sel_pick(const TamTensor* __restrict__ T, TamSel* __restrict__ sel,
-                                                             uint32_t* __restrict__ hist) {
+// After round r's histogram: the digit holding each of a tensor's two ranks
+// (ranks with equal prefixes share the first half of the histogram), the new
+// state, and the histogram cleared for the next round.  One workgroup per
+// tensor.
+__global__ __launch_bounds__(TAM_WG) void tam_k_sel_pick(const TamTensor* __restrict__ T, TamSel* __restrict__ sel,
+                                                         uint32_t* __restrict__ hist, int r) {
   if (tam_step_skipped(T)) return;
-  __shared__ uint32_t wsum[TAM_SEL_WG / 64];
+  if (!(T[blockIdx.x].flags & TAM_FLAG_COSTATE)) return;
+  __shared__ uint32_t wsum[TAM_WG / 64];
   __shared__ uint32_t new_prefix[2], new_k[2];
-  const TamTensor& d = T[blockIdx.x];
-  if (!(d.flags & TAM_FLAG_COSTATE)) return;
   const TamSel st = sel[blockIdx.x];
-  uint32_t prefix[2], mask;
-  int top;
-  if (st.top == 32) {
-    tam_sel_start(st, prefix, mask, top);
-  } else {
-    prefix[0] = st.prefix[0];
-    prefix[1] = st.prefix[1];
-    mask = st.mask;
-    top = st.top;
-  }
+  const TamSelRound w = tam_sel_round(r);
+  uint32_t* gh = hist + (uint64_t)blockIdx.x * 4096u;
   const uint32_t tid = threadIdx.x;
-  if (top >= 0) {
-    int sh;
-    uint32_t dmask;
-    tam_sel_window(top, sh, dmask);
-    uint32_t* gh = hist + (uint64_t)blockIdx.x * 4096u;
-    const bool same = prefix[0] == prefix[1];
-    if (tid < 2) {
-      new_prefix[tid] = prefix[tid];
-      new_k[tid] = st.k[tid];
-    }
-    __syncthreads();
-    for (int r = 0; r < 2; ++r) {
-      const uint32_t* hr = gh + (same ? 0u : (uint32_t)r) * 2048u;
-      const uint32_t h0 = hr[2 * tid], h1 = hr[2 * tid + 1];
-      const uint32_t pre = tam_wg_excl_scan(h0 + h1, wsum);
-      const uint32_t k = st.k[r];
-      if (k >= pre && k < pre + h0 + h1) {
-        const bool first = k < pre + h0;
-        const uint32_t digit = 2 * tid + (first ? 0u : 1u);
-        new_k[r] = k - (first ? pre : pre + h0);
-        new_prefix[r] = prefix[r] | (digit << sh);
+  const bool same = st.prefix[0] == st.prefix[1];
+  if (tid < 2) {
+    new_prefix[tid] = st.prefix[tid];
+    new_k[tid] = st.k[tid];
+  }
+  __syncthreads();
+  for (int r = 0; r < 2; ++r) {
+    // bins 8 tid .. 8 tid + 7 of rank r's histogram
+    const uint32_t* hr = gh + (same ? 0u : (uint32_t)r) * 2048u + 8u * tid;
+    const TamW4 a = tam_g((const TamW4*)hr)[0], b = tam_g((const TamW4*)hr)[1];
+    const uint32_t c[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    uint32_t tot = 0u;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) tot += c[i];
+    uint32_t pre = tam_wg_excl_scan(tot, wsum);
+    const uint32_t k = st.k[r];
+    if (k >= pre && k - pre < tot) {  // one thread: its bins hold rank k
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if (k >= pre && k - pre < c[i]) {
+          new_k[r] = k - pre;
+          new_prefix[r] = st.prefix[r] | ((8u * tid + (uint32_t)i) << w.sh);
+        }
+        pre += c[i];
       }
-      __syncthreads();
     }
-    // clear the histogram for the next pass
-    for (uint32_t i = tid; i < 4096u; i += TAM_SEL_WG) gh[i] = 0u;
-    if (tid == 0) {
-      TamSel o = st;
-      o.prefix[0] = new_prefix[0];
-      o.prefix[1] = new_prefix[1];
-      o.k[0] = new_k[0];
-      o.k[1] = new_k[1];
-      o.mask = mask | (dmask << sh);
-      o.top = sh - 1;
-      sel[blockIdx.x] = o;
-    }
-  } else if (tid == 0 && st.top == 32) {
-    TamSel o = st;  // every key equal: both thresholds are that key
-    o.prefix[0] = prefix[0];
-    o.prefix[1] = prefix[1];
-    o.mask = mask;
-    o.top = -1;
+  }
+  __syncthreads();
+  for (uint32_t i = tid; i < 4096u; i += TAM_WG) tam_g(gh)[i] = 0u;  // for the next round
+  if (tid == 0) {
+    TamSel o;
+    o.prefix[0] = new_prefix[0];
+    o.prefix[1] = new_prefix[1];
+    o.k[0] = new_k[0];
+    o.k[1] = new_k[1];
     sel[blockIdx.x] = o;
   }
 }
@@ -2523,6 +2453,12 @@ __global__ void tam_k_make_desc(TamTensor* __restrict__ out, uint64_t n, uint32_
   d.k_lo = k_lo;
   d.k_hi = k_hi;
   *out = d;
+}
+
+// Fresh selection state of the one tensor of desc and its cleared histogram.
+__global__ __launch_bounds__(TAM_WG) void tam_k_sel_reset(const TamTensor* __restrict__ desc, TamSel* __restrict__ sel,
+                                                          uint32_t* __restrict__ hist) {
+  tam_sel_reset_wg(desc[0], sel, hist);
 }
 
 // delta = fl(m - fl(alpha*g)) (costate.py:42)
@@ -2987,8 +2923,7 @@ static int tam_launch_pass(int pass, const TamTensor* d_tensors, const TamStepIn
                            partials);
       TAM_HIP_CHECK(hipGetLastError());
       hipLaunchKernelGGL(tam_k1_tail, dim3(info->tail_blocks), dim3(TAM_WG), 0, s, d_tensors, info->n_tensors,
-                         (uint32_t)seed,
-                         (uint32_t)(seed >> 32), partials);
+                         (uint32_t)seed, (uint32_t)(seed >> 32), partials, sel, hist);
       break;
     case 1:
       hipLaunchKernelGGL(tam_k_alpha_chunks, dim3(info->total_chunks), dim3(TAM_WG), 0, s, d_tensors,
@@ -3002,16 +2937,11 @@ static int tam_launch_pass(int pass, const TamTensor* d_tensors, const TamStepIn
                          d_tensors, info->n_tensors, info->total_tiles, alpha_new, ratios, ws);
       break;
     default:
-      hipLaunchKernelGGL(tam_k_sel_reset, dim3(info->n_tensors), dim3(TAM_WG), 0, s, d_tensors, sel, hist);
-      TAM_HIP_CHECK(hipGetLastError());
-      hipLaunchKernelGGL(tam_k_sel_minmax, dim3(info->total_slices), dim3(TAM_WG), 0, s, d_tensors,
-                         info->n_tensors, ratios, sel);
-      TAM_HIP_CHECK(hipGetLastError());
-      for (int r = 0; r < 3; ++r) {  // 11-bit digits: at most three rounds fix all 32 bits
+      for (int r = 0; r < 3; ++r) {  // the state was set by pass 0's tail kernel
         hipLaunchKernelGGL(tam_k_sel_hist, dim3(info->total_slices), dim3(TAM_WG), 0, s, d_tensors,
-                           info->n_tensors, ratios, sel, hist);
+                           info->n_tensors, ratios, sel, hist, r);
         TAM_HIP_CHECK(hipGetLastError());
-        hipLaunchKernelGGL(tam_k_sel_pick, dim3(info->n_tensors), dim3(TAM_SEL_WG), 0, s, d_tensors, sel, hist);
+        hipLaunchKernelGGL(tam_k_sel_pick, dim3(info->n_tensors), dim3(TAM_WG), 0, s, d_tensors, sel, hist, r);
         TAM_HIP_CHECK(hipGetLastError());
       }
       hipLaunchKernelGGL(tam_k_sel_labels, dim3(info->total_slices), dim3(TAM_WG), 0, s, d_tensors,
@@ -3249,12 +3179,10 @@ int tam_thresholds(const float* ratios, uint64_t nb, uint32_t k_lo, uint32_t k_h
   TAM_HIP_CHECK(hipGetLastError());
   hipLaunchKernelGGL(tam_k_sel_reset, dim3(1), dim3(TAM_WG), 0, s, desc, sel, hist);
   TAM_HIP_CHECK(hipGetLastError());
-  hipLaunchKernelGGL(tam_k_sel_minmax, dim3(slices), dim3(TAM_WG), 0, s, desc, 1, ratios, sel);
-  TAM_HIP_CHECK(hipGetLastError());
   for (int r = 0; r < 3; ++r) {
-    hipLaunchKernelGGL(tam_k_sel_hist, dim3(slices), dim3(TAM_WG), 0, s, desc, 1, ratios, sel, hist);
+    hipLaunchKernelGGL(tam_k_sel_hist, dim3(slices), dim3(TAM_WG), 0, s, desc, 1, ratios, sel, hist, r);
     TAM_HIP_CHECK(hipGetLastError());
-    hipLaunchKernelGGL(tam_k_sel_pick, dim3(1), dim3(TAM_SEL_WG), 0, s, desc, sel, hist);
+    hipLaunchKernelGGL(tam_k_sel_pick, dim3(1), dim3(TAM_WG), 0, s, desc, sel, hist, r);
     TAM_HIP_CHECK(hipGetLastError());
   }
   hipLaunchKernelGGL(tam_k_sel_taus, dim3(1), dim3(1), 0, s, sel, taus);
