@@ -23,9 +23,9 @@
 //           tensor (pairwise trees over the partials).
 //   pass 2  tam_k2_encode: CoState tiles: recompute m, delta = m - alpha*g,
 //           sign bits, block norms, fp16 amplitudes, block ratios.
-//   pass 3  tam_k_sel_hist and tam_k_sel_pick (three rounds), tam_k_sel_labels:
-//           radix selection of the two order statistics over slices of the
-//           ratios, labels, alpha write-back.
+//   pass 3  tam_k_sel_minmax, tam_k_sel_hist and tam_k_sel_pick (three
+//           rounds), tam_k_sel_labels: radix selection of the two order
+//           statistics over slices of the ratios, labels, alpha write-back.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -1621,20 +1621,27 @@ TAM_K1_FULL_KERNEL(tam_k1_main_f32, TAM_DTYPE_F32, TAM_K1_WAVES_F32)
 // pass 0's tail kernel
 // ---------------------------------------------------------------------------
 struct TamSel {
-  uint32_t prefix[2];  // bits fixed so far of the k_lo-th and k_hi-th smallest ratio
-  uint32_t k[2];       // rank within the ratios sharing that prefix
+  uint32_t kmin, kmax;  // key range (tam_k_sel_minmax)
+  uint32_t prefix[2];   // bits fixed so far of the k_lo-th and k_hi-th smallest ratio
+  uint32_t k[2];        // rank within the ratios sharing that prefix
+  uint32_t mask;        // bits fixed so far
+  int32_t top;          // highest bit not yet fixed (-1: done; 32: no round run yet)
 };
 
-// Every thread of one workgroup: tensor d's selection state before the first
-// round and its cleared histogram (4096 counts).
+// Every thread of one workgroup: tensor d's selection state before the key
+// range is known and its cleared histogram (4096 counts).
 __device__ __forceinline__ void tam_sel_reset_wg(const TamTensor& d, TamSel* __restrict__ sel,
                                                  uint32_t* __restrict__ hist) {
   for (uint32_t i = threadIdx.x; i < 4096u; i += blockDim.x) tam_g(hist)[i] = 0u;
   if (threadIdx.x == 0) {
     TamSel z;
+    z.kmin = 0xffffffffu;
+    z.kmax = 0u;
     z.prefix[0] = z.prefix[1] = 0u;
     z.k[0] = d.k_lo;
     z.k[1] = d.k_hi;
+    z.mask = 0u;
+    z.top = 32;
     *sel = z;
   }
 }
@@ -2088,19 +2095,23 @@ tam_k2_encode(const TamTensor* __restrict__ T, int nT, uint32_t total_tiles, con
 // ---------------------------------------------------------------------------
 // Ratios are >= +0 or NaN, so their fp32 bit patterns order like torch.sort
 // (NaN last).  The selection is an MSD radix select on those patterns, spread
-// over slices of 8192 keys so that large tensors use many workgroups; three
-// rounds fix bits 31..21, 20..10 and 9..0 of both order statistics.
-//   tam_k_sel_hist    per slice, once per round: LDS histogram of the round's
-//                     digit for the keys that match the prefix fixed so far of
-//                     each of the two ranks, added into the tensor's
-//                     histogram;
+// over slices of 8192 keys so that large tensors use many workgroups (the
+// state and histogram of each tensor are set by pass 0's tail kernel):
+//   tam_k_sel_minmax  per slice: min / max of the keys (atomic min / max per
+//                     tensor) -- the bits all keys share need no round, and
+//                     the first digit starts at the highest bit that differs,
+//                     so keys of similar magnitude spread over its bins
+//                     instead of piling into a few (LDS atomics on one bin
+//                     serialise);
+//   tam_k_sel_hist    per slice, three times: LDS histogram of the next 11-bit
+//                     digit below the bits already fixed, for the keys that
+//                     match the prefix of each of the two ranks, added into
+//                     the tensor's histogram;
 //   tam_k_sel_pick    per tensor, after each histogram: prefix sums of the
 //                     histogram pick the digit holding each rank; the
 //                     histogram is cleared for the next round;
 //   tam_k_sel_labels  per slice: labels from the two thresholds; alpha
 //                     write-back.
-// The order statistics are exact whatever the digit windows: after the last
-// round each prefix is the whole key of its rank.
 #define TAM_SLICE 8192u
 
 __host__ __device__ __forceinline__ uint32_t tam_sel_slices(uint32_t flags, uint32_t nb) {
@@ -2133,17 +2144,56 @@ __device__ __forceinline__ void tam_slice_keys(const uint32_t* __restrict__ keys
   }
 }
 
-// Digit window of selection round r: bits [sh, sh + width) below the bits
-// fixed by the earlier rounds (mask).
-struct TamSelRound {
-  uint32_t sh, dmask, mask;
-};
-__host__ __device__ __forceinline__ TamSelRound tam_sel_round(int r) {
-  TamSelRound w;
-  w.sh = r == 0 ? 21u : r == 1 ? 10u : 0u;
-  w.dmask = r == 2 ? 0x3ffu : 0x7ffu;
-  w.mask = r == 0 ? 0u : r == 1 ? 0xffe00000u : 0xfffffc00u;
-  return w;
+// The state a round starts from: before the first round, the bits above the
+// highest bit where kmin and kmax differ are shared by every key.
+__device__ __forceinline__ TamSel tam_sel_begin(TamSel s) {
+  if (s.top == 32) {
+    const uint32_t diff = s.kmin ^ s.kmax;
+    s.top = diff ? 31 - __builtin_clz(diff) : -1;
+    s.mask = s.top >= 31 ? 0u : (0xffffffffu << (s.top + 1));
+    s.prefix[0] = s.prefix[1] = s.kmin & s.mask;
+  }
+  return s;
+}
+
+// Digit window below the fixed bits: bits [sh, top].
+__device__ __forceinline__ void tam_sel_window(int top, int& sh, uint32_t& dmask) {
+  sh = top >= 10 ? top - 10 : 0;
+  dmask = (1u << (top - sh + 1)) - 1u;
+}
+
+__global__ __launch_bounds__(TAM_WG) void tam_k_sel_minmax(const TamTensor* __restrict__ T, int nT,
+                                                           const float* __restrict__ ratios, TamSel* __restrict__ sel) {
+  if (tam_step_skipped(T)) return;
+  __shared__ uint32_t red[2][TAM_WG / 64];
+  const int t = tam_slice_tensor(T, nT, blockIdx.x);
+  const TamTensor& d = T[t];
+  const uint32_t k0 = (blockIdx.x - d.slice0) * TAM_SLICE;
+  const uint32_t k1 = k0 + TAM_SLICE < d.nb ? k0 + TAM_SLICE : d.nb;
+  uint32_t kmin = 0xffffffffu, kmax = 0u;
+  tam_slice_keys((const uint32_t*)(ratios + d.ratio_off), k0, k1, [&](uint32_t k) {
+    kmin = k < kmin ? k : kmin;
+    kmax = k > kmax ? k : kmax;
+  });
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const uint32_t a = __shfl_xor(kmin, off), b = __shfl_xor(kmax, off);
+    kmin = a < kmin ? a : kmin;
+    kmax = b > kmax ? b : kmax;
+  }
+  if ((threadIdx.x & 63u) == 0) {
+    red[0][threadIdx.x >> 6] = kmin;
+    red[1][threadIdx.x >> 6] = kmax;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < TAM_WG / 64; ++w) {
+      kmin = red[0][w] < kmin ? red[0][w] : kmin;
+      kmax = red[1][w] > kmax ? red[1][w] : kmax;
+    }
+    atomicMin(&sel[t].kmin, kmin);
+    atomicMax(&sel[t].kmax, kmax);
+  }
 }
 
 // Exclusive prefix sum over the TAM_WG threads of the workgroup.
@@ -2163,26 +2213,29 @@ __device__ uint32_t tam_wg_excl_scan(uint32_t v, uint32_t* wsum) {
   return before + inc - v;
 }
 
-// Round r of the selection (r = 0, 1, 2, one launch each, in order).
+// One round of the selection (three launches, in order; a tensor whose bits
+// are all fixed returns at once).
 __global__ __launch_bounds__(TAM_WG) void tam_k_sel_hist(const TamTensor* __restrict__ T, int nT,
                                                          const float* __restrict__ ratios,
-                                                         const TamSel* __restrict__ sel, uint32_t* __restrict__ hist,
-                                                         int r) {
+                                                         const TamSel* __restrict__ sel, uint32_t* __restrict__ hist) {
   if (tam_step_skipped(T)) return;
   __shared__ uint32_t h[2][2048];
   const int t = tam_slice_tensor(T, nT, blockIdx.x);
   const TamTensor& d = T[t];
-  const TamSel st = sel[t];
-  const TamSelRound w = tam_sel_round(r);
+  const TamSel st = tam_sel_begin(sel[t]);
+  if (st.top < 0) return;  // uniform over the workgroup
+  int sh;
+  uint32_t dmask;
+  tam_sel_window(st.top, sh, dmask);
   for (uint32_t i = threadIdx.x; i < 4096u; i += TAM_WG) (&h[0][0])[i] = 0u;
   __syncthreads();
-  const uint32_t p0 = st.prefix[0], p1 = st.prefix[1];
+  const uint32_t p0 = st.prefix[0], p1 = st.prefix[1], mask = st.mask;
   const bool same = p0 == p1;
   const uint32_t k0 = (blockIdx.x - d.slice0) * TAM_SLICE;
   const uint32_t k1 = k0 + TAM_SLICE < d.nb ? k0 + TAM_SLICE : d.nb;
   tam_slice_keys((const uint32_t*)(ratios + d.ratio_off), k0, k1, [&](uint32_t key) {
-    const uint32_t dg = (key >> w.sh) & w.dmask;
-    const uint32_t km = key & w.mask;
+    const uint32_t dg = (key >> sh) & dmask;
+    const uint32_t km = key & mask;
     if (km == p0) atomicAdd(&h[0][dg], 1u);
     if (!same && km == p1) atomicAdd(&h[1][dg], 1u);
   });
@@ -2194,20 +2247,26 @@ __global__ __launch_bounds__(TAM_WG) void tam_k_sel_hist(const TamTensor* __rest
   }
 }
 
-// After round r's histogram: the digit holding each of a tensor's two ranks
+// After a round's histogram: the digit holding each of a tensor's two ranks
 // (ranks with equal prefixes share the first half of the histogram), the new
 // state, and the histogram cleared for the next round.  One workgroup per
 // tensor.
 __global__ __launch_bounds__(TAM_WG) void tam_k_sel_pick(const TamTensor* __restrict__ T, TamSel* __restrict__ sel,
-                                                         uint32_t* __restrict__ hist, int r) {
+                                                         uint32_t* __restrict__ hist) {
   if (tam_step_skipped(T)) return;
   if (!(T[blockIdx.x].flags & TAM_FLAG_COSTATE)) return;
   __shared__ uint32_t wsum[TAM_WG / 64];
   __shared__ uint32_t new_prefix[2], new_k[2];
-  const TamSel st = sel[blockIdx.x];
-  const TamSelRound w = tam_sel_round(r);
-  uint32_t* gh = hist + (uint64_t)blockIdx.x * 4096u;
+  const TamSel st = tam_sel_begin(sel[blockIdx.x]);
   const uint32_t tid = threadIdx.x;
+  if (st.top < 0) {  // every bit fixed (or every key equal): the prefixes are the keys
+    if (tid == 0) sel[blockIdx.x] = st;
+    return;
+  }
+  int sh;
+  uint32_t dmask;
+  tam_sel_window(st.top, sh, dmask);
+  uint32_t* gh = hist + (uint64_t)blockIdx.x * 4096u;
   const bool same = st.prefix[0] == st.prefix[1];
   if (tid < 2) {
     new_prefix[tid] = st.prefix[tid];
@@ -2229,7 +2288,7 @@ __global__ __launch_bounds__(TAM_WG) void tam_k_sel_pick(const TamTensor* __rest
       for (int i = 0; i < 8; ++i) {
         if (k >= pre && k - pre < c[i]) {
           new_k[r] = k - pre;
-          new_prefix[r] = st.prefix[r] | ((8u * tid + (uint32_t)i) << w.sh);
+          new_prefix[r] = st.prefix[r] | ((8u * tid + (uint32_t)i) << sh);
         }
         pre += c[i];
       }
@@ -2238,11 +2297,13 @@ __global__ __launch_bounds__(TAM_WG) void tam_k_sel_pick(const TamTensor* __rest
   __syncthreads();
   for (uint32_t i = tid; i < 4096u; i += TAM_WG) tam_g(gh)[i] = 0u;  // for the next round
   if (tid == 0) {
-    TamSel o;
+    TamSel o = st;
     o.prefix[0] = new_prefix[0];
     o.prefix[1] = new_prefix[1];
     o.k[0] = new_k[0];
     o.k[1] = new_k[1];
+    o.mask = st.mask | (dmask << sh);
+    o.top = sh - 1;
     sel[blockIdx.x] = o;
   }
 }
@@ -2937,11 +2998,15 @@ static int tam_launch_pass(int pass, const TamTensor* d_tensors, const TamStepIn
                          d_tensors, info->n_tensors, info->total_tiles, alpha_new, ratios, ws);
       break;
     default:
-      for (int r = 0; r < 3; ++r) {  // the state was set by pass 0's tail kernel
+      // the state and histograms were set by pass 0's tail kernel
+      hipLaunchKernelGGL(tam_k_sel_minmax, dim3(info->total_slices), dim3(TAM_WG), 0, s, d_tensors,
+                         info->n_tensors, ratios, sel);
+      TAM_HIP_CHECK(hipGetLastError());
+      for (int r = 0; r < 3; ++r) {  // 11-bit digits: at most three rounds fix all 32 bits
         hipLaunchKernelGGL(tam_k_sel_hist, dim3(info->total_slices), dim3(TAM_WG), 0, s, d_tensors,
-                           info->n_tensors, ratios, sel, hist, r);
+                           info->n_tensors, ratios, sel, hist);
         TAM_HIP_CHECK(hipGetLastError());
-        hipLaunchKernelGGL(tam_k_sel_pick, dim3(info->n_tensors), dim3(TAM_WG), 0, s, d_tensors, sel, hist, r);
+        hipLaunchKernelGGL(tam_k_sel_pick, dim3(info->n_tensors), dim3(TAM_WG), 0, s, d_tensors, sel, hist);
         TAM_HIP_CHECK(hipGetLastError());
       }
       hipLaunchKernelGGL(tam_k_sel_labels, dim3(info->total_slices), dim3(TAM_WG), 0, s, d_tensors,
@@ -3179,10 +3244,12 @@ int tam_thresholds(const float* ratios, uint64_t nb, uint32_t k_lo, uint32_t k_h
   TAM_HIP_CHECK(hipGetLastError());
   hipLaunchKernelGGL(tam_k_sel_reset, dim3(1), dim3(TAM_WG), 0, s, desc, sel, hist);
   TAM_HIP_CHECK(hipGetLastError());
+  hipLaunchKernelGGL(tam_k_sel_minmax, dim3(slices), dim3(TAM_WG), 0, s, desc, 1, ratios, sel);
+  TAM_HIP_CHECK(hipGetLastError());
   for (int r = 0; r < 3; ++r) {
-    hipLaunchKernelGGL(tam_k_sel_hist, dim3(slices), dim3(TAM_WG), 0, s, desc, 1, ratios, sel, hist, r);
+    hipLaunchKernelGGL(tam_k_sel_hist, dim3(slices), dim3(TAM_WG), 0, s, desc, 1, ratios, sel, hist);
     TAM_HIP_CHECK(hipGetLastError());
-    hipLaunchKernelGGL(tam_k_sel_pick, dim3(1), dim3(TAM_WG), 0, s, desc, sel, hist, r);
+    hipLaunchKernelGGL(tam_k_sel_pick, dim3(1), dim3(TAM_WG), 0, s, desc, sel, hist);
     TAM_HIP_CHECK(hipGetLastError());
   }
   hipLaunchKernelGGL(tam_k_sel_taus, dim3(1), dim3(1), 0, s, sel, taus);
