@@ -1952,24 +1952,29 @@ __device__ __forceinline__ void tam_k2_any(const TamTensor& d, uint32_t wq, uint
   }
 }
 
-// Pass 2 over full units of 16-bit tensors without error feedback (the common
-// case): 16 elements per lane, 8 lanes per block, as pass 0's main kernels.
-// The unit's inputs are loaded one unit ahead of their use: the lane's 16
-// gradient elements, its block's CoState state and its two sign bytes.
+// Pass 2 over full units of tensors without error feedback (the common case):
+// 16 elements per lane, 8 lanes per block, as pass 0's main kernels.  The
+// unit's inputs are loaded one unit ahead of their use: the lane's 16 gradient
+// elements (two 16-byte words for a 16-bit tensor, four for fp32), its block's
+// CoState state and its two sign bytes.  tam_k2_encode takes the units of
+// 16-bit tensors, tam_k2_encode_f32 those of fp32 tensors (when it runs).
+template <bool F32>
 struct TamK2U {
-  TamW4 g0, g1;
+  TamW4 g[F32 ? 4 : 2];
   TamCsIn cs;  // byte: the sign bytes of elements e0..e0+7 (low) and e0+8..e0+15
 };
+template <bool F32>
 __device__ __forceinline__ bool tam_k2u_prefetchable(const TamTensor& d, uint32_t u) {
-  return d.dtype != TAM_DTYPE_F32 && !(d.flags & TAM_FLAG_EF) && tam_unit_full(d, u);
+  return (d.dtype == TAM_DTYPE_F32) == F32 && !(d.flags & TAM_FLAG_EF) && tam_unit_full(d, u);
 }
-__device__ __forceinline__ TamK2U tam_k2u_load(const TamTensor& d, uint32_t u, uint32_t lane) {
+template <bool F32>
+__device__ __forceinline__ TamK2U<F32> tam_k2u_load(const TamTensor& d, uint32_t u, uint32_t lane) {
   const uint32_t b = u * 8u + (lane >> 3);
   const uint64_t e0 = (uint64_t)b * TAM_BLOCK_SIZE + (lane & 7u) * TAM_EPU;
-  const TAM_GLOBAL TamW4* gp = tam_g((const TamW4*)((const uint16_t*)d.grad + e0));
-  TamK2U r;
-  r.g0 = gp[0];
-  r.g1 = gp[1];
+  const TAM_GLOBAL TamW4* gp = tam_g((const TamW4*)((const char*)d.grad + e0 * (F32 ? 4u : 2u)));
+  TamK2U<F32> r;
+#pragma unroll
+  for (int k = 0; k < (F32 ? 4 : 2); ++k) r.g[k] = gp[k];
   r.cs = TamCsIn{0u, 0u, 0u, 0.0f};
   if (d.flags & TAM_FLAG_HAS_STATE) {
     r.cs.label = tam_g(d.labels)[b];
@@ -1988,13 +1993,21 @@ __device__ __forceinline__ TamK2U tam_k2u_load(const TamTensor& d, uint32_t u, u
 // fp16 amplitude (lane 4) and the ratio (lane 5).
 template <uint32_t DT>
 __device__ __forceinline__ void tam_k2_unit(const TamTensor& d, uint32_t u, uint32_t lane, float a,
-                                            float* __restrict__ ratios, const TamK2U& in) {
+                                            float* __restrict__ ratios, const TamK2U<DT == TAM_DTYPE_F32>& in) {
   const uint32_t l8 = lane & 7u;
   const uint32_t b = u * 8u + (lane >> 3);
   const uint64_t e0 = (uint64_t)b * TAM_BLOCK_SIZE + l8 * TAM_EPU;
   float g[TAM_EPU], m[TAM_EPU], dl[TAM_EPU];
-  tam_unpack8<DT>(in.g0, g);
-  tam_unpack8<DT>(in.g1, g + TAM_EPL);
+  if constexpr (DT == TAM_DTYPE_F32) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const TamF4 gk = __builtin_bit_cast(TamF4, in.g[k]);
+      g[4 * k] = gk.x; g[4 * k + 1] = gk.y; g[4 * k + 2] = gk.z; g[4 * k + 3] = gk.w;
+    }
+  } else {
+    tam_unpack8<DT>(in.g[0], g);
+    tam_unpack8<DT>(in.g[1], g + TAM_EPL);
+  }
   // a scalar load (alpha is not written in this pass): no vector-memory wait
   // covers the next unit's loads
   const float alpha_prev = (d.flags & TAM_FLAG_HAS_STATE) ? *(const TAM_CONST float*)d.alpha : 0.0f;
@@ -2038,46 +2051,60 @@ __device__ __forceinline__ void tam_k2_unit(const TamTensor& d, uint32_t u, uint
 // the current one.  Descriptors and the alphas come through scalar loads
 // (their indices are wave-uniform): no vector-memory wait then covers the
 // loads in flight.  Workgroups of two waves stride over the tiles; wave w takes
-// unit 2(tile - tile0) + w.  Units of fp32 or error-feedback tensors, and units
-// that are not full, take the quarter path (tam_k2_any) for their two quarters.
+// unit 2(tile - tile0) + w.  tam_k2_encode takes the full units of 16-bit
+// tensors, tam_k2_encode_f32 those of fp32 tensors (both: without error
+// feedback).  The kernel given `quarters` also takes, quarter by quarter
+// (tam_k2_any), every other unit of a CoState tensor: error feedback, not
+// full, or of the other kernel's dtype when that kernel does not run
+// (`other_units` false).
 #ifndef TAM_K2_WAVES
 #define TAM_K2_WAVES 7
 #endif
-__global__ __launch_bounds__(TAM_K1U_WG) __attribute__((amdgpu_waves_per_eu(TAM_K2_WAVES, TAM_K2_WAVES))) void
-tam_k2_encode(const TamTensor* __restrict__ T, int nT, uint32_t total_tiles, const float* __restrict__ alpha_new,
-              float* __restrict__ ratios, char* __restrict__ ws) {
+#ifndef TAM_K2_WAVES_F32
+#define TAM_K2_WAVES_F32 6
+#endif
+template <bool F32>
+__device__ __forceinline__ void tam_k2_body(const TamTensor* __restrict__ T, int nT, uint32_t total_tiles,
+                                            const float* __restrict__ alpha_new, float* __restrict__ ratios,
+                                            char* __restrict__ ws, bool quarters, bool other_units) {
   if (tam_step_skipped(T)) return;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63u;
   const auto desc = [&](int i) -> const TamTensor& { return T[__builtin_amdgcn_readfirstlane(i)]; };
-  // the next tile at or after `tile` of a CoState tensor (uniform)
+  const auto unit_of = [&](uint32_t tile, int ti) { return (tile - desc(ti).tile0) * 2u + wave; };
+  // the next tile at or after `tile` with work for this wave (uniform)
   const auto next = [&](uint32_t& tile, int& ti) -> bool {
     for (; tile < total_tiles; tile += gridDim.x) {
       ti = tam_advance_tensor(T, nT, ti, tile);
-      if (desc(ti).flags & TAM_FLAG_COSTATE) return true;
+      const TamTensor& dd = desc(ti);
+      if ((dd.flags & TAM_FLAG_COSTATE) && (quarters || tam_k2u_prefetchable<F32>(dd, unit_of(tile, ti))))
+        return true;
     }
     return false;
   };
   uint32_t tile = tam_tile_slot(blockIdx.x, gridDim.x);
   int ti = tam_find_tensor(T, nT, tile < total_tiles ? tile : total_tiles - 1u);
   bool have = next(tile, ti);
-  TamK2U pre = {};
-  bool pre_ok = have && tam_k2u_prefetchable(desc(ti), (tile - desc(ti).tile0) * 2u + wave);
-  if (pre_ok) pre = tam_k2u_load(desc(ti), (tile - desc(ti).tile0) * 2u + wave, lane);
+  TamK2U<F32> pre = {};
+  bool pre_ok = have && tam_k2u_prefetchable<F32>(desc(ti), unit_of(tile, ti));
+  if (pre_ok) pre = tam_k2u_load<F32>(desc(ti), unit_of(tile, ti), lane);
   while (have) {
     uint32_t ntile = tile + gridDim.x;
     int nti = ti;
     const bool nhave = next(ntile, nti);
     const TamTensor& d = desc(ti);
-    const uint32_t u = (tile - d.tile0) * 2u + wave;
+    const uint32_t u = unit_of(tile, ti);
     const float a = *(const TAM_CONST float*)(alpha_new + __builtin_amdgcn_readfirstlane(ti));
-    TamK2U npre = {};
-    const bool npre_ok = nhave && tam_k2u_prefetchable(desc(nti), (ntile - desc(nti).tile0) * 2u + wave);
-    if (npre_ok) npre = tam_k2u_load(desc(nti), (ntile - desc(nti).tile0) * 2u + wave, lane);
-    if (pre_ok && d.dtype == TAM_DTYPE_BF16) {
-      tam_k2_unit<TAM_DTYPE_BF16>(d, u, lane, a, ratios, pre);
-    } else if (pre_ok) {
-      tam_k2_unit<TAM_DTYPE_F16>(d, u, lane, a, ratios, pre);
+    TamK2U<F32> npre = {};
+    const bool npre_ok = nhave && tam_k2u_prefetchable<F32>(desc(nti), unit_of(ntile, nti));
+    if (npre_ok) npre = tam_k2u_load<F32>(desc(nti), unit_of(ntile, nti), lane);
+    bool done = pre_ok;
+    if constexpr (F32) {
+      if (pre_ok) tam_k2_unit<TAM_DTYPE_F32>(d, u, lane, a, ratios, pre);
     } else {
+      if (pre_ok && d.dtype == TAM_DTYPE_BF16) tam_k2_unit<TAM_DTYPE_BF16>(d, u, lane, a, ratios, pre);
+      else if (pre_ok) tam_k2_unit<TAM_DTYPE_F16>(d, u, lane, a, ratios, pre);
+    }
+    if (!done && quarters && !(other_units && tam_k2u_prefetchable<!F32>(d, u))) {
       tam_k2_any(d, 2u * u, lane, a, ratios, ws);
       tam_k2_any(d, 2u * u + 1u, lane, a, ratios, ws);
     }
@@ -2087,6 +2114,18 @@ tam_k2_encode(const TamTensor* __restrict__ T, int nT, uint32_t total_tiles, con
     pre = npre;
     pre_ok = npre_ok;
   }
+}
+
+__global__ __launch_bounds__(TAM_K1U_WG) __attribute__((amdgpu_waves_per_eu(TAM_K2_WAVES, TAM_K2_WAVES))) void
+tam_k2_encode(const TamTensor* __restrict__ T, int nT, uint32_t total_tiles, const float* __restrict__ alpha_new,
+              float* __restrict__ ratios, char* __restrict__ ws, int quarters, int other_units) {
+  tam_k2_body<false>(T, nT, total_tiles, alpha_new, ratios, ws, quarters != 0, other_units != 0);
+}
+
+__global__ __launch_bounds__(TAM_K1U_WG) __attribute__((amdgpu_waves_per_eu(TAM_K2_WAVES_F32, TAM_K2_WAVES_F32))) void
+tam_k2_encode_f32(const TamTensor* __restrict__ T, int nT, uint32_t total_tiles, const float* __restrict__ alpha_new,
+                  float* __restrict__ ratios, char* __restrict__ ws, int quarters, int other_units) {
+  tam_k2_body<true>(T, nT, total_tiles, alpha_new, ratios, ws, quarters != 0, other_units != 0);
 }
 
 // ---------------------------------------------------------------------------
@@ -2787,7 +2826,8 @@ static bool tam_wd_keeps_16bit(uint32_t dtype, float c_wd) {
 // is 14% faster with 32 rounds than with one resident round of persistent
 // workgroups (8 rounds: 1% slower than 32); pass 2, which loads each quarter
 // one ahead, is fastest with 8 rounds (7% faster than 32, 15% than 1).
-enum { TAM_KS_K1_BF16, TAM_KS_K1_F16, TAM_KS_K1_F32, TAM_KS_K2, TAM_KS_K1_EF, TAM_KS_K4_EF, TAM_KS_COUNT };
+enum { TAM_KS_K1_BF16, TAM_KS_K1_F16, TAM_KS_K1_F32, TAM_KS_K2, TAM_KS_K2_F32, TAM_KS_K1_EF, TAM_KS_K4_EF,
+       TAM_KS_COUNT };
 #ifndef TAM_K2_GRID_ROUNDS
 #define TAM_K2_GRID_ROUNDS 8
 #endif
@@ -2952,7 +2992,7 @@ static int tam_launch_pass(int pass, const TamTensor* d_tensors, const TamStepIn
   float* alpha_old = (float*)(ws + info->off_ef_alpha);
   // vwg: virtual workgroups (each striding over the tiles on its own) per workgroup
   auto grid_of = [&](int which, const void* kernel, int block = TAM_WG, uint32_t vwg = 1u) {
-    const uint32_t rounds = which == TAM_KS_K2 ? TAM_K2_GRID_ROUNDS : TAM_GRID_ROUNDS;
+    const uint32_t rounds = (which == TAM_KS_K2 || which == TAM_KS_K2_F32) ? TAM_K2_GRID_ROUNDS : TAM_GRID_ROUNDS;
     const uint32_t g = tam_resident_grid(which, kernel, block) * rounds;
     const uint32_t need = (info->total_tiles + vwg - 1u) / vwg;
     return need < g ? need : g;
@@ -2992,11 +3032,24 @@ static int tam_launch_pass(int pass, const TamTensor* d_tensors, const TamStepIn
       TAM_HIP_CHECK(hipGetLastError());
       hipLaunchKernelGGL(tam_k_alpha, dim3(info->n_tensors), dim3(TAM_WG), 0, s, d_tensors, chunk_sums, alpha_new);
       break;
-    case 2:
-      hipLaunchKernelGGL(tam_k2_encode, dim3(grid_of(TAM_KS_K2, (const void*)tam_k2_encode, TAM_K1U_WG)),
-                         dim3(TAM_K1U_WG), 0, s,
-                         d_tensors, info->n_tensors, info->total_tiles, alpha_new, ratios, ws);
+    case 2: {
+      // full units by dtype class; the other units' quarters go to the 16-bit
+      // kernel when it runs, else to the fp32 one
+      const bool has16 = (info->dtype_mask & ((1u << TAM_DTYPE_BF16) | (1u << TAM_DTYPE_F16))) != 0;
+      const bool has32 = (info->dtype_mask & (1u << TAM_DTYPE_F32)) != 0;
+      if (has16 || !has32)
+        hipLaunchKernelGGL(tam_k2_encode, dim3(grid_of(TAM_KS_K2, (const void*)tam_k2_encode, TAM_K1U_WG)),
+                           dim3(TAM_K1U_WG), 0, s, d_tensors, info->n_tensors, info->total_tiles, alpha_new, ratios,
+                           ws, 1, has32 ? 1 : 0);
+      if (has32) {
+        TAM_HIP_CHECK(hipGetLastError());
+        hipLaunchKernelGGL(tam_k2_encode_f32,
+                           dim3(grid_of(TAM_KS_K2_F32, (const void*)tam_k2_encode_f32, TAM_K1U_WG)),
+                           dim3(TAM_K1U_WG), 0, s, d_tensors, info->n_tensors, info->total_tiles, alpha_new, ratios,
+                           ws, has16 ? 0 : 1, 0);
+      }
       break;
+    }
     default:
       // the state and histograms were set by pass 0's tail kernel
       hipLaunchKernelGGL(tam_k_sel_minmax, dim3(info->total_slices), dim3(TAM_WG), 0, s, d_tensors,
