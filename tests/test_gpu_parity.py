@@ -182,6 +182,17 @@ def test_m_and_v_fp16():
     _check(run_side_by_side(sizes, [F16] * len(sizes), steps=6, lr=1e-3))
 
 
+def test_m_and_v_mixed_dtypes_split_pass_2():
+    # 16-bit and fp32 CoState tensors in one step: pass 2's 16-bit kernel takes
+    # the 16-bit units and every tail quarter, its fp32 kernel the full fp32
+    # units; then the same with unaligned views (every unit to the quarter path)
+    log("m+v mixed bf16 / fp32 / fp16 with tails, aligned and unaligned, 4 steps")
+    sizes = [8192 * 9 + 300, 4096 * 5 + 17, 8192 * 3, 5000, 1024 * 7 + 129]
+    dts = [F32, BF16, F32, F16, F32]
+    _check(run_side_by_side(sizes, dts, steps=4, lr=1e-3, weight_decay=0.01))
+    _check(run_side_by_side(sizes, dts, steps=3, offset=1, lr=1e-3, weight_decay=0.01))
+
+
 @pytest.mark.parametrize("bits", [2, 3, 6, 8])
 def test_v_bits(bits):
     log(f"m+v fp32 v_bits={bits}")
