@@ -635,7 +635,8 @@ def main():
             "step_hbm_frac": step_gbps / HBM_PEAK_GBPS,
         },
         "roofline": {
-            "kernel": "pass 0 (tam_k1_main_<dtype> + tam_k1_tail)",
+            "kernel": ("pass 0 (tam_k1_ef + tam_k1_tail)" if kw.get("error_feedback")
+                       else "pass 0 (tam_k1_main_<dtype> + tam_k1_tail)"),
             "bound": "hbm",
             "achieved": k1_gbps,
             "peak": HBM_PEAK_GBPS,
