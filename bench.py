@@ -205,7 +205,7 @@ def _time_mirror(TM, shapes, dtype, kw, log_sigma, threads, min_steps, budget_s,
 
 
 def cpu_baseline(shapes, dtype, kw, log_sigma, budget_s=20.0):
-    """The reference's CPU step timed on this host (BASELINE's CPU plan).
+    """The reference's CPU step timed on this host, as the reported baseline.
 
     Runs oracle/torch_mirror.py in faithful mode -- the reference CPU path
     restated op for op in torch (it reproduces the reference's outputs bit for
