@@ -91,6 +91,55 @@ def test_thresholds_and_classify(nb, null_pct, amp_pct):
     assert _same(_np(C.classify_blocks(_t(r), float(t0o[0]), float(t1o[0]))), lab_o)
 
 
+def _edge_ratios(case):
+    """Ratio arrays that drive the radix selection through its edge cases."""
+    rng = np.random.default_rng(7)
+    if case == "all_equal":          # kmin == kmax: no round runs
+        return np.full(20_000, 0.37, np.float32)
+    if case == "all_zero":
+        return np.zeros(8192, np.float32)
+    if case == "low_bits":           # keys differ only in their last bits: every round narrows
+        return (np.float32(1.0).view(np.uint32) + rng.integers(0, 7, 30_000, dtype=np.uint32)).view(np.float32)
+    if case == "two_values":         # one jump between the two ranks
+        r = np.full(16_384, 0.5, np.float32)
+        r[8000:] = 0.75
+        return r
+    if case == "nan_and_zero":       # NaN orders last, +0 first
+        r = np.abs(rng.standard_normal(8193)).astype(np.float32)
+        r[rng.integers(0, 8193, 400)] = np.nan
+        r[rng.integers(0, 8193, 400)] = 0.0
+        return r
+    if case == "nan_at_rank":        # the upper rank lands among the NaNs
+        r = np.abs(rng.standard_normal(12_000)).astype(np.float32)
+        r[:2400] = np.nan
+        return r
+    if case == "slice_edge":         # exactly one full slice (8193 keys: nan_and_zero)
+        return np.abs(rng.standard_normal(8192)).astype(np.float32)
+    raise ValueError(case)
+
+
+@pytest.mark.parametrize("case", ["all_equal", "all_zero", "low_bits", "two_values", "nan_and_zero", "nan_at_rank",
+                                  "slice_edge"])
+def test_thresholds_edge_cases(case):
+    from turboadam_amd import costate as C
+
+    log(f"thresholds edge case {case}")
+    r = _edge_ratios(case)
+    nb = r.size
+    for null_pct, amp_pct in ((0.1, 0.9), (0.05, 0.95)):
+        t0o, t1o = np.zeros(1, np.float32), np.zeros(1, np.float32)
+        k_lo, k_hi = O.ranks(nb, null_pct, amp_pct)
+        O.lib().or_thresholds(O.ptr(r), nb, k_lo, k_hi, O.ptr(t0o), O.ptr(t1o))
+        t0, t1 = C.compute_thresholds(_t(r), null_pct, amp_pct)
+        # the oracle's order statistics are plain sorts of the bit patterns
+        keys = np.sort(r.view(np.uint32))
+        assert t0o.view(np.uint32)[0] == keys[k_lo] and t1o.view(np.uint32)[0] == keys[k_hi]
+        assert _same(np.float32(t0.item()), t0o[0]) and _same(np.float32(t1.item()), t1o[0])
+        lab_o = np.empty(nb, np.uint8)
+        O.lib().or_classify(O.ptr(r), nb, float(t0o[0]), float(t1o[0]), O.ptr(lab_o))
+        assert _same(_np(C.classify_blocks(_t(r), t0, t1)), lab_o)
+
+
 @pytest.mark.parametrize("n", [300, 5000, 70_001])
 def test_decode_blocks(n):
     from turboadam_amd import costate as C
